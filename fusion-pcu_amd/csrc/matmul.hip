@@ -1,0 +1,470 @@
+// Strict F32/F64 MatMul for gfx950.
+//
+// Contract (core/dialect/tensor/reference/strict_matmul/strict_matmul.rs:22-73): each
+// output cell starts from +0 and walks k in increasing order, rounding the product and
+// then the sum on their own (no FMA, no MFMA, no reassociation). The first fault is the
+// lowest (row-major cell, k, Multiply before Add).
+//
+// Three launches:
+//  1. prefilter   per-row minimum exponent of op(A) and per-column minimum exponent of
+//                 op(B) over finite nonzero entries (bandwidth-bound, ~2 reads of A and B).
+//  2. main        LDS-staged 128x128 output tile per 256-thread workgroup, 8x8 register
+//                 block per thread, k in order with separate v_mul/v_add. The epilogue
+//                 marks a cell suspect when its result is non-finite (the only trace an
+//                 invalid operand or an overflow leaves) or when the two exponents allow a
+//                 product small enough to be tiny (the only way an underflow can arise),
+//                 and keeps the first suspect cell with one atomicMin per wave.
+//  3. replay      exact ordered re-execution of suspect cells in row-major order from the
+//                 first suspect, with per-op classification; stops once the earliest fault
+//                 found lies before the cells still to visit. Returns at once when no cell
+//                 is suspect, which is the fault-free path.
+#include "pcu_device.hpp"
+#include "pcu_kernels.hpp"
+
+#include <limits.h>
+
+#pragma clang fp contract(off)
+
+namespace pcu {
+
+constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
+
+__device__ __forceinline__ int ilog2_abs(float v)
+{
+    uint32_t b = bits_of(v);
+    uint32_t e = (b >> 23) & 0xff, f = b & 0x7fffff;
+    if (e == 0xff || (e == 0 && f == 0))
+        return kExpNone;
+    if (e == 0)
+        return (31 - __clz(f)) - 149;
+    return (int)e - 127;
+}
+__device__ __forceinline__ int ilog2_abs(double v)
+{
+    uint64_t b = bits_of(v);
+    uint64_t e = (b >> 52) & 0x7ff, f = b & 0x000fffffffffffffull;
+    if (e == 0x7ff || (e == 0 && f == 0))
+        return kExpNone;
+    if (e == 0)
+        return (63 - __clzll(f)) - 1074;
+    return (int)e - 1023;
+}
+
+__device__ __forceinline__ int wave_min_i32(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        int o = __shfl_xor(v, off, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+// out[r] = min over c of ilog2|X[r, c]| for a row-major R x C matrix; one wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, uint64_t R,
+                                                      uint64_t C, int *__restrict__ out)
+{
+    uint64_t r = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    if (r >= R)
+        return; // whole wave exits together
+    int lane = threadIdx.x % 64;
+    int m = kExpNone;
+    const T *row = X + r * C;
+    for (uint64_t c = lane; c < C; c += 64) {
+        int e = ilog2_abs(row[c]);
+        m = e < m ? e : m;
+    }
+    m = wave_min_i32(m);
+    if (lane == 0)
+        out[r] = m;
+}
+
+// out[c] = min over r of ilog2|X[r, c]|; a block covers 256 columns x 64 rows and folds
+// its partial minimum in with atomicMin (out pre-filled with kExpNone).
+template <typename T>
+__global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, uint64_t R,
+                                                      uint64_t C, int *__restrict__ out)
+{
+    uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= C)
+        return;
+    uint64_t r0 = (uint64_t)blockIdx.y * 64;
+    uint64_t r1 = r0 + 64 < R ? r0 + 64 : R;
+    int m = kExpNone;
+    for (uint64_t r = r0; r < r1; r++) {
+        int e = ilog2_abs(X[r * C + c]);
+        m = e < m ? e : m;
+    }
+    atomicMin(&out[c], m);
+}
+
+__global__ void k_fill_i32(int *p, uint64_t n, int v)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void k_fill_u64(unsigned long long *p, uint64_t n, unsigned long long v)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// ------------------------------------------------------------------- main tile
+
+constexpr int BM = 128, BN = 128, BK = 8, PAD = 4;
+
+// Four consecutive elements of a row-major operand starting at p[0]; `valid` of them are
+// in bounds (the rest read as +0, which leaves every accumulator unchanged: +0 * +0 = +0
+// and acc + (+0) == acc since an accumulator started at +0 is never -0).
+template <typename T, bool VEC>
+__device__ __forceinline__ void load4(const T *__restrict__ p, int valid, T (&v)[4])
+{
+    if (VEC && valid >= 4) {
+        if (sizeof(T) == 4) {
+            float4 q = *reinterpret_cast<const float4 *>(p);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        } else {
+            double2 q0 = *reinterpret_cast<const double2 *>(p);
+            double2 q1 = *reinterpret_cast<const double2 *>(p + 2);
+            v[0] = q0.x; v[1] = q0.y; v[2] = q1.x; v[3] = q1.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = i < valid ? p[i] : (T)0;
+    }
+}
+
+template <typename T, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(256) void k_strict_gemm(
+    const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
+    const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
+    int vec_c, unsigned long long *suspect)
+{
+    __shared__ __align__(16) T As[2][BK][BM + PAD];
+    __shared__ __align__(16) T Bs[2][BK][BN + PAD];
+
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+
+    // Grouped tile order: 8 tile-rows share their B panels while they are L2-resident.
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int group = 8;
+    int bid = blockIdx.x;
+    int per_group = group * tiles_n;
+    int gid = bid / per_group;
+    int first_m = gid * group;
+    int gsize = tiles_m - first_m < group ? tiles_m - first_m : group;
+    int tile_m = first_m + (bid % per_group) % gsize;
+    int tile_n = (bid % per_group) / gsize;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+    T acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[i][j] = (T)0;
+
+    T ra[4], rb[4];
+
+    // Global -> registers for the tile starting at k0.
+    auto fetch = [&](int k0) {
+        if (!TA) { // A is M x K: row m0 + tid/2, columns k0 + (tid&1)*4 .. +3
+            int m = m0 + tid / 2, k = k0 + (tid & 1) * 4;
+            int valid = (m < M) ? (K - k < 4 ? (K - k > 0 ? K - k : 0) : 4) : 0;
+            load4<T, VA>(A + (size_t)m * K + k, valid, ra);
+        } else {   // A is K x M: row k0 + tid/32, columns m0 + (tid%32)*4 .. +3
+            int k = k0 + tid / 32, m = m0 + (tid % 32) * 4;
+            int valid = (k < K) ? (M - m < 4 ? (M - m > 0 ? M - m : 0) : 4) : 0;
+            load4<T, VA>(A + (size_t)k * M + m, valid, ra);
+        }
+        if (!TB) { // B is K x N: row k0 + tid/32, columns n0 + (tid%32)*4 .. +3
+            int k = k0 + tid / 32, n = n0 + (tid % 32) * 4;
+            int valid = (k < K) ? (N - n < 4 ? (N - n > 0 ? N - n : 0) : 4) : 0;
+            load4<T, VB>(B + (size_t)k * N + n, valid, rb);
+        } else {   // B is N x K: row n0 + tid/2, columns k0 + (tid&1)*4 .. +3
+            int n = n0 + tid / 2, k = k0 + (tid & 1) * 4;
+            int valid = (n < N) ? (K - k < 4 ? (K - k > 0 ? K - k : 0) : 4) : 0;
+            load4<T, VB>(B + (size_t)n * K + k, valid, rb);
+        }
+    };
+    // Registers -> LDS buffer `buf` in k-major layout.
+    auto stash = [&](int buf) {
+        if (!TA) {
+            int m = tid / 2, k = (tid & 1) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                As[buf][k + i][m] = ra[i];
+        } else {
+            int k = tid / 32, m = (tid % 32) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                As[buf][k][m + i] = ra[i];
+        }
+        if (!TB) {
+            int k = tid / 32, n = (tid % 32) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                Bs[buf][k][n + i] = rb[i];
+        } else {
+            int n = tid / 2, k = (tid & 1) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                Bs[buf][k + i][n] = rb[i];
+        }
+    };
+
+    const int ktiles = (K + BK - 1) / BK;
+    if (ktiles > 0) {
+        fetch(0);
+        stash(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles)
+            fetch((kt + 1) * BK);
+#pragma unroll
+        for (int k = 0; k < BK; k++) {
+            T a[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[i] = As[cur][k][ty * 4 + i];
+                a[4 + i] = As[cur][k][64 + ty * 4 + i];
+                b[i] = Bs[cur][k][tx * 4 + i];
+                b[4 + i] = Bs[cur][k][64 + tx * 4 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    T p = a[i] * b[j];
+                    acc[i][j] = acc[i][j] + p;
+                }
+        }
+        if (kt + 1 < ktiles)
+            stash(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: publish the tile and find the first suspect cell of this lane.
+    uint64_t key = kNoFault;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int r = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+        if (r >= M)
+            continue;
+        int rexp = check_risk ? row_exp[r] : 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int c0 = n0 + h * 64 + tx * 4;
+            T *dst = C + (size_t)r * N + c0;
+            if (vec_c && c0 + 4 <= N) {
+                if (sizeof(T) == 4) {
+                    *reinterpret_cast<float4 *>(dst) =
+                        make_float4(acc[i][h * 4], acc[i][h * 4 + 1], acc[i][h * 4 + 2], acc[i][h * 4 + 3]);
+                } else {
+                    reinterpret_cast<double2 *>(dst)[0] = make_double2(acc[i][h * 4], acc[i][h * 4 + 1]);
+                    reinterpret_cast<double2 *>(dst)[1] = make_double2(acc[i][h * 4 + 2], acc[i][h * 4 + 3]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (c0 + j < N)
+                        dst[j] = acc[i][h * 4 + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int c = c0 + j;
+                if (c >= N)
+                    continue;
+                bool bad = !finite_bits(acc[i][h * 4 + j]);
+                if (check_risk)
+                    bad |= rexp + col_exp[c] < thr;
+                if (bad) {
+                    uint64_t cell = (uint64_t)r * N + c;
+                    key = cell < key ? cell : key;
+                }
+            }
+        }
+    }
+    wave_record_fault(key, suspect);
+}
+
+// --------------------------------------------------------------- exact replay
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_strict_gemm_replay(
+    const T *__restrict__ A, const T *__restrict__ B, const T *__restrict__ C, uint64_t M,
+    uint64_t N, uint64_t K, int ta, int tb, const int *__restrict__ row_exp,
+    const int *__restrict__ col_exp, int thr, int check_risk, int policy,
+    const unsigned long long *suspect, unsigned long long *fault,
+    const unsigned long long *prior, unsigned n_prior)
+{
+    const uint64_t first = *suspect;
+    if (first == kNoFault)
+        return;
+    for (unsigned i = 0; i < n_prior; i++)
+        if (prior[i] != kNoFault)
+            return; // an earlier op faulted: that fault is the one reported
+    const uint64_t cells = M * N;
+    const uint64_t threads = (uint64_t)gridDim.x * blockDim.x;
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint64_t base = first; base < cells; base += threads) {
+        uint64_t best = __atomic_load_n(fault, __ATOMIC_RELAXED);
+        if (best != kNoFault && K > 0 && ((best >> 3) / 2) / K < base)
+            break;
+        uint64_t cell = base + tid;
+        if (cell >= cells)
+            break;
+        uint64_t r = cell / N, c = cell % N;
+        bool bad = !finite_bits(C[cell]);
+        if (check_risk)
+            bad |= row_exp[r] + col_exp[c] < thr;
+        if (!bad)
+            continue;
+        T total = (T)0;
+        for (uint64_t k = 0; k < K; k++) {
+            T a = ta ? A[k * M + r] : A[r * K + k];
+            T b = tb ? B[c * K + k] : B[k * N + c];
+            T p = a * b;
+            uint32_t kind = classify_mul(a, b, p, policy);
+            if (kind != kOk) {
+                atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2, kind));
+                break;
+            }
+            T nxt = total + p;
+            kind = classify_add(total, p, nxt, policy);
+            if (kind != kOk) {
+                atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2 + 1, kind));
+                break;
+            }
+            total = nxt;
+        }
+    }
+}
+
+// ================================================================= launchers
+
+size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols)
+{
+    size_t r = ((rows * sizeof(int)) + 255) & ~(size_t)255;
+    size_t c = ((cols * sizeof(int)) + 255) & ~(size_t)255;
+    return r + c + 256;
+}
+
+MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols)
+{
+    char *p = (char *)base;
+    size_t r = ((rows * sizeof(int)) + 255) & ~(size_t)255;
+    size_t c = ((cols * sizeof(int)) + 255) & ~(size_t)255;
+    MatmulScratch s;
+    s.row_exp = (int *)p;
+    s.col_exp = (int *)(p + r);
+    s.suspect = (unsigned long long *)(p + r + c);
+    return s;
+}
+
+hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value)
+{
+    if (n == 0)
+        return hipSuccess;
+    unsigned grid = (unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+    hipLaunchKernelGGL(k_fill_u64, dim3(grid), dim3(256), 0, s, p, n, (unsigned long long)value);
+    return hipGetLastError();
+}
+
+static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Minimum exponent of each row of a stored R x C matrix (rows) or of each column (cols).
+template <typename T>
+static void exp_min(hipStream_t s, const T *X, uint64_t R, uint64_t C, bool along_rows, int *out)
+{
+    if (along_rows) {
+        hipLaunchKernelGGL(k_exp_min_rows<T>, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, X, R, C, out);
+    } else {
+        unsigned fg = (unsigned)((C + 255) / 256 < 1024 ? (C + 255) / 256 : 1024);
+        hipLaunchKernelGGL(k_fill_i32, dim3(fg ? fg : 1), dim3(256), 0, s, out, C, kExpNone);
+        hipLaunchKernelGGL(k_exp_min_cols<T>, dim3((unsigned)((C + 255) / 256), (unsigned)((R + 63) / 64)),
+                           dim3(256), 0, s, X, R, C, out);
+    }
+}
+
+template <typename T, bool TA, bool TB>
+static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C, int M, int N,
+                          int K, const int *re, const int *ce, int thr, int risk,
+                          unsigned long long *suspect)
+{
+    bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    int vc = (N % 4 == 0) && aligned16(C);
+    if (va && vb)
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+    else if (va)
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+    else if (vb)
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+    else
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+}
+
+template <typename T>
+static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
+                                  bool tb, const T *A, const T *B, T *C, int policy,
+                                  MatmulScratch sc, unsigned long long *fault,
+                                  const unsigned long long *prior, unsigned n_prior)
+{
+    if (M == 0 || N == 0)
+        return hipSuccess;
+    // Smallest exponent sum of a product that needs no replay (see pcu_device.hpp):
+    // IEEE: a product >= 2^-126 (2^-1022) is never tiny; RejectSubnormal: products
+    // >= 2^-103 (2^-970) are multiples of the smallest normal, so no partial sum is
+    // subnormal; AllowGradual: underflow is never a fault.
+    const bool f32 = sizeof(T) == 4;
+    int risk = policy != kPolicyAllowGradual;
+    int thr = policy == kPolicyRejectSubnormal ? (f32 ? -103 : -970) : (f32 ? -126 : -1022);
+    if (risk && K > 0) {
+        exp_min<T>(s, A, ta ? K : M, ta ? M : K, !ta, sc.row_exp);
+        exp_min<T>(s, B, tb ? N : K, tb ? K : N, tb, sc.col_exp);
+    } else if (risk) {
+        risk = 0; // an empty reduction has no arithmetic events
+    }
+    hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);
+    dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)));
+    const int m = (int)M, n = (int)N, k = (int)K;
+    if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    else gemm_dispatch<T, true, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(1024), dim3(256), 0, s, A, B, (const T *)C, M, N, K,
+                       (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, risk, policy,
+                       (const unsigned long long *)sc.suspect, fault, prior, n_prior);
+    return hipGetLastError();
+}
+
+hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
+                                uint64_t cols, bool transpose_left, bool transpose_right,
+                                const void *a, const void *b, void *c, int policy,
+                                MatmulScratch scratch, unsigned long long *fault,
+                                const unsigned long long *prior, unsigned n_prior)
+{
+    if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
+        return hipErrorInvalidValue;
+    if (dtype == 0)
+        return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
+                                      (const float *)a, (const float *)b, (float *)c, policy,
+                                      scratch, fault, prior, n_prior);
+    return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
+                                   (const double *)a, (const double *)b, (double *)c, policy,
+                                   scratch, fault, prior, n_prior);
+}
+
+} // namespace pcu

@@ -1,0 +1,381 @@
+// Device-side fault classification for the strict owned-tensor kernels (gfx950).
+//
+// Every kernel computes values with the hardware's IEEE-754 binary32/binary64 unit
+// (round-to-nearest-even, denormals preserved, no contraction: the library is compiled
+// with -ffp-contract=off and -fno-gpu-flush-denormals-to-zero). IEEE RNE gives the
+// reference's value for every non-faulting operation (the reference's integer law is
+// RNE with gradual underflow: core/scalar_checked_float.rs:361-448). What hardware
+// results cannot show directly is the fault classification, which the functions below
+// recover exactly:
+//   invalid   : a non-finite operand (core/scalar_checked_float.rs:321-322)
+//   overflow  : finite operands, infinite rounded result (:416-426)
+//   underflow : policy applied to (tiny after rounding at unbounded exponent, inexact
+//               after bounded packing, result subnormal) (:390-447,
+//               core/scalar_float_underflow.rs:61-73)
+// The cheap screens (`*_suspect`) are taken on every lane; the exact routines run only on
+// lanes the screen flags.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace pcu {
+
+enum : uint32_t {
+    kOk = 0,
+    kDivideByZero = 1,
+    kOverflow = 3,
+    kUnderflow = 4,
+    kInvalid = 5,
+};
+
+enum : int { kPolicyIeee = 0, kPolicyRejectSubnormal = 1, kPolicyAllowGradual = 2 };
+
+constexpr uint64_t kNoFault = ~0ull;
+
+// Packed fault word: (ordinal << 3) | kind; atomicMin keeps the earliest ordinal
+// (backends/rocm/owned_dispatch.rs:20,76-110 uses the same packing).
+__device__ __forceinline__ uint64_t pack_fault(uint64_t ordinal, uint32_t kind)
+{
+    return (ordinal << 3) | kind;
+}
+
+// ------------------------------------------------------------------ bit helpers
+
+__device__ __forceinline__ uint32_t bits_of(float v) { return __float_as_uint(v); }
+__device__ __forceinline__ uint64_t bits_of(double v) { return (uint64_t)__double_as_longlong(v); }
+
+__device__ __forceinline__ bool finite_bits(float v)
+{
+    return (bits_of(v) & 0x7f800000u) != 0x7f800000u;
+}
+__device__ __forceinline__ bool finite_bits(double v)
+{
+    return (bits_of(v) & 0x7ff0000000000000ull) != 0x7ff0000000000000ull;
+}
+
+__device__ __forceinline__ bool is_zero(float v) { return (bits_of(v) & 0x7fffffffu) == 0; }
+__device__ __forceinline__ bool is_zero(double v) { return (bits_of(v) & 0x7fffffffffffffffull) == 0; }
+
+// Nonzero subnormal encoding.
+__device__ __forceinline__ bool subnormal(float v)
+{
+    uint32_t m = bits_of(v) & 0x7fffffffu;
+    return m != 0 && m < 0x00800000u;
+}
+__device__ __forceinline__ bool subnormal(double v)
+{
+    uint64_t m = bits_of(v) & 0x7fffffffffffffffull;
+    return m != 0 && m < 0x0010000000000000ull;
+}
+
+// |v| <= smallest normal (bitwise, so no flush mode can interfere).
+__device__ __forceinline__ bool at_most_min_normal(float v)
+{
+    return (bits_of(v) & 0x7fffffffu) <= 0x00800000u;
+}
+__device__ __forceinline__ bool at_most_min_normal(double v)
+{
+    return (bits_of(v) & 0x7fffffffffffffffull) <= 0x0010000000000000ull;
+}
+
+// ------------------------------------------------------------- add / subtract
+// An IEEE sum that is tiny is exact, so Add/Sub never raise tiny-inexact underflow;
+// RejectSubnormalResult still rejects a nonzero subnormal sum (including the zero-operand
+// passthrough, core/scalar_checked_float.rs:508-532). Exact cancellation gives +0.
+
+template <typename T>
+__device__ __forceinline__ uint32_t classify_add(T a, T b, T r, int policy)
+{
+    if (!finite_bits(a) || !finite_bits(b))
+        return kInvalid;
+    if (!finite_bits(r))
+        return kOverflow;
+    if (policy == kPolicyRejectSubnormal && subnormal(r))
+        return kUnderflow;
+    return kOk;
+}
+
+template <typename T>
+__device__ __forceinline__ bool add_suspect(T a, T b, T r, int policy)
+{
+    return !finite_bits(r) || !finite_bits(a) || !finite_bits(b) ||
+           (policy == kPolicyRejectSubnormal && subnormal(r));
+}
+
+// ------------------------------------------------------------------- multiply
+
+// Exact tininess/inexactness of a binary32 product: the product of two binary32 values
+// is exact in binary64 (48 significant bits), so comparisons against it are exact.
+// Tiny after rounding to 24 bits with an unbounded exponent <=> |p| < 2^-126 - 2^-151
+// (the midpoint below 2^-126 rounds up to 2^-126 under ties-to-even).
+__device__ __forceinline__ uint32_t mul_underflow_exact(float a, float b, float r, int policy)
+{
+    double p = (double)a * (double)b;
+    bool tiny = fabs(p) < 0x1.ffffffp-127;
+    bool inexact = (double)r != p;
+    if (policy == kPolicyIeee)
+        return (tiny && inexact) ? kUnderflow : kOk;
+    return (subnormal(r) || (tiny && inexact)) ? kUnderflow : kOk;
+}
+
+// Binary64: the 106-bit integer product of the significands decides both facts.
+// value(x) = sig * 2^q with sig < 2^53; value(a*b) = P * 2^(qa+qb).
+__device__ __forceinline__ void decode_f64(double v, uint64_t &sig, int &q)
+{
+    uint64_t b = bits_of(v);
+    uint64_t e = (b >> 52) & 0x7ff;
+    uint64_t f = b & 0x000fffffffffffffull;
+    if (e == 0) {
+        sig = f;
+        q = -1074;
+    } else {
+        sig = f | 0x0010000000000000ull;
+        q = (int)e - 1075;
+    }
+}
+
+__device__ __forceinline__ int bit_length_u128(uint64_t hi, uint64_t lo)
+{
+    return hi ? 128 - __clzll(hi) : (lo ? 64 - __clzll(lo) : 0);
+}
+
+// Low `n` bits of (hi:lo) are nonzero.
+__device__ __forceinline__ bool low_bits_nonzero(uint64_t hi, uint64_t lo, int n)
+{
+    if (n <= 0)
+        return false;
+    if (n >= 128)
+        return (hi | lo) != 0;
+    if (n >= 64)
+        return lo != 0 || (hi & ((n == 64) ? 0ull : ((1ull << (n - 64)) - 1))) != 0;
+    return (lo & ((1ull << n) - 1)) != 0;
+}
+
+// Bit `n` of (hi:lo).
+__device__ __forceinline__ uint64_t bit_at(uint64_t hi, uint64_t lo, int n)
+{
+    if (n < 0 || n >= 128)
+        return 0;
+    return n >= 64 ? (hi >> (n - 64)) & 1 : (lo >> n) & 1;
+}
+
+// Classify an exact value P * 2^q (P = hi:lo > 0) rounded to `prec` bits whose smallest
+// normal exponent is `emin` (value >= 2^emin is normal) and whose subnormal quantum is
+// 2^qmin. tiny: unbounded rounding < 2^emin; inexact: bounded rounding discards bits.
+__device__ __forceinline__ void classify_exact(uint64_t hi, uint64_t lo, int q, int prec, int emin,
+                                               int qmin, bool &tiny, bool &inexact)
+{
+    int len = bit_length_u128(hi, lo);
+    int top = len - 1;                 // value in [2^(top+q), 2^(top+q+1))
+    int e = top + q;                   // unbounded exponent before rounding
+    int drop = top - (prec - 1);       // bits of P below the kept precision
+    bool carry = false;
+    if (drop > 0) {
+        // Round to nearest even at bit `drop`; carry out when all kept bits are ones.
+        uint64_t half = bit_at(hi, lo, drop - 1);
+        bool sticky = low_bits_nonzero(hi, lo, drop - 1);
+        bool lsb = bit_at(hi, lo, drop) != 0;
+        bool up = half && (sticky || lsb);
+        if (up) {
+            // Kept bits all ones <=> P >> drop == 2^prec - 1.
+            bool all_ones = true;
+            for (int i = drop; i < drop + prec; i++)
+                if (!bit_at(hi, lo, i)) {
+                    all_ones = false;
+                    break;
+                }
+            carry = all_ones;
+        }
+    }
+    tiny = (e + (carry ? 1 : 0)) < emin;
+    // Bounded: the lowest kept weight is max(2^(e - prec + 1), 2^qmin).
+    int lowest = e - (prec - 1);
+    if (lowest < qmin)
+        lowest = qmin;
+    inexact = low_bits_nonzero(hi, lo, lowest - q);
+}
+
+__device__ __forceinline__ uint32_t mul_underflow_exact(double a, double b, double r, int policy)
+{
+    uint64_t sa, sb;
+    int qa, qb;
+    decode_f64(a, sa, qa);
+    decode_f64(b, sb, qb);
+    uint64_t lo = sa * sb;
+    uint64_t hi = __umul64hi(sa, sb);
+    bool tiny, inexact;
+    classify_exact(hi, lo, qa + qb, 53, -1022, -1074, tiny, inexact);
+    if (policy == kPolicyIeee)
+        return (tiny && inexact) ? kUnderflow : kOk;
+    return (subnormal(r) || (tiny && inexact)) ? kUnderflow : kOk;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t classify_mul(T a, T b, T r, int policy)
+{
+    if (!finite_bits(a) || !finite_bits(b))
+        return kInvalid;
+    if (!finite_bits(r))
+        return kOverflow;
+    if (policy == kPolicyAllowGradual || !at_most_min_normal(r))
+        return kOk;
+    if (is_zero(a) || is_zero(b))
+        return kOk; // exact signed zero (core/scalar_checked_float.rs:553-555)
+    return mul_underflow_exact(a, b, r, policy);
+}
+
+template <typename T>
+__device__ __forceinline__ bool mul_suspect(T a, T b, T r, int policy)
+{
+    return !finite_bits(r) || !finite_bits(a) || !finite_bits(b) ||
+           (policy != kPolicyAllowGradual && at_most_min_normal(r) && !is_zero(a) && !is_zero(b));
+}
+
+// --------------------------------------------------------------------- divide
+// Binary32: a = q*b exactly <=> (double)r*(double)b == (double)a (48-bit product, exact);
+// tiny <=> |a| < (2^-126 - 2^-151)*|b|, a 49-bit exact product in binary64.
+__device__ __forceinline__ uint32_t div_underflow_exact(float a, float b, float r, int policy)
+{
+    double ab = fabs((double)a), bb = fabs((double)b);
+    bool tiny = ab < 0x1.ffffffp-127 * bb;
+    bool inexact = (double)r * (double)b != (double)a;
+    if (policy == kPolicyIeee)
+        return (tiny && inexact) ? kUnderflow : kOk;
+    return (subnormal(r) || (tiny && inexact)) ? kUnderflow : kOk;
+}
+
+// Binary64 long division of the normalised significands: 56 quotient bits plus a sticky
+// remainder give the exact rounding facts (the reference divides with the same extent,
+// core/scalar_checked_float/f64.rs:372-431).
+__device__ __forceinline__ uint32_t div_underflow_exact(double a, double b, double r, int policy)
+{
+    uint64_t sa, sb;
+    int qa, qb;
+    decode_f64(a, sa, qa);
+    decode_f64(b, sb, qb);
+    int la = 63 - __clzll(sa), lb = 63 - __clzll(sb);
+    sa <<= (52 - la);
+    qa -= (52 - la);
+    sb <<= (52 - lb);
+    qb -= (52 - lb);
+    int q = qa - qb; // quotient = (sa/sb) * 2^q, sa/sb in (1/2, 2)
+    uint64_t num = sa;
+    if (num < sb) {
+        num <<= 1;
+        q -= 1;
+    }
+    // num/sb in [1, 2): produce 56 quotient bits (value Q * 2^(q-55)).
+    uint64_t quot = 0, rem = num;
+    for (int i = 0; i < 56; i++) {
+        quot <<= 1;
+        if (rem >= sb) {
+            rem -= sb;
+            quot |= 1;
+        }
+        rem <<= 1;
+    }
+    // Sticky: make the remainder visible as an extra low bit below the 56 quotient bits.
+    uint64_t lo = (quot << 1) | (rem != 0 ? 1ull : 0ull);
+    uint64_t hi = quot >> 63;
+    bool tiny, inexact;
+    classify_exact(hi, lo, q - 56, 53, -1022, -1074, tiny, inexact);
+    if (policy == kPolicyIeee)
+        return (tiny && inexact) ? kUnderflow : kOk;
+    return (subnormal(r) || (tiny && inexact)) ? kUnderflow : kOk;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t classify_div(T a, T b, T r, int policy)
+{
+    if (!finite_bits(a) || !finite_bits(b))
+        return kInvalid;
+    if (is_zero(b))
+        return kDivideByZero;
+    if (is_zero(a))
+        return kOk;
+    if (!finite_bits(r))
+        return kOverflow;
+    if (policy == kPolicyAllowGradual || !at_most_min_normal(r))
+        return kOk;
+    return div_underflow_exact(a, b, r, policy);
+}
+
+template <typename T>
+__device__ __forceinline__ bool div_suspect(T a, T b, T r, int policy)
+{
+    return !finite_bits(r) || !finite_bits(a) || !finite_bits(b) || is_zero(b) ||
+           (policy != kPolicyAllowGradual && at_most_min_normal(r) && !is_zero(a));
+}
+
+// ------------------------------------------------------------- relu selection
+// core/scalar_checked_float.rs:273-309: non-finite -> invalid; negative or zero -> +0;
+// policy applied to the (exact) selected value.
+template <typename T>
+__device__ __forceinline__ T relu_select(T x);
+template <>
+__device__ __forceinline__ float relu_select(float x)
+{
+    uint32_t b = bits_of(x);
+    return ((b & 0x80000000u) || (b & 0x7fffffffu) == 0) ? 0.0f : x;
+}
+template <>
+__device__ __forceinline__ double relu_select(double x)
+{
+    uint64_t b = bits_of(x);
+    return ((b >> 63) || (b & 0x7fffffffffffffffull) == 0) ? 0.0 : x;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t classify_relu(T x, T r, int policy)
+{
+    if (!finite_bits(x))
+        return kInvalid;
+    if (policy == kPolicyRejectSubnormal && subnormal(r))
+        return kUnderflow;
+    return kOk;
+}
+
+// core/scalar_checked_float.rs:634-652: strictly positive input selects upstream.
+template <typename T>
+__device__ __forceinline__ bool strictly_positive(T x)
+{
+    return !(bits_of(x) >> (sizeof(T) * 8 - 1)) && !is_zero(x);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t classify_relu_backward(T x, T up, T r, int policy)
+{
+    if (!finite_bits(x) || !finite_bits(up))
+        return kInvalid;
+    if (policy == kPolicyRejectSubnormal && subnormal(r))
+        return kUnderflow;
+    return kOk;
+}
+
+// ---------------------------------------------------------- wave reductions
+// Minimum of a 64-bit key over the wavefront (gfx950 waves are 64 lanes wide).
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        uint64_t o = __shfl_xor(v, off, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+// Record the wave's earliest packed fault with one atomic. `key` is kNoFault on lanes
+// without a fault; the ballot keeps the fault-free path to one instruction.
+__device__ __forceinline__ void wave_record_fault(uint64_t key, unsigned long long *word)
+{
+    if (__ballot(key != kNoFault) == 0)
+        return;
+    uint64_t m = wave_min_u64(key);
+    if (__lane_id() == 0)
+        atomicMin(word, (unsigned long long)m);
+}
+
+} // namespace pcu

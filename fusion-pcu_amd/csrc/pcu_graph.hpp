@@ -1,0 +1,88 @@
+// Host-side tensor graph: the reference's Graph builder, reverse-mode derivative of an MSE
+// root, execution plan, and a prepared executor over the strict kernels.
+#pragma once
+
+#include "pcu_runtime.hpp"
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace pcu {
+
+enum class Op : uint32_t {
+    Input = 0,
+    Uniform = 1,
+    Add = 2,
+    Sub = 3,
+    Mul = 4,
+    Div = 5,
+    SgdUpdate = 6,
+    MatMul = 7,
+    Relu = 8,
+    ReluBackward = 9,
+    MeanSquaredError = 10,
+};
+
+enum class Mode : int32_t { None = -1, Boundary = 0, Strict = 1 };
+
+struct Node {
+    Op op = Op::Input;
+    uint32_t a = UINT32_MAX, b = UINT32_MAX; // operands
+    bool tl = false, tr = false;             // MatMul transposes
+    float lr = 0.0f;                         // SgdUpdate rate
+    uint64_t value_bits = 0;                 // Uniform value (dtype-sized bit pattern)
+    std::vector<uint64_t> shape;
+    int dtype = 0;                           // 0 f32, 1 f64
+    Mode mode = Mode::None;                  // numerical mode (MatMul/MSE/SGD/ReluBackward)
+    int policy = -1;                         // float underflow policy; -1 when none
+};
+
+struct Graph {
+    std::vector<Node> nodes;
+    Mode mode = Mode::Boundary; // default numerical mode for new compound nodes
+    std::string error;
+
+    uint32_t push(Node n);
+    pcu_status check_id(uint32_t id) const;
+    uint64_t elements(uint32_t id) const;
+
+    pcu_status input(int dtype, const std::vector<uint64_t> &shape, uint32_t *id);
+    pcu_status uniform(int dtype, const std::vector<uint64_t> &shape, uint64_t bits, uint32_t *id);
+    pcu_status binary(Op op, uint32_t a, uint32_t b, uint32_t *id);
+    pcu_status relu(uint32_t x, uint32_t *id);
+    pcu_status relu_backward(uint32_t x, uint32_t up, uint32_t *id);
+    pcu_status matmul(uint32_t a, uint32_t b, bool tl, bool tr, uint32_t *id);
+    pcu_status mse(uint32_t p, uint32_t t, uint32_t *id);
+    pcu_status sgd(uint32_t w, uint32_t g, float lr, uint32_t *id);
+
+    // gradients.rs: build_backward_mse with optional targets. `grads` gets one entry per
+    // node that existed before the call (UINT32_MAX when the node has no derivative).
+    pcu_status backward(uint32_t loss, const std::vector<uint32_t> *targets,
+                        std::vector<uint32_t> *grads);
+    pcu_status plan(const std::vector<uint32_t> &outputs, std::vector<uint32_t> *order) const;
+};
+
+struct Prepared {
+    Ctx *ctx = nullptr;
+    Graph graph;                    // frozen copy
+    std::vector<uint32_t> order;    // plan
+    std::vector<uint32_t> outputs;  // requested outputs (graph ids)
+    std::vector<uint32_t> inputs;   // Input nodes in graph order
+    std::vector<void *> buf[2];     // per-node device buffers, two banks for outputs
+    std::vector<int> is_output;     // per node
+    std::vector<int> fused_into;    // Add fused into the ReLU at this id (or -1)
+    std::vector<int> mse_side;      // MSE runs on the side stream
+    std::vector<void *> dense_uniform;
+    int bank = 0;                   // bank written by the next execution
+    bool published = false;
+    std::vector<void *> published_ptr;
+    std::string error;
+
+    ~Prepared();
+    pcu_status build(Ctx *c, const Graph &g, const std::vector<uint32_t> &outs);
+    pcu_status execute(const std::vector<const void *> &device_inputs, pcu_fault *fault);
+    void *value_ptr(uint32_t id, const std::vector<const void *> &in, int bank) const;
+};
+
+} // namespace pcu

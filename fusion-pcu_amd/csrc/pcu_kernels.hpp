@@ -1,0 +1,53 @@
+// Host-side launch interface of the gfx950 kernels (implemented in *.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pcu {
+
+enum : int { kOpAdd = 0, kOpSub = 1, kOpMul = 2, kOpDiv = 3 };
+
+// Elementwise family. `b == nullptr` selects the uniform right operand `*b_value`
+// (host memory, dtype-sized). Each launcher enqueues on `s` and never synchronizes.
+hipError_t launch_binary(hipStream_t s, int dtype, int op, uint64_t n, const void *a,
+                         const void *b, const void *b_value, void *out, int policy,
+                         unsigned long long *fault);
+hipError_t launch_relu(hipStream_t s, int dtype, uint64_t n, const void *x, void *out,
+                       int policy, unsigned long long *fault);
+hipError_t launch_relu_backward(hipStream_t s, int dtype, uint64_t n, const void *x,
+                                const void *up, void *out, int policy,
+                                unsigned long long *fault);
+hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, const void *b,
+                           const void *b_value, void *out, int policy,
+                           unsigned long long *fault_add, unsigned long long *fault_relu);
+hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
+                      double rate, void *out, int policy, unsigned long long *fault);
+// `squares` is n elements of scratch; `count` is the element count rounded to the dtype.
+hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                      void *squares, double count, void *out, int policy,
+                      unsigned long long *fault);
+
+// Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.
+struct MatmulScratch {
+    int *row_exp;                  // rows entries
+    int *col_exp;                  // cols entries
+    unsigned long long *suspect;   // first suspect cell (kNoFault when none)
+};
+size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);
+MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
+
+// C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
+// `prior`/`n_prior` are the fault words of the ops enqueued before this one: the exact
+// replay skips its work once one of them holds a fault (that earlier fault is reported).
+hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
+                                uint64_t cols, bool transpose_left, bool transpose_right,
+                                const void *a, const void *b, void *c, int policy,
+                                MatmulScratch scratch, unsigned long long *fault,
+                                const unsigned long long *prior, unsigned n_prior);
+
+// Small device utilities (fill kernels rather than memsets, so a captured graph replays
+// them as kernels).
+hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value);
+
+} // namespace pcu

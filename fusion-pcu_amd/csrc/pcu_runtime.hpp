@@ -1,0 +1,84 @@
+// Host runtime state behind the C ABI.
+#pragma once
+
+#include "../../include/pcu_rocm.h"
+#include "pcu_kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+namespace pcu {
+
+extern thread_local std::string g_thread_error;
+
+// Ordered fault domain of one node (core/dialect/tensor/fault_domain/fault_domain.rs:30-34).
+enum class Prim { Elementwise, MatMul, Sgd, Mse };
+
+struct NodeInfo {
+    Prim prim;
+    uint64_t extent; // elements, or output cells for MatMul
+    uint64_t inner;  // MatMul reduction length
+};
+
+double count_as(int dtype, uint64_t n);
+
+struct Ctx {
+    static constexpr unsigned kMaxNodes = 4096;
+    static constexpr size_t kStagingBytes = 64u << 20;
+
+    int device = -1;
+    std::string arch;
+    hipStream_t stream = nullptr; // ordered work
+    hipStream_t side = nullptr;   // serial MSE sums overlapped with ordered work
+    hipEvent_t side_done = nullptr, main_ready = nullptr;
+    bool side_pending = false;
+    hipMemPool_t pool = nullptr;
+    void *staging = nullptr;
+    hipEvent_t staging_ev[2] = {nullptr, nullptr};
+    hipEvent_t marks[16] = {};
+    unsigned long long *fault_words = nullptr; // device, kMaxNodes words
+    unsigned long long *host_words = nullptr;  // pinned mirror
+    bool in_program = false;
+    bool implicit_program = false;
+    std::vector<NodeInfo> nodes;
+    std::string error;
+
+    Ctx() = default;
+    Ctx(const Ctx &) = delete;
+    Ctx &operator=(const Ctx &) = delete;
+    ~Ctx();
+
+    pcu_status open(int device);
+    void fail(const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+    pcu_status hip(hipError_t e, const char *what);
+
+    pcu_status alloc(size_t bytes, void **out);
+    pcu_status release(void *p);
+    pcu_status copy(void *dst, const void *src, size_t bytes, bool upload);
+    pcu_status join_side();
+    pcu_status scratch(size_t bytes, hipStream_t s, void **out);
+
+    pcu_status begin_program(bool implicit);
+    pcu_status end_program(pcu_fault *first);
+    pcu_status add_node(NodeInfo info, unsigned long long **word);
+    pcu_status start_op();
+    pcu_status finish_op(pcu_status launched, pcu_fault *fault);
+
+    pcu_status op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl, int tr,
+                         const void *a, const void *b, void *c, int policy);
+    pcu_status op_binary(int dtype, int op, uint64_t n, const void *a, const void *b,
+                         const void *b_value, void *out, int policy);
+    pcu_status op_relu(int dtype, uint64_t n, const void *x, void *out, int policy);
+    pcu_status op_relu_backward(int dtype, uint64_t n, const void *x, const void *up, void *out,
+                                int policy);
+    pcu_status op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
+                           const void *b_value, void *out, int policy);
+    pcu_status op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate, void *out,
+                      int policy);
+    pcu_status op_mse(int dtype, uint64_t n, const void *p, const void *t, void *out, int policy,
+                      bool on_side);
+};
+
+} // namespace pcu

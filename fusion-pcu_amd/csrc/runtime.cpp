@@ -1,0 +1,794 @@
+// Context, memory, staging, fault records and the op-level C ABI (include/pcu_rocm.h).
+//
+// Execution model: one ordered HIP stream per context. Every op enqueues its kernels and
+// records into its own 64-bit fault word (node-indexed array in device memory, filled
+// with the no-fault sentinel when a program begins). A program ends with one stream
+// synchronization and one device-to-host copy of the used fault words; the first word
+// holding a fault in node order is decoded into TensorError coordinates. This replaces the
+// reference's per-node sentinel upload, launch, event wait and 8-byte readback
+// (backends/rocm/owned_dispatch.rs:1137-1204, 1556-1580).
+#include "pcu_runtime.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+namespace pcu {
+
+thread_local std::string g_thread_error;
+
+static const uint64_t kNoFaultWord = ~0ull;
+
+void Ctx::fail(const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    error = buf;
+}
+
+pcu_status Ctx::hip(hipError_t e, const char *what)
+{
+    if (e == hipSuccess)
+        return PCU_OK;
+    fail("%s: %s", what, hipGetErrorString(e));
+    (void)hipGetLastError();
+    return e == hipErrorOutOfMemory ? PCU_ERR_OUT_OF_MEMORY : PCU_ERR_DEVICE;
+}
+
+pcu_status Ctx::open(int dev)
+{
+    device = dev;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= dev || dev < 0) {
+        fail("no HIP device %d (found %d)", dev, count);
+        return PCU_ERR_DEVICE;
+    }
+    pcu_status st;
+    if ((st = hip(hipSetDevice(dev), "hipSetDevice")))
+        return st;
+    hipDeviceProp_t prop;
+    if ((st = hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties")))
+        return st;
+    arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0) {
+        fail("device %d is %s; this library is built for gfx950 (MI355X) only", dev, arch.c_str());
+        return PCU_ERR_UNSUPPORTED;
+    }
+    if ((st = hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate")))
+        return st;
+    if ((st = hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate")))
+        return st;
+    if ((st = hip(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate")))
+        return st;
+    if ((st = hip(hipEventCreateWithFlags(&main_ready, hipEventDisableTiming), "hipEventCreate")))
+        return st;
+    for (auto &e : marks)
+        if ((st = hip(hipEventCreate(&e), "hipEventCreate")))
+            return st;
+    // Retain freed pool memory: resident weights and per-call scratch are reused without
+    // returning to the OS between calls.
+    if ((st = hip(hipDeviceGetDefaultMemPool(&pool, dev), "hipDeviceGetDefaultMemPool")))
+        return st;
+    uint64_t threshold = ~0ull;
+    if ((st = hip(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold),
+                  "hipMemPoolSetAttribute")))
+        return st;
+    if ((st = hip(hipHostMalloc(&staging, kStagingBytes, hipHostMallocDefault), "hipHostMalloc")))
+        return st;
+    for (auto &e : staging_ev)
+        if ((st = hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate")))
+            return st;
+    if ((st = hip(hipMalloc(&fault_words, sizeof(unsigned long long) * kMaxNodes), "hipMalloc")))
+        return st;
+    if ((st = hip(hipHostMalloc((void **)&host_words, sizeof(unsigned long long) * kMaxNodes,
+                                hipHostMallocDefault), "hipHostMalloc")))
+        return st;
+    return PCU_OK;
+}
+
+Ctx::~Ctx()
+{
+    if (device < 0)
+        return;
+    (void)hipSetDevice(device);
+    if (stream)
+        (void)hipStreamSynchronize(stream);
+    if (side)
+        (void)hipStreamSynchronize(side);
+    if (fault_words)
+        (void)hipFree(fault_words);
+    if (host_words)
+        (void)hipHostFree(host_words);
+    if (staging)
+        (void)hipHostFree(staging);
+    for (auto &e : staging_ev)
+        if (e)
+            (void)hipEventDestroy(e);
+    for (auto &e : marks)
+        if (e)
+            (void)hipEventDestroy(e);
+    if (side_done)
+        (void)hipEventDestroy(side_done);
+    if (main_ready)
+        (void)hipEventDestroy(main_ready);
+    if (stream)
+        (void)hipStreamDestroy(stream);
+    if (side)
+        (void)hipStreamDestroy(side);
+}
+
+pcu_status Ctx::alloc(size_t bytes, void **out)
+{
+    if (!out) {
+        fail("null output pointer");
+        return PCU_ERR_ARGUMENT;
+    }
+    *out = nullptr;
+    if (bytes == 0)
+        bytes = 1;
+    pcu_status st = hip(hipMallocFromPoolAsync(out, bytes, pool, stream), "hipMallocFromPoolAsync");
+    if (st || in_program)
+        return st; // inside a program the buffer is used in stream order until the end
+    // Usable from any stream once the allocation is ordered.
+    return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+}
+
+pcu_status Ctx::release(void *p)
+{
+    if (!p)
+        return PCU_OK;
+    // Work still queued on the side stream may read the buffer.
+    pcu_status st = join_side();
+    if (st)
+        return st;
+    return hip(hipFreeAsync(p, stream), "hipFreeAsync");
+}
+
+pcu_status Ctx::join_side()
+{
+    if (!side_pending)
+        return PCU_OK;
+    pcu_status st = hip(hipEventRecord(side_done, side), "hipEventRecord");
+    if (st)
+        return st;
+    st = hip(hipStreamWaitEvent(stream, side_done, 0), "hipStreamWaitEvent");
+    side_pending = false;
+    return st;
+}
+
+pcu_status Ctx::copy(void *dst, const void *src, size_t bytes, bool upload)
+{
+    if (bytes == 0)
+        return PCU_OK;
+    if (!dst || !src) {
+        fail("null copy pointer");
+        return PCU_ERR_ARGUMENT;
+    }
+    pcu_status st = join_side();
+    if (st)
+        return st;
+    // Double-buffered pinned staging: the host copy into (or out of) one half overlaps the
+    // DMA of the other half.
+    const size_t half = kStagingBytes / 2;
+    char *stage[2] = {(char *)staging, (char *)staging + half};
+    size_t off = 0;
+    int slot = 0;
+    bool used[2] = {false, false};
+    if (upload) {
+        while (off < bytes) {
+            size_t n = std::min(half, bytes - off);
+            if (used[slot] && (st = hip(hipEventSynchronize(staging_ev[slot]), "hipEventSynchronize")))
+                return st;
+            memcpy(stage[slot], (const char *)src + off, n);
+            if ((st = hip(hipMemcpyAsync((char *)dst + off, stage[slot], n, hipMemcpyHostToDevice, stream),
+                          "hipMemcpyAsync")))
+                return st;
+            if ((st = hip(hipEventRecord(staging_ev[slot], stream), "hipEventRecord")))
+                return st;
+            used[slot] = true;
+            off += n;
+            slot ^= 1;
+        }
+        return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    }
+    // Download: keep one chunk in flight while the previous one is copied out.
+    size_t pending_off = 0, pending_n = 0;
+    int pending_slot = -1;
+    while (off < bytes || pending_slot >= 0) {
+        if (off < bytes) {
+            size_t n = std::min(half, bytes - off);
+            if ((st = hip(hipMemcpyAsync(stage[slot], (const char *)src + off, n, hipMemcpyDeviceToHost, stream),
+                          "hipMemcpyAsync")))
+                return st;
+            if ((st = hip(hipEventRecord(staging_ev[slot], stream), "hipEventRecord")))
+                return st;
+            if (pending_slot >= 0) {
+                if ((st = hip(hipEventSynchronize(staging_ev[pending_slot]), "hipEventSynchronize")))
+                    return st;
+                memcpy((char *)dst + pending_off, stage[pending_slot], pending_n);
+            }
+            pending_off = off;
+            pending_n = n;
+            pending_slot = slot;
+            off += n;
+            slot ^= 1;
+        } else {
+            if ((st = hip(hipEventSynchronize(staging_ev[pending_slot]), "hipEventSynchronize")))
+                return st;
+            memcpy((char *)dst + pending_off, stage[pending_slot], pending_n);
+            pending_slot = -1;
+        }
+    }
+    return PCU_OK;
+}
+
+// ---------------------------------------------------------------- programs
+
+pcu_status Ctx::begin_program(bool implicit)
+{
+    if (in_program) {
+        fail("a program is already open on this context");
+        return PCU_ERR_STATE;
+    }
+    pcu_status st = hip(hipSetDevice(device), "hipSetDevice");
+    if (st)
+        return st;
+    in_program = true;
+    implicit_program = implicit;
+    nodes.clear();
+    // Only the words a program uses are read back; fill them all once (a kernel rather
+    // than a memset so the sequence stays capturable).
+    return hip(launch_fill_u64(stream, fault_words, kMaxNodes, kNoFaultWord), "fill fault words");
+}
+
+pcu_status Ctx::add_node(NodeInfo info, unsigned long long **word)
+{
+    if (!in_program) {
+        fail("no program open");
+        return PCU_ERR_STATE;
+    }
+    if (nodes.size() >= kMaxNodes) {
+        fail("program exceeds %u nodes", kMaxNodes);
+        return PCU_ERR_STATE;
+    }
+    *word = fault_words + nodes.size();
+    nodes.push_back(info);
+    return PCU_OK;
+}
+
+// Decode a packed word under the op's ordered fault domain
+// (core/dialect/tensor/fault_domain/fault_domain.rs:122-180) and reject statuses no
+// admitted op can produce (the reference treats them as protocol errors:
+// backends/rocm/owned_dispatch.rs:127-141).
+static bool decode_word(const NodeInfo &n, uint64_t word, pcu_fault *f)
+{
+    uint64_t ordinal = word >> 3;
+    uint32_t kind = (uint32_t)(word & 7);
+    if (kind != PCU_FAULT_DIVIDE_BY_ZERO && kind != PCU_FAULT_OVERFLOW &&
+        kind != PCU_FAULT_UNDERFLOW && kind != PCU_FAULT_INVALID)
+        return false;
+    f->kind = kind;
+    f->ordinal = ordinal;
+    f->element_index = 0;
+    f->reduction_index = 0;
+    f->step = PCU_STEP_NONE;
+    switch (n.prim) {
+    case Prim::Elementwise:
+        if (ordinal >= n.extent)
+            return false;
+        f->element_index = ordinal;
+        return true;
+    case Prim::MatMul: {
+        if (n.inner == 0 || ordinal >= n.extent * n.inner * 2)
+            return false;
+        uint64_t pair = ordinal / 2;
+        f->element_index = pair / n.inner;
+        f->reduction_index = pair % n.inner;
+        f->step = (ordinal & 1) ? PCU_STEP_ADD : PCU_STEP_MULTIPLY;
+        // The first Add of a cell adds a checked product to +0: it cannot fault.
+        if ((ordinal & 1) && f->reduction_index == 0)
+            return false;
+        return kind != PCU_FAULT_DIVIDE_BY_ZERO;
+    }
+    case Prim::Sgd:
+        if (ordinal >= n.extent * 2)
+            return false;
+        f->element_index = ordinal / 2;
+        f->step = (ordinal & 1) ? PCU_STEP_SUBTRACT : PCU_STEP_MULTIPLY;
+        return kind != PCU_FAULT_DIVIDE_BY_ZERO;
+    case Prim::Mse:
+        if (ordinal > n.extent * 3)
+            return false;
+        if (ordinal == n.extent * 3) {
+            f->reduction_index = n.extent;
+            f->step = PCU_STEP_DIVIDE;
+            return kind == PCU_FAULT_UNDERFLOW;
+        }
+        f->reduction_index = ordinal / 3;
+        f->step = ordinal % 3 == 0 ? PCU_STEP_SUBTRACT
+                                   : (ordinal % 3 == 1 ? PCU_STEP_MULTIPLY : PCU_STEP_ADD);
+        return kind != PCU_FAULT_DIVIDE_BY_ZERO;
+    }
+    return false;
+}
+
+pcu_status Ctx::end_program(pcu_fault *first)
+{
+    if (!in_program) {
+        fail("no program open");
+        return PCU_ERR_STATE;
+    }
+    in_program = false;
+    pcu_status st = join_side();
+    if (st)
+        return st;
+    size_t used = nodes.size();
+    if (used) {
+        if ((st = hip(hipMemcpyAsync(host_words, fault_words, used * sizeof(unsigned long long),
+                                     hipMemcpyDeviceToHost, stream), "hipMemcpyAsync")))
+            return st;
+    }
+    if ((st = hip(hipStreamSynchronize(stream), "hipStreamSynchronize")))
+        return st;
+    for (size_t i = 0; i < used; i++) {
+        uint64_t w = host_words[i];
+        if (w == kNoFaultWord)
+            continue;
+        pcu_fault f;
+        memset(&f, 0, sizeof f);
+        if (!decode_word(nodes[i], w, &f)) {
+            fail("malformed fault word 0x%016llx at node %zu", (unsigned long long)w, i);
+            return PCU_ERR_PROTOCOL;
+        }
+        f.node = (uint32_t)i;
+        if (first)
+            *first = f;
+        return PCU_ARITHMETIC_FAULT;
+    }
+    return PCU_OK;
+}
+
+pcu_status Ctx::finish_op(pcu_status launched, pcu_fault *fault)
+{
+    if (!implicit_program)
+        return launched;
+    if (launched) {
+        in_program = false;
+        (void)hipStreamSynchronize(stream);
+        return launched;
+    }
+    implicit_program = false;
+    return end_program(fault);
+}
+
+pcu_status Ctx::start_op()
+{
+    if (in_program)
+        return hip(hipSetDevice(device), "hipSetDevice");
+    return begin_program(true);
+}
+
+// Scratch comes from the stream-ordered pool and is released on the same stream right
+// after the op's kernels, so later ops reuse it without a host round trip.
+pcu_status Ctx::scratch(size_t bytes, hipStream_t s, void **out)
+{
+    return hip(hipMallocFromPoolAsync(out, bytes ? bytes : 1, pool, s), "hipMallocFromPoolAsync");
+}
+
+// ---------------------------------------------------------------------- ops
+
+static bool valid_dtype(int d) { return d == PCU_F32 || d == PCU_F64; }
+static bool valid_policy(int p) { return p >= 0 && p <= 2; }
+static size_t dsize(int d) { return d == PCU_F32 ? 4 : 8; }
+
+pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
+                          int tr, const void *a, const void *b, void *c, int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || !c || ((rows * inner) && !a) ||
+        ((inner * cols) && !b)) {
+        fail("strict_matmul: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    NodeInfo info{Prim::MatMul, rows * cols, inner};
+    pcu_status st = add_node(info, &word);
+    if (st)
+        return st;
+    if (rows == 0 || cols == 0)
+        return PCU_OK;
+    void *sc = nullptr;
+    if ((st = scratch(matmul_scratch_bytes(rows, cols), stream, &sc)))
+        return st;
+    MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
+    unsigned prior = (unsigned)(word - fault_words);
+    hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
+                                        b, c, policy, s, word, fault_words, prior);
+    if ((st = hip(e, "strict_matmul launch")))
+        return st;
+    return hip(hipFreeAsync(sc, stream), "hipFreeAsync");
+}
+
+pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const void *b,
+                          const void *b_value, void *out, int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || op < 0 || op > 3 ||
+        (n && (!a || !out || (!b && !b_value)))) {
+        fail("checked_binary: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
+    if (st)
+        return st;
+    return hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word), "checked_binary launch");
+}
+
+pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!x || !out))) {
+        fail("checked_relu: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
+    if (st)
+        return st;
+    return hip(launch_relu(stream, dtype, n, x, out, policy, word), "checked_relu launch");
+}
+
+pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const void *up, void *out,
+                                 int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!x || !up || !out))) {
+        fail("checked_relu_backward: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
+    if (st)
+        return st;
+    return hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word),
+               "checked_relu_backward launch");
+}
+
+pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
+                            const void *b_value, void *out, int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!a || !out || (!b && !b_value)))) {
+        fail("checked_add_relu: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *w_add, *w_relu;
+    pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &w_add);
+    if (st)
+        return st;
+    if ((st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &w_relu)))
+        return st;
+    return hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu),
+               "checked_add_relu launch");
+}
+
+// The F64 rate is the exact widening of the F32 literal (reference.rs:507-514); a float
+// converts to double exactly.
+pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
+                       void *out, int policy)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!w || !g || !out))) {
+        fail("strict_sgd: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    uint32_t rb;
+    memcpy(&rb, &rate, 4);
+    if ((rb & 0x7f800000u) == 0x7f800000u) {
+        fail("strict_sgd: learning rate must be finite (TensorError::InvalidLearningRate)");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Sgd, n, 0}, &word);
+    if (st)
+        return st;
+    return hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word), "strict_sgd launch");
+}
+
+// Element count rounded to nearest even (core/dialect/tensor/constants/constants.rs:18-28).
+double count_as(int dtype, uint64_t n)
+{
+    if (dtype == PCU_F64)
+        return (double)n; // u64 -> binary64 conversion rounds to nearest even
+    // u64 -> binary32 rounded to nearest even with integer operations.
+    if (n == 0)
+        return 0.0;
+    int top = 63 - __builtin_clzll(n);
+    uint64_t sig;
+    int exp = top;
+    if (top <= 23) {
+        sig = n;
+    } else {
+        int shift = top - 23;
+        uint64_t q = n >> shift, rem = n & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+        sig = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+        if (sig == (1ull << 24)) {
+            sig >>= 1;
+            exp += 1;
+        }
+        return ldexp((double)sig, exp - 23);
+    }
+    return (double)sig;
+}
+
+pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void *out,
+                       int policy, bool on_side)
+{
+    if (!valid_dtype(dtype) || !valid_policy(policy) || !p || !t || !out) {
+        fail("strict_mse: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (n == 0) {
+        fail("strict_mse: empty input (TensorError::ShapeMismatch)");
+        return PCU_ERR_SHAPE;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Mse, n, 0}, &word);
+    if (st)
+        return st;
+    hipStream_t s = stream;
+    if (on_side) {
+        // The serial sum overlaps the following ordered work; the side stream starts after
+        // everything enqueued so far (the prediction's producers).
+        if ((st = hip(hipEventRecord(main_ready, stream), "hipEventRecord")))
+            return st;
+        if ((st = hip(hipStreamWaitEvent(side, main_ready, 0), "hipStreamWaitEvent")))
+            return st;
+        s = side;
+        side_pending = true;
+    }
+    void *sq = nullptr;
+    if ((st = scratch(n * dsize(dtype), s, &sq)))
+        return st;
+    if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word),
+                  "strict_mse launch")))
+        return st;
+    return hip(hipFreeAsync(sq, s), "hipFreeAsync");
+}
+
+} // namespace pcu
+
+// ======================================================================= C ABI
+
+using pcu::Ctx;
+
+static pcu_status bad_ctx()
+{
+    pcu::g_thread_error = "null context";
+    return PCU_ERR_ARGUMENT;
+}
+
+extern "C" {
+
+int pcu_abi_version(void) { return PCU_ROCM_ABI_VERSION; }
+
+pcu_status pcu_ctx_open(int device, pcu_ctx **out)
+{
+    if (!out) {
+        pcu::g_thread_error = "null output pointer";
+        return PCU_ERR_ARGUMENT;
+    }
+    *out = nullptr;
+    Ctx *c = new (std::nothrow) Ctx();
+    if (!c) {
+        pcu::g_thread_error = "out of host memory";
+        return PCU_ERR_OUT_OF_MEMORY;
+    }
+    pcu_status st = c->open(device);
+    if (st) {
+        pcu::g_thread_error = c->error;
+        delete c;
+        return st;
+    }
+    *out = reinterpret_cast<pcu_ctx *>(c);
+    return PCU_OK;
+}
+
+void pcu_ctx_close(pcu_ctx *ctx) { delete reinterpret_cast<Ctx *>(ctx); }
+
+const char *pcu_last_error(const pcu_ctx *ctx)
+{
+    if (!ctx)
+        return pcu::g_thread_error.c_str();
+    return reinterpret_cast<const Ctx *>(ctx)->error.c_str();
+}
+
+void *pcu_ctx_stream(pcu_ctx *ctx) { return ctx ? (void *)reinterpret_cast<Ctx *>(ctx)->stream : nullptr; }
+
+pcu_status pcu_ctx_synchronize(pcu_ctx *ctx)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    pcu_status st = c->join_side();
+    if (st)
+        return st;
+    return c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+pcu_status pcu_buf_alloc(pcu_ctx *ctx, size_t bytes, void **device_ptr)
+{
+    if (!ctx)
+        return bad_ctx();
+    return reinterpret_cast<Ctx *>(ctx)->alloc(bytes, device_ptr);
+}
+
+pcu_status pcu_buf_free(pcu_ctx *ctx, void *device_ptr)
+{
+    if (!ctx)
+        return bad_ctx();
+    return reinterpret_cast<Ctx *>(ctx)->release(device_ptr);
+}
+
+pcu_status pcu_upload(pcu_ctx *ctx, void *device_dst, const void *host_src, size_t bytes)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (c->in_program) {
+        c->fail("pcu_upload inside a program");
+        return PCU_ERR_STATE;
+    }
+    return c->copy(device_dst, host_src, bytes, true);
+}
+
+pcu_status pcu_download(pcu_ctx *ctx, void *host_dst, const void *device_src, size_t bytes)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (c->in_program) {
+        c->fail("pcu_download inside a program");
+        return PCU_ERR_STATE;
+    }
+    return c->copy(host_dst, device_src, bytes, false);
+}
+
+#define PCU_OP_PROLOGUE                       \
+    if (!ctx)                                 \
+        return bad_ctx();                     \
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);    \
+    pcu_status st = c->start_op();            \
+    if (st)                                   \
+        return st;
+
+pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
+                             uint64_t cols, int transpose_left, int transpose_right,
+                             const void *left, const void *right, void *out,
+                             pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_matmul(dtype, rows, inner, cols, transpose_left, transpose_right, left, right, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_checked_binary(pcu_ctx *ctx, pcu_dtype dtype, pcu_binary_op op, uint64_t n,
+                              const void *left, const void *right, void *out,
+                              pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    if (n && !right) {
+        c->fail("checked_binary: null right operand");
+        return c->finish_op(PCU_ERR_ARGUMENT, fault);
+    }
+    st = c->op_binary(dtype, op, n, left, right, nullptr, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_checked_binary_uniform(pcu_ctx *ctx, pcu_dtype dtype, pcu_binary_op op,
+                                      uint64_t n, const void *left, uint64_t right_bits,
+                                      void *out, pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    uint32_t b32 = (uint32_t)right_bits;
+    const void *value = dtype == PCU_F32 ? (const void *)&b32 : (const void *)&right_bits;
+    st = c->op_binary(dtype, op, n, left, nullptr, value, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_checked_relu(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *input,
+                            void *out, pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_relu(dtype, n, input, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_checked_relu_backward(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n,
+                                     const void *input, const void *upstream, void *out,
+                                     pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_relu_backward(dtype, n, input, upstream, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_checked_add_relu(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *left,
+                                const void *right, void *out, pcu_underflow policy,
+                                pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    if (n && !right) {
+        c->fail("checked_add_relu: null right operand");
+        return c->finish_op(PCU_ERR_ARGUMENT, fault);
+    }
+    st = c->op_add_relu(dtype, n, left, right, nullptr, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_strict_sgd(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *weights,
+                          const void *gradient, float learning_rate, void *out,
+                          pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_sgd(dtype, n, weights, gradient, learning_rate, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_strict_mse(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *prediction,
+                          const void *target, void *out_scalar, pcu_underflow policy,
+                          pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_mse(dtype, n, prediction, target, out_scalar, policy, false);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_program_begin(pcu_ctx *ctx)
+{
+    if (!ctx)
+        return bad_ctx();
+    return reinterpret_cast<Ctx *>(ctx)->begin_program(false);
+}
+
+pcu_status pcu_program_end(pcu_ctx *ctx, pcu_fault *first_fault)
+{
+    if (!ctx)
+        return bad_ctx();
+    return reinterpret_cast<Ctx *>(ctx)->end_program(first_fault);
+}
+
+uint32_t pcu_program_next_node(const pcu_ctx *ctx)
+{
+    return ctx ? (uint32_t)reinterpret_cast<const Ctx *>(ctx)->nodes.size() : 0;
+}
+
+pcu_status pcu_mark(pcu_ctx *ctx, int slot)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (slot < 0 || slot >= (int)(sizeof(c->marks) / sizeof(c->marks[0]))) {
+        c->fail("mark slot out of range");
+        return PCU_ERR_ARGUMENT;
+    }
+    return c->hip(hipEventRecord(c->marks[slot], c->stream), "hipEventRecord");
+}
+
+pcu_status pcu_elapsed_ms(pcu_ctx *ctx, int from_slot, int to_slot, float *ms)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    int n = (int)(sizeof(c->marks) / sizeof(c->marks[0]));
+    if (from_slot < 0 || to_slot < 0 || from_slot >= n || to_slot >= n || !ms) {
+        c->fail("mark slot out of range");
+        return PCU_ERR_ARGUMENT;
+    }
+    pcu_status st = c->hip(hipEventSynchronize(c->marks[to_slot]), "hipEventSynchronize");
+    if (st)
+        return st;
+    return c->hip(hipEventElapsedTime(ms, c->marks[from_slot], c->marks[to_slot]), "hipEventElapsedTime");
+}
+
+} // extern "C"

@@ -1,0 +1,59 @@
+"""CPU-side checks of the C ABI: the library loads without a GPU and exports every
+function include/pcu_rocm.h declares, and the Python binding covers the same set."""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for header in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not header.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", header)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(pcu_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for required in ("pcu_ctx_open", "pcu_strict_matmul", "pcu_strict_sgd", "pcu_strict_mse",
+                     "pcu_checked_binary", "pcu_checked_relu", "pcu_checked_relu_backward",
+                     "pcu_program_begin", "pcu_program_end"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(pcu_pkg):
+    lib_path = pcu_pkg.library_path()
+    assert os.path.exists(lib_path), "build the library first (python __graft_entry__.py)"
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = sorted(_declared_functions() - exported)
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_binding_covers_header_and_loads_without_gpu(pcu_pkg):
+    from fusion_pcu_amd import _abi
+    assert set(_abi.SIGNATURES) >= _declared_functions() - _graph_only()
+    lib = pcu_pkg.lib()
+    assert lib.pcu_abi_version() == 1
+
+
+def _graph_only():
+    from fusion_pcu_amd import _abi
+    return {n for n in _declared_functions() if n not in _abi.SIGNATURES and n.startswith("pcu_graph")}
+
+
+def test_opening_a_context_without_gpu_fails_loudly(pcu_pkg):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        pcu_pkg.Context(0)

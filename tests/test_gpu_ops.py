@@ -1,0 +1,382 @@
+"""GPU parity of every op-level entry point against the CPU oracle (bit-exact values and
+first-fault coordinates), through the C ABI. Sizes are chosen so the oracle finishes in
+seconds; the full BASELINE sizes live in test_gpu_configs.py."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+POLICY = {"IeeeAfterRounding": 0, "RejectSubnormalResult": 1, "AllowGradualUnderflow": 2}
+OP_NAMES = ["add", "sub", "mul", "div"]
+
+
+@pytest.fixture(scope="module")
+def ctx(pcu_pkg):
+    c = pcu_pkg.Context(0)
+    yield c
+    c.close()
+
+
+def _gpu_fault(pcu_pkg, fn):
+    """Run fn; return (result, oracle-style fault tuple or None)."""
+    try:
+        return fn(), None
+    except pcu_pkg.PcuExecutionError as e:
+        assert e.tensor_fault is not None, e
+        f = e.tensor_fault
+        return None, (f.element_index, f.reduction_index, int(f.step), int(f.kind))
+
+
+def _ofault(f):
+    return None if f is None else (f.element_index, f.reduction_index, f.step, f.kind)
+
+
+def _bits(a):
+    a = np.asarray(a)
+    return a.view(np.uint32 if a.dtype == np.float32 else np.uint64)
+
+
+def _patterns(rng, n, dtype, low):
+    if dtype == np.float32:
+        b = rng.integers(0, 2 ** 32, size=n, dtype=np.uint64).astype(np.uint32)
+        if low:
+            e = rng.integers(0, 90, size=n).astype(np.uint32)
+            b = (b & np.uint32(0x807FFFFF)) | (e << np.uint32(23))
+        return b.view(np.float32)
+    b = rng.integers(0, 2 ** 63, size=n, dtype=np.uint64) * np.uint64(2)
+    if low:
+        e = rng.integers(0, 560, size=n).astype(np.uint64)
+        b = (b & np.uint64(0x800FFFFFFFFFFFFF)) | (e << np.uint64(52))
+    return b.view(np.float64)
+
+
+# ---------------------------------------------------------------- scalar law
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_scalar_law_single_element_parity(ctx, pcu_pkg, dtype):
+    """Each op on one element at a time: value and fault kind equal the integer law,
+    including tiny-after-rounding underflow near the subnormal range."""
+    rng = np.random.default_rng(1234 + (dtype == np.float64))
+    a = np.concatenate([_patterns(rng, 150, dtype, False), _patterns(rng, 250, dtype, True)])
+    b = np.concatenate([_patterns(rng, 150, dtype, False), _patterns(rng, 250, dtype, True)])
+    a[:4] = [np.inf, -0.0, np.nan, np.finfo(dtype).tiny]
+    b[:4] = [1.0, 0.0, 0.0, 0.5]
+    da, db = ctx.upload(a), ctx.upload(b)
+    out = ctx.empty((1,), dtype)
+    mism = []
+    es = np.dtype(dtype).itemsize
+    for i in range(len(a)):
+        va = pcu_pkg.DeviceArray(ctx, da.ptr + i * es, (1,), dtype)
+        vb = pcu_pkg.DeviceArray(ctx, db.ptr + i * es, (1,), dtype)
+        for op in range(4):
+            for policy in (0, 1, 2):
+                got, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_binary(op, va, vb, policy, out=out).numpy())
+                ref, rf = oracle.binary(op, a[i:i + 1], b[i:i + 1], policy=policy, fast=False)
+                if _ofault(rf) != gf or (rf is None and _bits(got)[0] != _bits(ref)[0]):
+                    mism.append((OP_NAMES[op], policy, hex(int(_bits(a)[i])), hex(int(_bits(b)[i])), gf, _ofault(rf)))
+    assert not mism, mism[:10]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("n", [1, 3, 4097, 1 << 20])
+def test_binary_arrays_parity(ctx, pcu_pkg, dtype, n):
+    rng = np.random.default_rng(n)
+    a = rng.uniform(-4, 4, n).astype(dtype)
+    b = rng.uniform(-4, 4, n).astype(dtype)
+    b[b == 0] = 1
+    da, db = ctx.upload(a), ctx.upload(b)
+    for op in range(4):
+        for uniform in (False, True):
+            rhs = b[0] if uniform else db
+            got = ctx.checked_binary(op, da, rhs).numpy()
+            ref, rf = oracle.binary(op, a, b[:1] if uniform else b)
+            assert rf is None
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_binary_first_fault_parity(ctx, pcu_pkg, dtype):
+    rng = np.random.default_rng(99)
+    n = 100_003
+    for trial in range(6):
+        a = rng.uniform(-1, 1, n).astype(dtype)
+        b = rng.uniform(-1, 1, n).astype(dtype)
+        k = rng.integers(1, 6)
+        idx = rng.choice(n, size=k, replace=False)
+        kinds = [np.nan, np.inf, np.finfo(dtype).max, np.finfo(dtype).tiny * 0.5,
+                 np.finfo(dtype).tiny]
+        a[idx] = rng.choice(np.array(kinds, dtype=dtype), size=k)
+        b[idx] = rng.choice(np.array([2.0, 0.0, -np.finfo(dtype).max, 0.25], dtype=dtype), size=k)
+        da, db = ctx.upload(a), ctx.upload(b)
+        for op in range(4):
+            for policy in (0, 1, 2):
+                _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_binary(op, da, db, policy))
+                _, rf = oracle.binary(op, a, b, policy=policy)
+                assert gf == _ofault(rf), (trial, OP_NAMES[op], policy, gf, rf)
+
+
+# --------------------------------------------------------------------- relu
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_relu_family_parity(ctx, pcu_pkg, dtype):
+    rng = np.random.default_rng(5)
+    n = 65_537
+    x = np.concatenate([_patterns(rng, n // 2, dtype, True), rng.uniform(-2, 2, n - n // 2).astype(dtype)])
+    x = x[np.isfinite(x)]
+    up = rng.uniform(-2, 2, x.size).astype(dtype)
+    dx, dup = ctx.upload(x), ctx.upload(up)
+    for policy in (0, 1, 2):
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_relu(dx, policy).numpy())
+        ref, rf = oracle.relu(x, policy=policy)
+        assert gf == _ofault(rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_relu_backward(dx, dup, policy).numpy())
+        ref, rf = oracle.relu_backward(x, up, policy=policy)
+        assert gf == _ofault(rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+    x2 = x.copy()
+    x2[777] = np.nan
+    _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_relu(ctx.upload(x2)))
+    assert gf == (777, 0, 0, 5)
+    up2 = up.copy()
+    up2[333] = -np.inf
+    _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_relu_backward(dx, ctx.upload(up2)))
+    assert gf == (333, 0, 0, 5)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_fused_add_relu_reports_add_then_relu(ctx, pcu_pkg, dtype):
+    rng = np.random.default_rng(8)
+    n = 10_000
+    a = rng.uniform(-1, 1, n).astype(dtype)
+    b = rng.uniform(-1, 1, n).astype(dtype)
+    da, db = ctx.upload(a), ctx.upload(b)
+    got = ctx.checked_add_relu(da, db).numpy()
+    s, _ = oracle.binary(oracle.OP_ADD, a, b)
+    ref, _ = oracle.relu(s)
+    np.testing.assert_array_equal(_bits(got), _bits(ref))
+    # An Add overflow at 900 is node 0 even though a later element would fault too.
+    a[900] = np.finfo(dtype).max
+    b[900] = np.finfo(dtype).max
+    a[5000] = np.nan
+    da, db = ctx.upload(a), ctx.upload(b)
+    with ctx.program():
+        pass
+    try:
+        with ctx.program():
+            ctx.checked_add_relu(da, db)
+        raise AssertionError("expected a fault")
+    except pcu_pkg.PcuExecutionError as e:
+        f = e.tensor_fault
+        assert (f.node, f.element_index, int(f.kind)) == (0, 900, 3)
+
+
+# ---------------------------------------------------------------------- SGD
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("n", [1, 5, 1 << 16, (1 << 20) + 3])
+def test_sgd_parity(ctx, pcu_pkg, dtype, n):
+    rng = np.random.default_rng(n + 17)
+    w = rng.normal(0, 1, n).astype(dtype)
+    g = rng.normal(0, 1e-3, n).astype(dtype)
+    dw, dg = ctx.upload(w), ctx.upload(g)
+    for rate in (0.01, 0.1, 1.0e-3):
+        got = ctx.strict_sgd(dw, dg, rate).numpy()
+        ref, rf = oracle.sgd(w, g, rate)
+        assert rf is None
+        np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_sgd_faults_parity(ctx, pcu_pkg, dtype):
+    rng = np.random.default_rng(31)
+    n = 50_000
+    for trial in range(8):
+        w = rng.normal(0, 1, n).astype(dtype)
+        g = rng.normal(0, 1e-3, n).astype(dtype)
+        sl = slice(1000 + trial * 3000, 1000 + trial * 3000 + 500)
+        w[sl] = np.finfo(dtype).tiny * 0.9  # near-subnormal weights (the C4 slice)
+        if trial % 2:
+            g[sl] = np.finfo(dtype).tiny * 7  # 0.01 * g is tiny and inexact
+        if trial == 2:
+            g[40_000] = np.inf
+        if trial == 4:
+            w[20] = np.nan
+        if trial == 6:
+            w[7] = np.finfo(dtype).max
+            g[7] = -np.finfo(dtype).max
+        dw, dg = ctx.upload(w), ctx.upload(g)
+        for policy in (0, 1, 2):
+            rate = 1.0 if trial == 6 else 0.01
+            got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_sgd(dw, dg, rate, policy).numpy())
+            ref, rf = oracle.sgd(w, g, rate, policy=policy)
+            assert gf == _ofault(rf), (trial, policy, gf, rf)
+            if rf is None:
+                np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+# ---------------------------------------------------------------------- MSE
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("n", [1, 2, 17, 4096, 100_000, 1 << 20])
+def test_mse_parity(ctx, pcu_pkg, dtype, n):
+    rng = np.random.default_rng(n)
+    p = rng.uniform(-1, 1, n).astype(dtype)
+    t = rng.uniform(-1, 1, n).astype(dtype)
+    got = ctx.strict_mse(ctx.upload(p), ctx.upload(t)).numpy()
+    ref, rf = oracle.mse(p, t)
+    assert rf is None
+    assert _bits(got).item() == _bits(ref).item()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_mse_faults_parity(ctx, pcu_pkg, dtype):
+    rng = np.random.default_rng(77)
+    n = 30_000
+    big = np.finfo(dtype).max
+    cases = []
+    p = rng.uniform(-1, 1, n).astype(dtype); t = rng.uniform(-1, 1, n).astype(dtype)
+    p[123] = np.nan; cases.append((p.copy(), t.copy()))
+    p[123] = 0.5; p[50] = big; p[51] = big; cases.append((p.copy(), t.copy()))      # Multiply overflow
+    p[50] = 0.5; p[51] = 0.5
+    p[10:20] = np.sqrt(big) * 0.9; cases.append((p.copy(), t.copy()))             # Add overflow
+    p[10:20] = 0.5
+    p[:] = np.finfo(dtype).tiny * 3; t[:] = 0; cases.append((p.copy(), t.copy()))  # tiny squares
+    p[:] = 0; t[:] = 0; p[0] = np.finfo(dtype).tiny * 2 ** 20; cases.append((p.copy(), t.copy()))
+    for i, (pp, tt) in enumerate(cases):
+        for policy in (0, 1, 2):
+            got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_mse(ctx.upload(pp), ctx.upload(tt), policy).numpy())
+            ref, rf = oracle.mse(pp, tt, policy=policy)
+            assert gf == _ofault(rf), (i, policy, gf, rf)
+            if rf is None:
+                assert _bits(got).item() == _bits(ref).item()
+
+
+# ------------------------------------------------------------------- MatMul
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (2, 3, 2), (65, 3, 17), (128, 128, 128),
+                                   (129, 67, 255), (300, 257, 130), (512, 1024, 256)])
+def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape):
+    m, k, n = shape
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    for tl in (False, True):
+        for tr in (False, True):
+            a = rng.uniform(-1, 1, (k, m) if tl else (m, k)).astype(dtype)
+            b = rng.uniform(-1, 1, (n, k) if tr else (k, n)).astype(dtype)
+            got = ctx.strict_matmul(ctx.upload(a), ctx.upload(b), tl, tr).numpy()
+            ref, rf = oracle.matmul(a, b, tl, tr)
+            assert rf is None
+            np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{shape} {tl} {tr}")
+
+
+def _run_tensor_case(ctx, pcu_pkg, case):
+    dtype = np.float32 if case["dtype"] == "f32" else np.float64
+    itype = np.uint32 if dtype == np.float32 else np.uint64
+    ins = []
+    for s in case["inputs"]:
+        arr = np.array([int(x, 16) for x in s["bits"]], dtype=itype).view(dtype)
+        ins.append(arr.reshape(s["shape"]) if s["shape"] else arr.reshape(1))
+    policy = POLICY[case["policy"]]
+    if case["op"] == "matmul":
+        fn = lambda: ctx.strict_matmul(ctx.upload(ins[0]), ctx.upload(ins[1]), case["params"]["tl"],
+                                       case["params"]["tr"], policy).numpy()
+    elif case["op"] == "sgd":
+        rate = np.array([int(case["params"]["rate"], 16)], dtype=np.uint32).view(np.float32)[0]
+        fn = lambda: ctx.strict_sgd(ctx.upload(ins[0].reshape(-1)), ctx.upload(ins[1].reshape(-1)),
+                                    rate, policy).numpy()
+    else:
+        fn = lambda: ctx.strict_mse(ctx.upload(ins[0].reshape(-1)), ctx.upload(ins[1].reshape(-1)),
+                                    policy).numpy()
+    return fn, itype
+
+
+STEP = {"Multiply": 1, "Add": 2, "Subtract": 3, "Divide": 4}
+KIND = {"ArithmeticOverflow": 3, "ArithmeticUnderflow": 4, "InvalidFloatingOperand": 5}
+
+
+@pytest.mark.parametrize("case", json.load(open(os.path.join(GOLDEN, "tensor_kat.json")))["cases"],
+                         ids=lambda c: f"{c['op']}-{c['dtype']}-{c['source']}")
+def test_reference_tensor_known_answers_on_gpu(ctx, pcu_pkg, case):
+    fn, itype = _run_tensor_case(ctx, pcu_pkg, case)
+    got, gf = _gpu_fault(pcu_pkg, fn)
+    if case["fault"] is not None:
+        e, r, step, kind = case["fault"]
+        assert gf == (e, r, STEP[step], KIND[kind]), (gf, case)
+    else:
+        assert gf is None, (gf, case)
+        assert [int(v) for v in np.asarray(got).reshape(-1).view(itype)] == [int(v, 16) for v in case["output"]]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_fault_variants_parity(ctx, pcu_pkg, dtype):
+    """The C2 fault variants at 256^3: 0.1% of A set to 3.0e38 (Add overflow) and 0.1% of
+    B set to NaN (Multiply invalid at the lowest cell), plus tiny operands (underflow)."""
+    rng = np.random.default_rng(2024)
+    m = k = n = 256
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    huge = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    cnt = int(np.ceil(0.001 * m * k))
+    for variant in range(4):
+        aa, bb = a.copy(), b.copy()
+        if variant == 0:
+            aa.reshape(-1)[rng.choice(m * k, cnt * 8, replace=False)] = huge
+        elif variant == 1:
+            bb.reshape(-1)[rng.choice(k * n, cnt, replace=False)] = np.nan
+        elif variant == 2:
+            aa[100:110, :] *= dtype(np.finfo(dtype).tiny)  # tiny-inexact products in rows 100..109
+        else:
+            bb[:, 7] = np.finfo(dtype).tiny * 0.5  # exact tiny products? rounding decides
+        for policy in (0, 1, 2):
+            got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), False, False, policy).numpy())
+            ref, rf = oracle.matmul(aa, bb, policy=policy)
+            assert gf == _ofault(rf), (variant, policy, gf, rf)
+            if rf is None:
+                np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+# ------------------------------------------------------------------ program
+
+
+def test_program_reports_first_node_and_recovers(ctx, pcu_pkg):
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (64, 32)).astype(np.float32)
+    b = rng.uniform(-1, 1, (32, 48)).astype(np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    bad = b.copy()
+    bad[5, 9] = np.nan
+    dbad = ctx.upload(bad)
+    dnan = ctx.upload(np.array([np.nan], np.float32))
+    # node 0 fine, node 1 faults at (cell 9, k 5), node 2 faults too: node 1 is reported.
+    try:
+        with ctx.program():
+            ctx.strict_matmul(da, db)
+            ctx.strict_matmul(da, dbad)
+            ctx.checked_relu(dnan)
+        raise AssertionError("expected fault")
+    except pcu_pkg.PcuExecutionError as e:
+        f = e.tensor_fault
+        assert (f.node, f.element_index, f.reduction_index, int(f.step), int(f.kind)) == (1, 9, 5, 1, 5)
+    # A fault never poisons the next call (backends/rocm/tensor/strict_matmul/hardware.rs:244-313).
+    got = ctx.strict_matmul(da, db).numpy()
+    ref, _ = oracle.matmul(a, b)
+    np.testing.assert_array_equal(_bits(got), _bits(ref))
+    with ctx.program():
+        x = ctx.strict_matmul(da, db)
+        y = ctx.checked_relu(x)
+    ref2, _ = oracle.relu(ref)
+    np.testing.assert_array_equal(_bits(y.numpy()), _bits(ref2))
