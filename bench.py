@@ -1,0 +1,248 @@
+"""Benchmark of the strict owned-tensor hot path on one MI355X.
+
+Headline (BASELINE.json `metric`): strict F32 MatMul 4096^3, A and B uniform[-1,1]
+(seeded), inputs resident in HBM. One step = one complete strict MatMul call through the C
+ABI: exponent prefilter, main tile kernel, exact-replay check and the terminal fault-word
+readback. `value` is GFLOP/s = 2*M*N*K / step time. The dominant kernel's live duration
+(HIP events on its own stream) gives the roofline; `cpu_baseline` times the faithful
+single-thread CPU port of the reference's integer-law MatMul on a bounded row sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "fusion-pcu_amd")
+
+METRIC = "strict F32 MatMul GFLOP/s @4096³ (% FP32 vector peak); MLP train steps/s"
+FP32_PEAK_TFLOPS = 157.3       # MI355X FP32 vector (= dense FP32 matrix) peak
+FP32_STRICT_CEILING = 39.3     # unpacked v_mul_f32 + v_add_f32: 64 lanes x 2 ops/clk/CU
+FP64_PEAK_TFLOPS = 78.6
+HBM_PEAK_GBS = 8000.0
+
+
+def _package():
+    if "fusion_pcu_amd" in sys.modules:
+        return sys.modules["fusion_pcu_amd"]
+    spec = importlib.util.spec_from_file_location(
+        "fusion_pcu_amd", os.path.join(PKG_DIR, "__init__.py"), submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["fusion_pcu_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
+    from fusion_pcu_amd import synthetic as syn
+    a = syn.uniform(seed_a, (m, k), dtype)
+    b = syn.uniform(seed_b, (k, n), dtype)
+    da, db = ctx.upload(a), ctx.upload(b)
+    dc = ctx.empty((m, n), dtype)
+    for _ in range(warmup):
+        ctx.strict_matmul(da, db, out=dc)
+    ctx.synchronize()
+    ctx.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.strict_matmul(da, db, out=dc)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    gemm_ms, gemm_n = ctx.kernel_time("strict_gemm")
+    pre_ms, _ = ctx.kernel_time("gemm_prefilter")
+    rep_ms, _ = ctx.kernel_time("gemm_replay")
+    ctx.profile(False)
+    for x in (da, db, dc):
+        x.free()
+    ms_step = (t1 - t0) * 1e3 / steps
+    return {
+        "ms_per_step": ms_step,
+        "gflops": 2.0 * m * n * k / (ms_step * 1e-3) / 1e9,
+        "gemm_avg_ms": gemm_ms / max(gemm_n, 1),
+        "gemm_launches": gemm_n,
+        "prefilter_avg_ms": pre_ms / max(gemm_n, 1),
+        "replay_avg_ms": rep_ms / max(gemm_n, 1),
+    }
+
+
+def bench_sgd(pkg, ctx, n, steps, warmup):
+    """C4: strict F32 SGD over 2^28 elements (12 B/elem compulsory traffic)."""
+    from fusion_pcu_amd import synthetic as syn
+    w = syn.normal(41, (n,), 1.0, np.float32)
+    g = syn.normal(42, (n,), 1e-3, np.float32)
+    w[: n // 100] = np.float32(1e-38)
+    dw, dg = ctx.upload(w), ctx.upload(g)
+    del w, g
+    out = ctx.empty((n,), np.float32)
+    for _ in range(warmup):
+        ctx.strict_sgd(dw, dg, 0.01, out=out)
+    ctx.synchronize()
+    ctx.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.strict_sgd(dw, dg, 0.01, out=out)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    k_ms, k_n = ctx.kernel_time("sgd")
+    ctx.profile(False)
+    for x in (dw, dg, out):
+        x.free()
+    avg = k_ms / max(k_n, 1)
+    return {"elements": n, "ms_per_step": (t1 - t0) * 1e3 / steps, "kernel_avg_ms": avg,
+            "kernel_GBps": 12.0 * n / (avg * 1e-3) / 1e9,
+            "kernel_hbm_frac": 12.0 * n / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def cpu_baseline(m, k, n, rows):
+    """Faithful port (integer-significand law, one thread) on `rows` output rows."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    from fusion_pcu_amd import synthetic as syn
+    a = syn.uniform(11, (m, k), np.float32)
+    b = syn.uniform(12, (k, n), np.float32)
+    t0 = time.perf_counter()
+    _, fault = oracle.matmul(a, b, rows_subset=(0, rows), fast=False)
+    dt = time.perf_counter() - t0
+    assert fault is None
+    return {
+        "value": 2.0 * rows * n * k / dt / 1e9,
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"output rows 0..{rows - 1} of the strict F32 MatMul {m}x{k}x{n} "
+                  f"({rows * n} cells, {rows * n * k} ordered multiply/add pairs) with the "
+                  f"faithful single-thread integer-law port of the reference CPU backend; "
+                  f"{dt:.1f} s",
+    }
+
+
+def probe(pkg, M, K, N) -> int:
+    """One launch of each kernel whose HBM traffic is measured with rocprofv3 --pmc:
+    the strict F32 MatMul 4096^3, a copy-like calibration kernel (checked Add of +0 over
+    2^26 f32: 256 MiB read + 256 MiB written) and strict SGD over 2^26 f32."""
+    from fusion_pcu_amd import synthetic as syn
+    n = 1 << 26
+    with pkg.Context(0) as ctx:
+        da = ctx.upload(syn.uniform(11, (M, K), np.float32))
+        db = ctx.upload(syn.uniform(12, (K, N), np.float32))
+        dc = ctx.empty((M, N), np.float32)
+        x = ctx.upload(syn.uniform(21, (n,), np.float32))
+        g = ctx.upload(syn.uniform(22, (n,), np.float32))
+        y = ctx.empty((n,), np.float32)
+        log("probe: warmup")
+        ctx.strict_matmul(da, db, out=dc)
+        ctx.checked_binary(0, x, 0.0, out=y)
+        ctx.strict_sgd(x, g, 0.01, out=y)
+        log("probe: one launch each")
+        ctx.strict_matmul(da, db, out=dc)
+        ctx.checked_binary(0, x, 0.0, out=y)
+        ctx.strict_sgd(x, g, 0.01, out=y)
+        ctx.synchronize()
+    log("probe: done")
+    return 0
+
+
+def _traffic(workload: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as fh:
+            return json.load(fh).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=12)
+    ap.add_argument("--probe", action="store_true",
+                    help="run each profiled kernel once (for rocprofv3 --pmc passes) and exit")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the strict path has no multi-GPU leg in this "
+              f"build (requested --gpus {args.gpus})", file=sys.stderr)
+        return 2
+
+    pkg = _package()
+    M = N = K = 4096
+    if args.probe:
+        return probe(pkg, M, K, N)
+    with pkg.Context(0) as ctx:
+        log("strict F32 MatMul 4096^3")
+        mm = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup)
+        extra = {}
+        if not args.no_extra:
+            log("strict F64 MatMul 4096^3 (C3 shape)")
+            f64 = bench_matmul(pkg, ctx, M, K, N, np.float64, max(2, args.steps // 3), 1, 31, 32)
+            extra["f64_matmul_4096"] = {
+                "gflops": f64["gflops"], "gemm_avg_ms": f64["gemm_avg_ms"],
+                "gemm_tflops": 2.0 * M * N * K / (f64["gemm_avg_ms"] * 1e-3) / 1e12,
+                "frac_fp64_vector_peak": 2.0 * M * N * K / (f64["gemm_avg_ms"] * 1e-3) / 1e12 / FP64_PEAK_TFLOPS,
+            }
+            log("strict F32 SGD 2^28 (C4 shape)")
+            extra["sgd_f32_2p28"] = bench_sgd(pkg, ctx, 1 << 28, max(5, args.steps), 2)
+
+    gemm_s = mm["gemm_avg_ms"] * 1e-3
+    achieved = 2.0 * M * N * K / gemm_s / 1e12
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(achieved, 3),
+        "peak": FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+        "traffic": _traffic("strict_gemm_f32_4096"),
+        "kernel": "k_strict_gemm<float> (main tile kernel)",
+        "kernel_avg_ms": round(mm["gemm_avg_ms"], 4),
+        "algorithmic_flops_per_launch": 2 * M * N * K,
+        "strict_valu_ceiling_tflops": FP32_STRICT_CEILING,
+        "frac_of_strict_ceiling": round(achieved / FP32_STRICT_CEILING, 4),
+    }
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline: faithful port on {args.cpu_rows} rows")
+        cpu = cpu_baseline(M, K, N, args.cpu_rows)
+    line = {
+        "metric": METRIC,
+        "value": round(mm["gflops"], 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mm["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (SplitMix64 uniform[-1,1], seeds 11/12)",
+        "config": {"workload": "strict F32 MatMul 4096x4096x4096 (A,B uniform[-1,1]); one step = "
+                               "prefilter + tile kernel + replay check + fault readback",
+                   "m": M, "k": K, "n": N},
+        "pct_fp32_vector_peak": round(100.0 * mm["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

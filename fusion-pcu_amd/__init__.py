@@ -251,6 +251,18 @@ class Context:
         self.check(self._lib.pcu_elapsed_ms(self.handle, a, b, ctypes.byref(ms)))
         return float(ms.value)
 
+    def profile(self, on: bool = True) -> None:
+        """Start (and reset) or stop per-kernel HIP-event timing."""
+        self.check(self._lib.pcu_profile_enable(self.handle, int(on)))
+
+    def kernel_time(self, kernel: str) -> Tuple[float, int]:
+        """(total milliseconds, launches) of one kernel since profile(True)."""
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        self.check(self._lib.pcu_profile_read(self.handle, _abi.KERNEL_IDS[kernel],
+                                              ctypes.byref(ms), ctypes.byref(n)))
+        return float(ms.value), int(n.value)
+
     # ------------------------------------------------------------------- ops
     def _call(self, fn, *args) -> None:
         f = _abi.Fault()

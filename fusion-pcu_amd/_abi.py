@@ -76,6 +76,64 @@ SIGNATURES = {
     "pcu_program_next_node": (_u32, [_vp]),
     "pcu_mark": (_i32, [_vp, _i32]),
     "pcu_elapsed_ms": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_float)]),
+    "pcu_profile_enable": (_i32, [_vp, _i32]),
+    "pcu_profile_read": (_i32, [_vp, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]),
+}
+
+
+class NodeDesc(ctypes.Structure):
+    _fields_ = [
+        ("op", ctypes.c_uint32),
+        ("left", ctypes.c_uint32),
+        ("right", ctypes.c_uint32),
+        ("transpose_left", ctypes.c_uint32),
+        ("transpose_right", ctypes.c_uint32),
+        ("dtype", ctypes.c_uint32),
+        ("numerical_mode", ctypes.c_int32),
+        ("underflow_policy", ctypes.c_int32),
+        ("learning_rate", ctypes.c_float),
+        ("rank", ctypes.c_uint32),
+        ("value_bits", ctypes.c_uint64),
+        ("shape", ctypes.c_uint64 * 8),
+    ]
+
+
+_U32P = ctypes.POINTER(ctypes.c_uint32)
+_U64P = ctypes.POINTER(ctypes.c_uint64)
+SIGNATURES.update({
+    "pcu_graph_create": (_i32, [_VPP]),
+    "pcu_graph_destroy": (None, [_vp]),
+    "pcu_graph_set_numerical_mode": (_i32, [_vp, _i32]),
+    "pcu_graph_input": (_i32, [_vp, _i32, _u32, _U64P, _U32P]),
+    "pcu_graph_uniform": (_i32, [_vp, _i32, _u32, _U64P, _u64, _U32P]),
+    "pcu_graph_binary": (_i32, [_vp, _i32, _u32, _u32, _U32P]),
+    "pcu_graph_relu": (_i32, [_vp, _u32, _U32P]),
+    "pcu_graph_relu_backward": (_i32, [_vp, _u32, _u32, _U32P]),
+    "pcu_graph_matmul": (_i32, [_vp, _u32, _u32, _i32, _i32, _U32P]),
+    "pcu_graph_mean_squared_error": (_i32, [_vp, _u32, _u32, _U32P]),
+    "pcu_graph_sgd_update": (_i32, [_vp, _u32, _u32, _f32, _U32P]),
+    "pcu_graph_set_underflow_policy": (_i32, [_vp, _u32, _i32]),
+    "pcu_graph_set_value_numerical_mode": (_i32, [_vp, _u32, _i32]),
+    "pcu_graph_backward_mse": (_i32, [_vp, _u32, _U32P, _u32]),
+    "pcu_graph_backward_mse_for_targets": (_i32, [_vp, _u32, _u32, _U32P, _U32P]),
+    "pcu_graph_node_count": (_u32, [_vp]),
+    "pcu_graph_describe": (_i32, [_vp, _u32, ctypes.POINTER(NodeDesc)]),
+    "pcu_graph_plan": (_i32, [_vp, _u32, _U32P, _U32P, _U32P]),
+    "pcu_prepare": (_i32, [_vp, _vp, _u32, _U32P, _VPP]),
+    "pcu_prepared_destroy": (None, [_vp]),
+    "pcu_prepared_input_count": (_u32, [_vp]),
+    "pcu_prepared_input_id": (_i32, [_vp, _u32, _U32P]),
+    "pcu_prepared_execute": (_i32, [_vp, _u32, ctypes.POINTER(ctypes.c_void_p), _FP]),
+    "pcu_prepared_output": (_vp, [_vp, _u32]),
+    "pcu_prepared_take_output": (_i32, [_vp, _u32, _VPP]),
+})
+
+GRAPH_OPS = ["Input", "Uniform", "Add", "Sub", "Mul", "Div", "SgdUpdate", "MatMul", "Relu",
+             "ReluBackward", "MeanSquaredError"]
+
+KERNEL_IDS = {
+    "strict_gemm": 0, "gemm_prefilter": 1, "gemm_replay": 2, "sgd": 3, "binary": 4,
+    "relu": 5, "relu_backward": 6, "add_relu": 7, "mse": 8,
 }
 
 _lib = None

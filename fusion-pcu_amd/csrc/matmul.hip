@@ -417,7 +417,8 @@ template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault,
-                                  const unsigned long long *prior, unsigned n_prior)
+                                  const unsigned long long *prior, unsigned n_prior,
+                                  hipEvent_t *ev)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -428,6 +429,8 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const bool f32 = sizeof(T) == 4;
     int risk = policy != kPolicyAllowGradual;
     int thr = policy == kPolicyRejectSubnormal ? (f32 ? -103 : -970) : (f32 ? -126 : -1022);
+    if (ev)
+        (void)hipEventRecord(ev[0], s);
     if (risk && K > 0) {
         exp_min<T>(s, A, ta ? K : M, ta ? M : K, !ta, sc.row_exp);
         exp_min<T>(s, B, tb ? N : K, tb ? K : N, tb, sc.col_exp);
@@ -437,6 +440,8 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);
     dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)));
     const int m = (int)M, n = (int)N, k = (int)K;
+    if (ev)
+        (void)hipEventRecord(ev[1], s);
     if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
     else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
     else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
@@ -444,9 +449,13 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
+    if (ev)
+        (void)hipEventRecord(ev[2], s);
     hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(1024), dim3(256), 0, s, A, B, (const T *)C, M, N, K,
                        (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, risk, policy,
                        (const unsigned long long *)sc.suspect, fault, prior, n_prior);
+    if (ev)
+        (void)hipEventRecord(ev[3], s);
     return hipGetLastError();
 }
 
@@ -454,17 +463,18 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault,
-                                const unsigned long long *prior, unsigned n_prior)
+                                const unsigned long long *prior, unsigned n_prior,
+                                hipEvent_t *ev)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (dtype == 0)
         return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                       (const float *)a, (const float *)b, (float *)c, policy,
-                                      scratch, fault, prior, n_prior);
+                                      scratch, fault, prior, n_prior, ev);
     return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                    (const double *)a, (const double *)b, (double *)c, policy,
-                                   scratch, fault, prior, n_prior);
+                                   scratch, fault, prior, n_prior, ev);
 }
 
 } // namespace pcu

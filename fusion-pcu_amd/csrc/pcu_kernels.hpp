@@ -40,11 +40,14 @@ MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
 // `prior`/`n_prior` are the fault words of the ops enqueued before this one: the exact
 // replay skips its work once one of them holds a fault (that earlier fault is reported).
+// `ev` (optional, 4 events) is recorded before the prefilter, before and after the main
+// kernel, and after the replay.
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault,
-                                const unsigned long long *prior, unsigned n_prior);
+                                const unsigned long long *prior, unsigned n_prior,
+                                hipEvent_t *ev = nullptr);
 
 // Small device utilities (fill kernels rather than memsets, so a captured graph replays
 // them as kernels).

@@ -45,6 +45,22 @@ struct Ctx {
     std::vector<NodeInfo> nodes;
     std::string error;
 
+    // Per-kernel device timing (pcu_profile_*): event pairs resolved on read.
+    struct Timing {
+        int kernel;
+        hipEvent_t a, b;
+    };
+    bool profiling = false;
+    std::vector<Timing> timings;
+    std::vector<hipEvent_t> event_pool;
+    double prof_ms[PCU_KERNEL_COUNT] = {};
+    uint64_t prof_n[PCU_KERNEL_COUNT] = {};
+    hipEvent_t take_event();
+    // Records the opening event of a timed region on `s` (nullptr when not profiling).
+    hipEvent_t timer_start(hipStream_t s);
+    void timer_stop(int kernel, hipEvent_t start, hipStream_t s);
+    pcu_status resolve_timings();
+
     Ctx() = default;
     Ctx(const Ctx &) = delete;
     Ctx &operator=(const Ctx &) = delete;
@@ -62,6 +78,8 @@ struct Ctx {
 
     pcu_status begin_program(bool implicit);
     pcu_status end_program(pcu_fault *first);
+    // Every faulted node in node order (empty when none).
+    pcu_status end_program_all(std::vector<pcu_fault> *faults);
     pcu_status add_node(NodeInfo info, unsigned long long **word);
     pcu_status start_op();
     pcu_status finish_op(pcu_status launched, pcu_fault *fault);

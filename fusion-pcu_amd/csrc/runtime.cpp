@@ -112,6 +112,12 @@ Ctx::~Ctx()
     for (auto &e : marks)
         if (e)
             (void)hipEventDestroy(e);
+    for (auto &t : timings) {
+        (void)hipEventDestroy(t.a);
+        (void)hipEventDestroy(t.b);
+    }
+    for (auto &e : event_pool)
+        (void)hipEventDestroy(e);
     if (side_done)
         (void)hipEventDestroy(side_done);
     if (main_ready)
@@ -317,8 +323,9 @@ static bool decode_word(const NodeInfo &n, uint64_t word, pcu_fault *f)
     return false;
 }
 
-pcu_status Ctx::end_program(pcu_fault *first)
+pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
 {
+    faults->clear();
     if (!in_program) {
         fail("no program open");
         return PCU_ERR_STATE;
@@ -346,11 +353,22 @@ pcu_status Ctx::end_program(pcu_fault *first)
             return PCU_ERR_PROTOCOL;
         }
         f.node = (uint32_t)i;
-        if (first)
-            *first = f;
-        return PCU_ARITHMETIC_FAULT;
+        faults->push_back(f);
     }
     return PCU_OK;
+}
+
+pcu_status Ctx::end_program(pcu_fault *first)
+{
+    std::vector<pcu_fault> faults;
+    pcu_status st = end_program_all(&faults);
+    if (st)
+        return st;
+    if (faults.empty())
+        return PCU_OK;
+    if (first)
+        *first = faults.front();
+    return PCU_ARITHMETIC_FAULT;
 }
 
 pcu_status Ctx::finish_op(pcu_status launched, pcu_fault *fault)
@@ -380,6 +398,62 @@ pcu_status Ctx::scratch(size_t bytes, hipStream_t s, void **out)
     return hip(hipMallocFromPoolAsync(out, bytes ? bytes : 1, pool, s), "hipMallocFromPoolAsync");
 }
 
+// ------------------------------------------------------------------ timing
+
+hipEvent_t Ctx::take_event()
+{
+    if (!event_pool.empty()) {
+        hipEvent_t e = event_pool.back();
+        event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+hipEvent_t Ctx::timer_start(hipStream_t s)
+{
+    if (!profiling)
+        return nullptr;
+    hipEvent_t e = take_event();
+    if (e)
+        (void)hipEventRecord(e, s);
+    return e;
+}
+
+void Ctx::timer_stop(int kernel, hipEvent_t start, hipStream_t s)
+{
+    if (!start)
+        return;
+    hipEvent_t e = take_event();
+    if (!e)
+        return;
+    (void)hipEventRecord(e, s);
+    timings.push_back({kernel, start, e});
+}
+
+pcu_status Ctx::resolve_timings()
+{
+    pcu_status st = join_side();
+    if (st)
+        return st;
+    if ((st = hip(hipStreamSynchronize(stream), "hipStreamSynchronize")))
+        return st;
+    for (const Timing &t : timings) {
+        float ms = 0.0f;
+        if ((st = hip(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime")))
+            return st;
+        prof_ms[t.kernel] += ms;
+        prof_n[t.kernel] += 1;
+        event_pool.push_back(t.a);
+        event_pool.push_back(t.b);
+    }
+    timings.clear();
+    return PCU_OK;
+}
+
 // ---------------------------------------------------------------------- ops
 
 static bool valid_dtype(int d) { return d == PCU_F32 || d == PCU_F64; }
@@ -406,10 +480,20 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         return st;
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
     unsigned prior = (unsigned)(word - fault_words);
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (profiling)
+        for (auto &x : ev)
+            x = take_event();
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
-                                        b, c, policy, s, word, fault_words, prior);
+                                        b, c, policy, s, word, fault_words, prior,
+                                        profiling ? ev : nullptr);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
+    if (profiling) {
+        timings.push_back({PCU_KERNEL_GEMM_PREFILTER, ev[0], ev[1]});
+        timings.push_back({PCU_KERNEL_STRICT_GEMM, ev[1], ev[2]});
+        timings.push_back({PCU_KERNEL_GEMM_REPLAY, ev[2], ev[3]});
+    }
     return hip(hipFreeAsync(sc, stream), "hipFreeAsync");
 }
 
@@ -425,7 +509,10 @@ pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const vo
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
         return st;
-    return hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word), "checked_binary launch");
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word), "checked_binary launch");
+    timer_stop(PCU_KERNEL_BINARY, t, stream);
+    return st;
 }
 
 pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int policy)
@@ -438,7 +525,10 @@ pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int pol
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
         return st;
-    return hip(launch_relu(stream, dtype, n, x, out, policy, word), "checked_relu launch");
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_relu(stream, dtype, n, x, out, policy, word), "checked_relu launch");
+    timer_stop(PCU_KERNEL_RELU, t, stream);
+    return st;
 }
 
 pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const void *up, void *out,
@@ -452,8 +542,11 @@ pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const voi
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
         return st;
-    return hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word),
-               "checked_relu_backward launch");
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word),
+             "checked_relu_backward launch");
+    timer_stop(PCU_KERNEL_RELU_BACKWARD, t, stream);
+    return st;
 }
 
 pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
@@ -469,8 +562,11 @@ pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
         return st;
     if ((st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &w_relu)))
         return st;
-    return hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu),
-               "checked_add_relu launch");
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu),
+             "checked_add_relu launch");
+    timer_stop(PCU_KERNEL_ADD_RELU, t, stream);
+    return st;
 }
 
 // The F64 rate is the exact widening of the F32 literal (reference.rs:507-514); a float
@@ -492,7 +588,10 @@ pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, floa
     pcu_status st = add_node(NodeInfo{Prim::Sgd, n, 0}, &word);
     if (st)
         return st;
-    return hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word), "strict_sgd launch");
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word), "strict_sgd launch");
+    timer_stop(PCU_KERNEL_SGD, t, stream);
+    return st;
 }
 
 // Element count rounded to nearest even (core/dialect/tensor/constants/constants.rs:18-28).
@@ -550,9 +649,11 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     void *sq = nullptr;
     if ((st = scratch(n * dsize(dtype), s, &sq)))
         return st;
+    hipEvent_t t0 = timer_start(s);
     if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word),
                   "strict_mse launch")))
         return st;
+    timer_stop(PCU_KERNEL_MSE, t0, s);
     return hip(hipFreeAsync(sq, s), "hipFreeAsync");
 }
 
@@ -761,6 +862,43 @@ pcu_status pcu_program_end(pcu_ctx *ctx, pcu_fault *first_fault)
 uint32_t pcu_program_next_node(const pcu_ctx *ctx)
 {
     return ctx ? (uint32_t)reinterpret_cast<const Ctx *>(ctx)->nodes.size() : 0;
+}
+
+pcu_status pcu_profile_enable(pcu_ctx *ctx, int on)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    pcu_status st = c->resolve_timings();
+    if (st)
+        return st;
+    for (int i = 0; i < PCU_KERNEL_COUNT; i++) {
+        c->prof_ms[i] = 0.0;
+        c->prof_n[i] = 0;
+    }
+    c->profiling = on != 0;
+    return PCU_OK;
+}
+
+pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t *launches)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (kernel < 0 || kernel >= PCU_KERNEL_COUNT || !total_ms || !launches) {
+        c->fail("profile read: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (c->in_program) {
+        c->fail("profile read inside a program");
+        return PCU_ERR_STATE;
+    }
+    pcu_status st = c->resolve_timings();
+    if (st)
+        return st;
+    *total_ms = c->prof_ms[kernel];
+    *launches = c->prof_n[kernel];
+    return PCU_OK;
 }
 
 pcu_status pcu_mark(pcu_ctx *ctx, int slot)

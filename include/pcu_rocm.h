@@ -175,6 +175,124 @@ uint32_t pcu_program_next_node(const pcu_ctx *ctx);
 pcu_status pcu_mark(pcu_ctx *ctx, int slot);
 pcu_status pcu_elapsed_ms(pcu_ctx *ctx, int from_slot, int to_slot, float *ms);
 
+/* Per-kernel device time: while enabled, every launch of the kernels below is bracketed
+ * by HIP events on the stream it runs on; pcu_profile_read synchronizes and returns the
+ * accumulated milliseconds and launch count since pcu_profile_enable. No counterpart in
+ * the reference (its per-node timing is host-side: backends/rocm/tensor.rs:1969-2020). */
+typedef enum pcu_kernel_id {
+    PCU_KERNEL_STRICT_GEMM = 0,     /* main strict MatMul tile kernel */
+    PCU_KERNEL_GEMM_PREFILTER = 1,  /* exponent prefilter (both operands) */
+    PCU_KERNEL_GEMM_REPLAY = 2,     /* exact replay of suspect cells */
+    PCU_KERNEL_SGD = 3,
+    PCU_KERNEL_BINARY = 4,
+    PCU_KERNEL_RELU = 5,
+    PCU_KERNEL_RELU_BACKWARD = 6,
+    PCU_KERNEL_ADD_RELU = 7,
+    PCU_KERNEL_MSE = 8,             /* squares + ordered sum + divide */
+    PCU_KERNEL_COUNT = 9
+} pcu_kernel_id;
+pcu_status pcu_profile_enable(pcu_ctx *ctx, int on);
+pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t *launches);
+
+/* -------------------------------------------------------------------- graph
+ * Host mirror of the reference's tensor Graph for the strict path: the builder calls
+ * (core/dialect/tensor.rs:4028-4329), reverse mode for an MSE root
+ * (core/dialect/tensor/gradients/gradients.rs:31-474), the execution plan
+ * (tensor.rs:3234-3300) and a prepared executor (backends/rocm/tensor.rs:5827-6015).
+ * Values are node indices in append order. Errors: PCU_ERR_ARGUMENT for UnknownValue and
+ * invalid rates, PCU_ERR_SHAPE for ShapeMismatch/MatMulShape/ScalarTypeMismatch,
+ * PCU_ERR_UNSUPPORTED for unsupported derivatives or Boundary compounds at prepare. */
+typedef struct pcu_graph pcu_graph;
+typedef struct pcu_prepared pcu_prepared;
+
+/* Op codes of pcu_node_desc.op. */
+typedef enum pcu_graph_op {
+    PCU_GRAPH_INPUT = 0,
+    PCU_GRAPH_UNIFORM = 1,
+    PCU_GRAPH_ADD = 2,
+    PCU_GRAPH_SUB = 3,
+    PCU_GRAPH_MUL = 4,
+    PCU_GRAPH_DIV = 5,
+    PCU_GRAPH_SGD_UPDATE = 6,
+    PCU_GRAPH_MATMUL = 7,
+    PCU_GRAPH_RELU = 8,
+    PCU_GRAPH_RELU_BACKWARD = 9,
+    PCU_GRAPH_MEAN_SQUARED_ERROR = 10
+} pcu_graph_op;
+
+/* NodeDescriptor (core/dialect/tensor.rs:3575-3586). numerical_mode: -1 none,
+ * 0 Boundary, 1 Strict; underflow_policy: -1 none, else pcu_underflow. Operands are
+ * UINT32_MAX when absent. */
+typedef struct pcu_node_desc {
+    uint32_t op;
+    uint32_t left, right;
+    uint32_t transpose_left, transpose_right;
+    uint32_t dtype;
+    int32_t numerical_mode;
+    int32_t underflow_policy;
+    float learning_rate;
+    uint32_t rank;
+    uint64_t value_bits;
+    uint64_t shape[8];
+} pcu_node_desc;
+
+pcu_status pcu_graph_create(pcu_graph **out);
+void pcu_graph_destroy(pcu_graph *graph);
+/* Graph::set_numerical_mode: compound nodes appended afterwards take this mode. */
+pcu_status pcu_graph_set_numerical_mode(pcu_graph *graph, int strict);
+pcu_status pcu_graph_input(pcu_graph *graph, pcu_dtype dtype, uint32_t rank, const uint64_t *shape,
+                           uint32_t *id);
+/* A dense logical tensor filled with one value (its bit pattern), never materialized
+ * unless a consumer needs it dense. */
+pcu_status pcu_graph_uniform(pcu_graph *graph, pcu_dtype dtype, uint32_t rank,
+                             const uint64_t *shape, uint64_t value_bits, uint32_t *id);
+pcu_status pcu_graph_binary(pcu_graph *graph, pcu_binary_op op, uint32_t left, uint32_t right,
+                            uint32_t *id);
+pcu_status pcu_graph_relu(pcu_graph *graph, uint32_t input, uint32_t *id);
+pcu_status pcu_graph_relu_backward(pcu_graph *graph, uint32_t input, uint32_t upstream,
+                                   uint32_t *id);
+pcu_status pcu_graph_matmul(pcu_graph *graph, uint32_t left, uint32_t right, int transpose_left,
+                            int transpose_right, uint32_t *id);
+pcu_status pcu_graph_mean_squared_error(pcu_graph *graph, uint32_t prediction, uint32_t target,
+                                        uint32_t *id);
+pcu_status pcu_graph_sgd_update(pcu_graph *graph, uint32_t weights, uint32_t gradient,
+                                float learning_rate, uint32_t *id);
+/* Graph::set_value_float_underflow_policy / set_value_numerical_mode. */
+pcu_status pcu_graph_set_underflow_policy(pcu_graph *graph, uint32_t id, pcu_underflow policy);
+pcu_status pcu_graph_set_value_numerical_mode(pcu_graph *graph, uint32_t id, int strict);
+/* Graph::backward_mse: grads[i] is the derivative value of node i (UINT32_MAX if none)
+ * for every node that existed before the call; capacity >= node count. */
+pcu_status pcu_graph_backward_mse(pcu_graph *graph, uint32_t loss, uint32_t *grads,
+                                  uint32_t capacity);
+/* Graph::backward_mse_for_targets (backward_mse_for is the one-target case). */
+pcu_status pcu_graph_backward_mse_for_targets(pcu_graph *graph, uint32_t loss, uint32_t n_targets,
+                                              const uint32_t *targets, uint32_t *grads);
+uint32_t pcu_graph_node_count(const pcu_graph *graph);
+pcu_status pcu_graph_describe(const pcu_graph *graph, uint32_t id, pcu_node_desc *out);
+/* execution_plan_for_outputs: node ids in execution order (order may be NULL to query the
+ * length; *order_len is its capacity on entry and the plan length on return). */
+pcu_status pcu_graph_plan(const pcu_graph *graph, uint32_t n_outputs, const uint32_t *outputs,
+                          uint32_t *order, uint32_t *order_len);
+
+/* Prepare once (plan, fusion of single-use Add->ReLU, device storage with two banks per
+ * output), execute many times. Inputs are device pointers in the order of the graph's Input
+ * nodes that the plan uses (pcu_prepared_input_id). An execution that faults publishes
+ * nothing and returns the first fault with `node` = its graph node id; the previous
+ * outputs stay published, so a resident weight fed back as an input is never lost. */
+pcu_status pcu_prepare(pcu_ctx *ctx, const pcu_graph *graph, uint32_t n_outputs,
+                       const uint32_t *outputs, pcu_prepared **out);
+void pcu_prepared_destroy(pcu_prepared *prepared);
+uint32_t pcu_prepared_input_count(const pcu_prepared *prepared);
+pcu_status pcu_prepared_input_id(const pcu_prepared *prepared, uint32_t index, uint32_t *id);
+pcu_status pcu_prepared_execute(pcu_prepared *prepared, uint32_t n_inputs,
+                                const void *const *device_inputs, pcu_fault *fault);
+/* Device pointer of published output `index` (NULL before the first success). */
+const void *pcu_prepared_output(const pcu_prepared *prepared, uint32_t index);
+/* Moves published output `index` to the caller, who frees it with pcu_buf_free; the
+ * program takes a fresh pool buffer for that slot. This is how a call returns fresh
+ * owners (fusion-pcu/global/arguments.rs:636-660) without a device copy. */
+pcu_status pcu_prepared_take_output(pcu_prepared *prepared, uint32_t index, void **device_ptr);
+
 #ifdef __cplusplus
 }
 #endif

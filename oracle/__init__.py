@@ -264,3 +264,6 @@ def matmul(a: np.ndarray, b: np.ndarray, tl=False, tr=False, policy=POLICY_IEEE,
 
 def host_flushes_denormals() -> bool:
     return bool(lib().orc_host_flushes_denormals())
+
+
+from .graph import graph_c1_step  # noqa: E402  (graph.py imports the ops above)

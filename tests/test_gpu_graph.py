@@ -1,0 +1,200 @@
+"""GPU parity of the prepared-graph path (the reference facade's capture + call) against
+the oracle's graph restatement: the C1 training loop with resident weights, the
+reference's own end-to-end known answers, transactional faults and small MLPs."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import graph as og
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def G(pcu_pkg):
+    from fusion_pcu_amd import graph
+    graph.configure(0)
+    return graph
+
+
+def _bits(a):
+    a = np.asarray(a)
+    return a.view(np.uint32 if a.dtype == np.float32 else np.uint64)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_c1_ten_steps_resident_weights(G, dtype):
+    """C1: X 64x128, W 128x64, b 64x64, Y 64x64 uniform[-1,1] (seeds 1..4), lr 0.01, 10
+    strict steps with W and b resident between calls; every step bit-exact."""
+    from fusion_pcu_amd import synthetic as syn
+    x = syn.uniform(1, (64, 128), dtype)
+    w = syn.uniform(2, (128, 64), dtype)
+    b = syn.uniform(3, (64, 64), dtype)
+    y = syn.uniform(4, (64, 64), dtype)
+    step = G.c1_training_step(0.01)
+    w_dev, b_dev = w, b
+    w_ref, b_ref = w, b
+    for it in range(10):
+        w_dev, b_dev, loss = step(x, w_dev, b_dev, y)   # device owners fed back
+        ref = oracle.graph_c1_step(x, w_ref, b_ref, y, 0.01)
+        assert ref["fault"] is None
+        w_ref, b_ref = ref["weights"], ref["bias"]
+        assert _bits(loss.numpy()).item() == _bits(ref["loss"]).item(), it
+        np.testing.assert_array_equal(_bits(w_dev.numpy()), _bits(w_ref), err_msg=f"step {it}")
+        np.testing.assert_array_equal(_bits(b_dev.numpy()), _bits(b_ref), err_msg=f"step {it}")
+    assert isinstance(w_dev, G.PcuTensor)
+
+
+def test_readme_known_answer(G):
+    """README.md:95-180: update (SGD 0.5) -> linear (strict matmul + bias) -> activate
+    (ReLU) gives [[0, 4], [3, 0]]."""
+
+    @G.function(strict=True)
+    def update(weights, gradients):
+        return G.sgd_update(weights, gradients, 0.5)
+
+    @G.function(strict=True)
+    def linear(inp, weights, bias):
+        return G.matmul(inp, weights) + bias
+
+    @G.function()
+    def activate(inp):
+        return G.relu(inp)
+
+    inp = np.array([[1.0, 2.0, 3.0], [-1.0, 0.0, 2.0]], np.float32)
+    weights = np.array([[1.0, -2.0], [0.0, 1.0], [2.0, 1.0]], np.float32)
+    grads = np.array([[2.0, -2.0], [0.0, 2.0], [2.0, 0.0]], np.float32)
+    bias = np.array([[-8.0, 2.0], [1.0, -5.0]], np.float32)
+    trained = update(weights, grads)
+    result = activate(linear(inp, trained, bias))
+    matrix = np.zeros((2, 2), np.float32)
+    result.read_into(matrix)
+    assert matrix.tolist() == [[0.0, 4.0], [3.0, 0.0]]
+
+
+def test_checked_training_example_known_answer(G):
+    """fusion-pcu/examples/checked-training/checked-training.rs:11-79: loss 0.5 and
+    weights [2, -1] -> [1.5, -1.0] after one step with rate 0.5."""
+
+    @G.function(strict=True)
+    def loss_fn(inp, weights, target):
+        return G.mean_squared_error(G.relu(G.matmul(inp, weights)), target)
+
+    @G.function(strict=True)
+    def training_step(inp, weights, target):
+        pre = G.matmul(inp, weights)
+        pred = G.relu(pre)
+        loss = G.mean_squared_error(pred, target)
+        grad = G.gradient(loss, weights)
+        return G.sgd_update(weights, grad, 0.5)
+
+    inp = np.array([[1.0, 0.0], [0.0, 1.0]], np.float32)
+    target = np.array([[1.0], [0.0]], np.float32)
+    weights = G.PcuTensor.from_numpy(np.array([[2.0], [-1.0]], np.float32))
+    before = loss_fn(inp, weights, target).numpy()
+    updated = training_step(inp, weights, target).numpy()
+    assert _bits(before).item() == _bits(np.float32(0.5)).item()
+    assert _bits(updated).reshape(-1).tolist() == _bits(np.array([1.5, -1.0], np.float32)).tolist()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_cpu_prepared_training_and_transactional_fault(G, pcu_pkg, dtype):
+    """backends/cpu/tests/prepared_tensor/prepared_tensor.rs:25-108: all-target backward,
+    outputs (loss, weight gradient, updated weights); a NaN input faults and leaves the
+    published outputs untouched; the next call succeeds."""
+    g = G.Graph()
+    g.set_numerical_mode(True)
+    inp = g.input((2, 2), dtype)
+    wts = g.input((2, 2), dtype)
+    tgt = g.input((2, 2), dtype)
+    pred = g.relu(g.matmul(inp, wts))
+    loss = g.mean_squared_error(pred, tgt)
+    grads = g.backward_mse(loss)
+    wg = grads[wts]
+    upd = g.sgd_update(wts, wg, 0.125)
+    outs = [loss, wg, upd]
+    ctx = G.default_context()
+    prep = g.prepare(ctx, outs)
+    x = np.array([1.0, -2.0, 3.0, 4.0], dtype).reshape(2, 2)
+    w = np.array([0.5, -0.25, 1.0, 0.75], dtype).reshape(2, 2)
+    y = np.array([0.0, 1.0, 2.0, -1.0], dtype).reshape(2, 2)
+    ref_g = og.Graph()
+    ref_g.mode = "Strict"
+    ri, rw, rt = ref_g.input((2, 2), dtype), ref_g.input((2, 2), dtype), ref_g.input((2, 2), dtype)
+    rl = ref_g.mean_squared_error(ref_g.relu(ref_g.matmul(ri, rw)), rt)
+    rgrads = ref_g.backward_mse(rl)
+    rupd = ref_g.sgd_update(rw, rgrads[rw], 0.125)
+    vals, fault = ref_g.evaluate({ri: x, rw: w, rt: y}, [rl, rgrads[rw], rupd])
+    assert fault is None
+    dx, dw, dy = ctx.upload(x), ctx.upload(w), ctx.upload(y)
+    by_id = {inp: dx.ptr, wts: dw.ptr, tgt: dy.ptr}
+    prep.execute([by_id[i] for i in prep.input_ids])
+    got = [pcu_pkg.DeviceArray(ctx, prep.output_ptr(k), d["shape"], d["dtype"]).numpy()
+           for k, d in enumerate(prep.output_desc)]
+    for have, want in zip(got, [vals[rl], vals[rgrads[rw]], vals[rupd]]):
+        np.testing.assert_array_equal(_bits(have), _bits(want))
+    published = [prep.output_ptr(k) for k in range(3)]
+    bad = x.copy()
+    bad[0, 0] = np.nan
+    dbad = ctx.upload(bad)
+    by_id[inp] = dbad.ptr
+    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+        prep.execute([by_id[i] for i in prep.input_ids])
+    _, rfault = ref_g.evaluate({ri: bad, rw: w, rt: y}, [rl, rgrads[rw], rupd])
+    tf = exc.value.tensor_fault
+    assert (tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+        (rfault.fault.element_index, rfault.fault.reduction_index, rfault.fault.step, rfault.fault.kind)
+    assert [prep.output_ptr(k) for k in range(3)] == published
+    again = [pcu_pkg.DeviceArray(ctx, prep.output_ptr(k), d["shape"], d["dtype"]).numpy()
+             for k, d in enumerate(prep.output_desc)]
+    for have, want in zip(again, got):
+        np.testing.assert_array_equal(_bits(have), _bits(want))
+    by_id[inp] = dx.ptr
+    prep.execute([by_id[i] for i in prep.input_ids])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_small_mlp_steps_parity(G, dtype):
+    """The C5 graph at reduced width (batch 128, 96 -> 256 -> 256 -> 64), three steps."""
+    from fusion_pcu_amd import synthetic as syn
+    dims, batch, lr = (96, 256, 256, 64), 128, 1e-3
+    x = syn.uniform(51, (batch, dims[0]), dtype)
+    y = syn.uniform(52, (batch, dims[3]), dtype)
+    ws = [syn.xavier_uniform(53 + i, dims[i], dims[i + 1], dtype) for i in range(3)]
+    step = G.mlp_training_step(lr)
+    ref_graph, ids = og.mlp_graph(dims, batch, dtype, lr)
+    dev = list(ws)
+    ref = list(ws)
+    for it in range(3):
+        w1, w2, w3, loss = step(x, *dev)
+        dev = [w1, w2, w3]
+        vals, fault = ref_graph.evaluate({ids["x"]: x, ids["w1"]: ref[0], ids["w2"]: ref[1],
+                                          ids["w3"]: ref[2], ids["y"]: y}, ids["outputs"])
+        assert fault is None
+        ref = [vals[o] for o in ids["outputs"][:3]]
+        assert _bits(loss.numpy()).item() == _bits(vals[ids["outputs"][3]]).item()
+        for have, want in zip(dev, ref):
+            np.testing.assert_array_equal(_bits(have.numpy()), _bits(want), err_msg=f"step {it}")
+
+
+def test_first_faulting_node_matches_oracle(G, pcu_pkg):
+    """A graph whose later nodes would also fault reports the earliest node, like the
+    reference's ordered per-node execution."""
+    from fusion_pcu_amd import synthetic as syn
+    x = syn.uniform(61, (32, 48), np.float32)
+    w = syn.uniform(62, (48, 16), np.float32)
+    b = syn.uniform(63, (32, 16), np.float32)
+    y = syn.uniform(64, (32, 16), np.float32)
+    w[7, 3] = np.float32(3.0e38)
+    w[9, 3] = np.float32(3.0e38)
+    x[:, 7] = 1.0
+    x[:, 9] = 1.0
+    step = G.c1_training_step(0.01)
+    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+        step(x, w, b, y)
+    ref = oracle.graph_c1_step(x, w, b, y, 0.01)
+    assert ref["fault"] is not None
+    tf = exc.value.tensor_fault
+    rf = ref["fault"]
+    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step, rf.fault.kind)
