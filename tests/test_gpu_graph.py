@@ -166,7 +166,7 @@ def test_small_mlp_steps_parity(G, dtype):
     dev = list(ws)
     ref = list(ws)
     for it in range(3):
-        w1, w2, w3, loss = step(x, *dev)
+        w1, w2, w3, loss = step(x, *dev, y)
         dev = [w1, w2, w3]
         vals, fault = ref_graph.evaluate({ids["x"]: x, ids["w1"]: ref[0], ids["w2"]: ref[1],
                                           ids["w3"]: ref[2], ids["y"]: y}, ids["outputs"])
