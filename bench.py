@@ -105,6 +105,43 @@ def bench_sgd(pkg, ctx, n, steps, warmup):
             "kernel_hbm_frac": 12.0 * n / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_mlp(pkg, ctx, steps, warmup):
+    """C5: strict F32 MLP 1024->4096->4096->1024, batch 4096, lr 1e-3, Xavier weights,
+    inputs and weights resident; one step = forward, MSE, backward, three SGD updates."""
+    from fusion_pcu_amd import graph as G
+    from fusion_pcu_amd import synthetic as syn
+    dims, batch = (1024, 4096, 4096, 1024), 4096
+    x = G.PcuTensor(ctx.upload(syn.uniform(51, (batch, dims[0]), np.float32)))
+    y = G.PcuTensor(ctx.upload(syn.uniform(52, (batch, dims[3]), np.float32)))
+    ws = [G.PcuTensor(ctx.upload(syn.xavier_uniform(53 + i, dims[i], dims[i + 1], np.float32)))
+          for i in range(3)]
+    step = G.mlp_training_step(1e-3)
+    for _ in range(warmup):
+        *ws, loss = step(x, *ws, y)
+    ctx.synchronize()
+    ctx.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        *ws, loss = step(x, *ws, y)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    kern = {k: ctx.kernel_time(k) for k in ("strict_gemm", "gemm_prefilter", "gemm_replay",
+                                            "sgd", "binary", "relu", "relu_backward", "mse")}
+    ctx.profile(False)
+    flops = 2.0 * batch * (dims[0] * dims[1] + dims[1] * dims[2] + dims[2] * dims[3]) * 3 \
+        - 2.0 * batch * dims[0] * dims[1]  # no input-gradient MatMul for X
+    ms = (t1 - t0) * 1e3 / steps
+    return {
+        "steps_per_s": 1e3 / ms,
+        "ms_per_step": ms,
+        "matmul_gflop_per_step": flops / 1e9,
+        "gemm_ms_per_step": kern["strict_gemm"][0] / steps,
+        "mse_ms_per_step": kern["mse"][0] / steps,
+        "elementwise_ms_per_step": sum(kern[k][0] for k in ("sgd", "binary", "relu", "relu_backward")) / steps,
+        "loss": float(loss.numpy()),
+    }
+
+
 def cpu_baseline(m, k, n, rows):
     """Faithful port (integer-significand law, one thread) on `rows` output rows."""
     sys.path.insert(0, ROOT)
@@ -185,11 +222,16 @@ def main() -> int:
     M = N = K = 4096
     if args.probe:
         return probe(pkg, M, K, N)
-    with pkg.Context(0) as ctx:
+    from fusion_pcu_amd import graph as G
+    G.configure(0)
+    ctx = G.default_context()
+    if True:
         log("strict F32 MatMul 4096^3")
         mm = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup)
         extra = {}
         if not args.no_extra:
+            log("strict F32 MLP training step (C5)")
+            extra["mlp_c5"] = bench_mlp(pkg, ctx, max(5, args.steps), 2)
             log("strict F64 MatMul 4096^3 (C3 shape)")
             f64 = bench_matmul(pkg, ctx, M, K, N, np.float64, max(2, args.steps // 3), 1, 31, 32)
             extra["f64_matmul_4096"] = {
@@ -236,6 +278,8 @@ def main() -> int:
                                "prefilter + tile kernel + replay check + fault readback",
                    "m": M, "k": K, "n": N},
         "pct_fp32_vector_peak": round(100.0 * mm["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 3),
+        "mlp_train_steps_per_s": (round(extra["mlp_c5"]["steps_per_s"], 3)
+                                  if "mlp_c5" in extra else None),
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,
