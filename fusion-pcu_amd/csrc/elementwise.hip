@@ -364,65 +364,331 @@ __global__ __launch_bounds__(256) void k_mse_squares(const T *__restrict__ p,
     wave_record_fault(key, fault);
 }
 
-// One wave. Every lane runs the same dependent chain; the squares are read through
-// uniform addresses (scalar loads), so each element costs one dependent VALU add.
-template <typename T>
-__global__ __launch_bounds__(64) void k_mse_ordered_sum(const T *__restrict__ sq, uint64_t n,
-                                                        T count, int policy, T *__restrict__ out,
-                                                        unsigned long long *fault)
+// Ordered sum of the squares, exact and parallel. Every square is +0 or positive, so the
+// running total never decreases. While the total stays inside one binade [2^E, 2^(E+1))
+// (or below the smallest normal), it is m * u for an integer m and the binade's quantum u,
+// and one rounded step total (+) s equals (m + r) * u where r is s/u rounded to the nearest
+// integer, a tie going to the r that makes m + r even. So inside a binade the chain is a
+// prefix sum of integers whose only coupling is the parity of m at each tie: a two-state
+// automaton, which composes associatively and scans in parallel. The first element whose
+// step would reach the binade's upper end (or any element a screen cannot place) is
+// executed as the real rounded hardware add, checked like every other Add, and starts the
+// next phase. Results equal the dependent chain of the contract bit for bit.
+
+template <typename T> struct SumBits;
+template <> struct SumBits<float> {
+    using U = uint32_t;
+    static constexpr int kFrac = 23;     // stored fraction bits
+    static constexpr int kQmin = -149;   // exponent of the smallest subnormal
+    static constexpr uint32_t kExpAll = 0xff;
+    static constexpr int kPer = 16;      // elements per thread of the ordered sum
+};
+template <> struct SumBits<double> {
+    using U = uint64_t;
+    static constexpr int kFrac = 52;
+    static constexpr int kQmin = -1074;
+    static constexpr uint32_t kExpAll = 0x7ff;
+    static constexpr int kPer = 8;
+};
+
+constexpr int kSumThreads = 512;
+constexpr uint64_t kSumCap = 1ull << 62;   // saturation of prefix sums (past any crossing)
+constexpr uint64_t kSumBig = 1ull << 54;   // r of a step that surely leaves the binade
+
+enum : uint32_t { kRBelow = 0, kRAbove = 1, kRTie = 2, kRForce = 3 };
+
+__device__ __forceinline__ uint64_t sat_add(uint64_t a, uint64_t b)
 {
-    // Elements at or after the first Subtract/Multiply fault are never summed.
-    uint64_t w = __atomic_load_n(fault, __ATOMIC_RELAXED);
-    uint64_t limit = n;
-    if (w != kNoFault)
-        limit = (w >> 3) / 3;
-    T total = (T)0;
-    uint64_t i = 0;
-    constexpr int CH = 16;
-    for (; i + CH <= limit; i += CH) {
-        T s[CH];
-#pragma unroll
-        for (int j = 0; j < CH; j++) s[j] = sq[i + j];
-        T before = total;
-#pragma unroll
-        for (int j = 0; j < CH; j++) total = total + s[j];
-        // Squares and partial sums are nonnegative and finite until an Add overflows, or,
-        // under RejectSubnormal, a partial sum is subnormal: replay the chunk to find it.
-        bool bad = !finite_bits(total) || (policy == kPolicyRejectSubnormal);
-        if (bad) {
-            T acc = before;
-            for (int j = 0; j < CH; j++) {
-                T nxt = acc + s[j];
-                uint32_t k = classify_add(acc, s[j], nxt, policy);
-                if (k != kOk) {
-                    if (__lane_id() == 0)
-                        atomicMin(fault, (unsigned long long)pack_fault(3 * (i + j) + 2, k));
-                    return;
-                }
-                acc = nxt;
-            }
-        }
-    }
-    for (; i < limit; i++) {
-        T nxt = total + sq[i];
-        uint32_t k = classify_add(total, sq[i], nxt, policy);
-        if (k != kOk) {
-            if (__lane_id() == 0)
-                atomicMin(fault, (unsigned long long)pack_fault(3 * i + 2, k));
-            return;
-        }
-        total = nxt;
-    }
-    if (limit < n)
+    uint64_t c = a + b; // a, b <= 2^62: no wrap
+    return c < kSumCap ? c : kSumCap;
+}
+
+// Step r of one square s (bits) on the quantum 2^ue, before the tie decision.
+template <typename T>
+__device__ __forceinline__ void sum_elem(typename SumBits<T>::U b, int ue, uint64_t &n,
+                                         uint32_t &cls)
+{
+    using B = SumBits<T>;
+    const uint32_t e = (uint32_t)(b >> B::kFrac) & B::kExpAll;
+    const uint64_t f = (uint64_t)b & ((1ull << B::kFrac) - 1);
+    if ((b >> (sizeof(T) * 8 - 1)) || e == B::kExpAll) { // negative or non-finite
+        n = kSumBig;
+        cls = kRForce;
         return;
-    T r = total / count;
-    uint32_t k = classify_div(total, count, r, policy);
-    if (__lane_id() == 0) {
-        if (k != kOk)
-            atomicMin(fault, (unsigned long long)pack_fault(3 * n, k));
-        else
-            *out = r;
     }
+    const uint64_t sig = e ? (f | (1ull << B::kFrac)) : f;
+    const int q = e ? (int)e + B::kQmin - 1 : B::kQmin;
+    cls = kRBelow;
+    if (sig == 0) {
+        n = 0;
+        return;
+    }
+    const int sh = q - ue;
+    if (sh >= 0) {
+        n = sh >= 11 ? kSumBig : (sig << sh);
+        n = n < kSumBig ? n : kSumBig;
+        return;
+    }
+    const int k = -sh;
+    if (k > 63) {
+        n = 0;
+        return;
+    }
+    n = sig >> k;
+    const uint64_t rem = sig & ((1ull << k) - 1), half = 1ull << (k - 1);
+    cls = rem < half ? kRBelow : (rem > half ? kRAbove : kRTie);
+}
+
+__device__ __forceinline__ uint64_t sum_step(uint64_t n, uint32_t cls, uint32_t parity)
+{
+    return n + (cls == kRAbove) + (cls == kRTie && ((parity ^ (uint32_t)n) & 1u));
+}
+
+// Effect of a run of steps as a function of the parity of m before it: the added count
+// and the parity after it, for each starting parity (bit 0: start even, bit 1: start odd).
+struct SumScan {
+    uint64_t r0, r1;
+    uint32_t p;
+};
+
+__device__ __forceinline__ SumScan scan_identity() { return SumScan{0, 0, 2u}; }
+
+__device__ __forceinline__ SumScan scan_compose(SumScan a, SumScan b)
+{
+    const uint32_t a0 = a.p & 1u, a1 = (a.p >> 1) & 1u;
+    const uint32_t b0 = b.p & 1u, b1 = (b.p >> 1) & 1u;
+    SumScan c;
+    c.r0 = sat_add(a.r0, a0 ? b.r1 : b.r0);
+    c.r1 = sat_add(a.r1, a1 ? b.r1 : b.r0);
+    c.p = (a0 ? b1 : b0) | ((a1 ? b1 : b0) << 1);
+    return c;
+}
+
+__device__ __forceinline__ SumScan scan_elem(uint64_t n, uint32_t cls)
+{
+    const uint64_t r0 = sum_step(n, cls, 0), r1 = sum_step(n, cls, 1);
+    return SumScan{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
+}
+
+__device__ __forceinline__ SumScan scan_shfl_up(SumScan v, int d)
+{
+    SumScan o;
+    o.r0 = __shfl_up(v.r0, d, 64);
+    o.r1 = __shfl_up(v.r1, d, 64);
+    o.p = __shfl_up(v.p, d, 64);
+    return o;
+}
+
+// Phase of a total given by its bits: quantum exponent, count m and the count at which
+// the next binade starts.
+template <typename T>
+__device__ __forceinline__ void sum_phase(typename SumBits<T>::U bits, int &ue, uint64_t &m,
+                                          uint64_t &mmax)
+{
+    using B = SumBits<T>;
+    const uint32_t e = (uint32_t)(bits >> B::kFrac) & B::kExpAll;
+    if (e == 0) {
+        ue = B::kQmin;
+        m = (uint64_t)bits;
+        mmax = 1ull << B::kFrac;
+    } else {
+        ue = (int)e + B::kQmin - 1;
+        m = ((uint64_t)bits & ((1ull << B::kFrac) - 1)) | (1ull << B::kFrac);
+        mmax = 1ull << (B::kFrac + 1);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ typename SumBits<T>::U sum_bits(int ue, uint64_t m)
+{
+    using B = SumBits<T>;
+    if (ue == B::kQmin && m < (1ull << B::kFrac))
+        return (typename SumBits<T>::U)m;
+    return (typename SumBits<T>::U)(((uint64_t)(ue - B::kQmin) << B::kFrac) + m);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_bits(typename SumBits<T>::U b);
+template <>
+__device__ __forceinline__ float from_bits<float>(uint32_t b) { return __uint_as_float(b); }
+template <>
+__device__ __forceinline__ double from_bits<double>(uint64_t b) { return __longlong_as_double((long long)b); }
+
+// One workgroup of 512 threads; thread t holds elements [base + P*t, base + P*t + P) of
+// each chunk of 512*P (P = 16 for binary32, 8 for binary64), and the next chunk is
+// fetched while the current one is scanned.
+template <typename T>
+__global__ __launch_bounds__(kSumThreads) void k_mse_ordered_sum(
+    const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
+    unsigned long long *fault)
+{
+    using U = typename SumBits<T>::U;
+    constexpr int kSumPer = SumBits<T>::kPer;
+    constexpr uint64_t kSumChunk = (uint64_t)kSumThreads * kSumPer;
+    __shared__ SumScan wave_tot[kSumThreads / 64];
+    __shared__ uint64_t wave_key[kSumThreads / 64];
+    __shared__ uint64_t s_limit;
+    __shared__ U s_total;     // total after a crossing step
+    __shared__ int s_stop;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        // Elements at or after the first Subtract/Multiply fault are never summed.
+        const uint64_t w = __atomic_load_n(fault, __ATOMIC_RELAXED);
+        s_limit = w == kNoFault ? n : (w >> 3) / 3;
+    }
+    __syncthreads();
+    const uint64_t limit = s_limit;
+    const U *src = reinterpret_cast<const U *>(sq);
+    const bool vec_ok = ((uintptr_t)sq & 15u) == 0;
+
+    int ue;
+    uint64_t m, mmax;
+    sum_phase<T>((U)0, ue, m, mmax); // the total starts at +0
+
+    U cur[kSumPer], nxt[kSumPer];
+    auto fetch = [&](uint64_t base, U (&dst)[kSumPer]) {
+        const uint64_t first = base + (uint64_t)tid * kSumPer;
+        if (vec_ok && base + kSumChunk <= limit) {
+            const uint4 *v = reinterpret_cast<const uint4 *>(src + first);
+            constexpr int per16 = 16 / sizeof(U);
+#pragma unroll
+            for (int q = 0; q < kSumPer / per16; q++) {
+                uint4 x = v[q];
+                const U *xs = reinterpret_cast<const U *>(&x);
+#pragma unroll
+                for (int j = 0; j < per16; j++)
+                    dst[q * per16 + j] = xs[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kSumPer; j++)
+                dst[j] = first + j < limit ? src[first + j] : (U)0;
+        }
+    };
+
+    if (limit > 0)
+        fetch(0, cur);
+    for (uint64_t base = 0; base < limit; base += kSumChunk) {
+        if (base + kSumChunk < limit)
+            fetch(base + kSumChunk, nxt);
+        const uint64_t first = base + (uint64_t)tid * kSumPer;
+        uint64_t start = base; // first element of the chunk not yet folded into m
+        for (;;) {
+            // Thread summary over its live elements.
+            SumScan mine = scan_identity();
+#pragma unroll
+            for (int j = 0; j < kSumPer; j++) {
+                uint64_t nn;
+                uint32_t cls;
+                sum_elem<T>(cur[j], ue, nn, cls);
+                const bool live = first + j >= start && first + j < limit;
+                if (live)
+                    mine = scan_compose(mine, scan_elem(nn, cls));
+            }
+            // Inclusive scan over the wave, then over the waves.
+            SumScan inc = mine;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                SumScan o = scan_shfl_up(inc, d);
+                if (lane >= d)
+                    inc = scan_compose(o, inc);
+            }
+            SumScan excl = scan_shfl_up(inc, 1);
+            if (lane == 0)
+                excl = scan_identity();
+            if (lane == 63)
+                wave_tot[wave] = inc;
+            __syncthreads();
+            // Every wave scans the per-wave totals on its first lanes (one LDS read each).
+            constexpr int kWaves = kSumThreads / 64;
+            SumScan wt = lane < kWaves ? wave_tot[lane] : scan_identity();
+#pragma unroll
+            for (int d = 1; d < kWaves; d <<= 1) {
+                SumScan o = scan_shfl_up(wt, d);
+                if (lane >= d)
+                    wt = scan_compose(o, wt);
+            }
+            SumScan total, before;
+            total.r0 = __shfl(wt.r0, kWaves - 1, 64);
+            total.r1 = __shfl(wt.r1, kWaves - 1, 64);
+            total.p = __shfl(wt.p, kWaves - 1, 64);
+            const int pw = wave > 0 ? wave - 1 : 0;
+            before.r0 = __shfl(wt.r0, pw, 64);
+            before.r1 = __shfl(wt.r1, pw, 64);
+            before.p = __shfl(wt.p, pw, 64);
+            if (wave == 0)
+                before = scan_identity();
+            before = scan_compose(before, excl);
+            // Walk this thread's elements from its exact starting state.
+            const uint32_t p0 = (uint32_t)(m & 1u);
+            uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+            uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
+            uint64_t key = kNoFault;
+            U key_bits = 0;
+            uint64_t key_m = 0;
+#pragma unroll
+            for (int j = 0; j < kSumPer; j++) {
+                uint64_t nn;
+                uint32_t cls;
+                sum_elem<T>(cur[j], ue, nn, cls);
+                const bool live = first + j >= start && first + j < limit;
+                if (live && key == kNoFault) {
+                    const uint64_t r = sum_step(nn, cls, pt);
+                    if (cls == kRForce || mt + r >= mmax) {
+                        key = first + j;
+                        key_bits = cur[j];
+                        key_m = mt;
+                    } else {
+                        mt += r;
+                        pt = (pt + (uint32_t)r) & 1u;
+                    }
+                }
+            }
+            const uint64_t wk = wave_min_u64(key);
+            if (lane == 0)
+                wave_key[wave] = wk;
+            __syncthreads();
+            const uint64_t cross = wave_min_u64(lane < kWaves ? wave_key[lane] : kNoFault);
+            if (cross == kNoFault) {
+                m = sat_add(m, p0 ? total.r1 : total.r0);
+                break;
+            }
+            if (key == cross) {
+                // The crossing step, executed and checked as the contract's Add.
+                const T acc = from_bits<T>(sum_bits<T>(ue, key_m));
+                const T s_i = from_bits<T>(key_bits);
+                const T r = acc + s_i;
+                const uint32_t kind = classify_add(acc, s_i, r, policy);
+                if (kind != kOk) {
+                    atomicMin(fault, (unsigned long long)pack_fault(3 * cross + 2, kind));
+                    s_stop = 1;
+                } else {
+                    s_stop = 0;
+                    s_total = (U)bits_of(r);
+                }
+            }
+            __syncthreads();
+            if (s_stop)
+                return;
+            sum_phase<T>(s_total, ue, m, mmax);
+            start = cross + 1;
+        }
+        if (base + kSumChunk < limit) {
+#pragma unroll
+            for (int j = 0; j < kSumPer; j++)
+                cur[j] = nxt[j];
+        }
+    }
+    if (limit < n || tid != 0)
+        return;
+    const T total = from_bits<T>(sum_bits<T>(ue, m));
+    const T r = total / count;
+    const uint32_t kind = classify_div(total, count, r, policy);
+    if (kind != kOk)
+        atomicMin(fault, (unsigned long long)pack_fault(3 * n, kind));
+    else
+        *out = r;
 }
 
 // ================================================================ launchers
@@ -590,7 +856,7 @@ static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    hipLaunchKernelGGL((k_mse_ordered_sum<T>), dim3(1), dim3(64), 0, s, (const T *)squares, n, count, policy, (T *)out, fault);
+    hipLaunchKernelGGL((k_mse_ordered_sum<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault);
     return hipGetLastError();
 }
 

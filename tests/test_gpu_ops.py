@@ -264,6 +264,46 @@ def test_mse_faults_parity(ctx, pcu_pkg, dtype):
                 assert _bits(got).item() == _bits(ref).item()
 
 
+def _tie_heavy(rng, n, dtype, lo, hi):
+    """Differences d = m * 2^k with small odd m, so the squares are 9-, 25-, 49-multiples
+    of even powers of two: many steps of the ordered sum land exactly on rounding ties or
+    next to them, and the total crosses many binades."""
+    m = rng.choice(np.array([1, 3, 5, 7], dtype=np.float64), n)
+    k = rng.integers(lo, hi, n).astype(np.float64)
+    return (m * np.exp2(k) * rng.choice([-1.0, 1.0], n)).astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_mse_ordered_sum_rounding_stress(ctx, pcu_pkg, dtype):
+    """The ordered sum of squares at sizes around the kernel's chunking (4096 and 8192
+    elements), with rounding ties, subnormal totals, huge steps after a tiny total and
+    overflow at chosen positions: bit-exact against the oracle's dependent chain."""
+    rng = np.random.default_rng(2024)
+    info = np.finfo(dtype)
+    sub_k = (-74, -62) if dtype == np.float32 else (-537, -505)
+    sizes = [1, 63, 4095, 4096, 4097, 8191, 8192, 8193, 3 * 8192 + 5, 70_001]
+    for n in sizes:
+        cases = [
+            _tie_heavy(rng, n, dtype, -20, 4),
+            _tie_heavy(rng, n, dtype, -14, -10),
+            _tie_heavy(rng, n, dtype, *sub_k),
+            np.concatenate([_tie_heavy(rng, n // 2, dtype, -30, -20),
+                            _tie_heavy(rng, n - n // 2, dtype, 5, 9)]),
+            rng.uniform(-1, 1, n).astype(dtype),
+        ]
+        if n > 2:
+            big = np.full(n, np.sqrt(info.max) * dtype(0.75), dtype)
+            big[: n // 3] = dtype(0.5)
+            cases.append(big)  # Add overflow once two huge squares meet
+        for i, p in enumerate(cases):
+            t = np.zeros(n, dtype)
+            got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_mse(ctx.upload(p), ctx.upload(t)).numpy())
+            ref, rf = oracle.mse(p, t)
+            assert gf == _ofault(rf), (n, i, gf, rf)
+            if rf is None:
+                assert _bits(got).item() == _bits(ref).item(), (n, i, got, ref)
+
+
 # ------------------------------------------------------------------- MatMul
 
 
