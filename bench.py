@@ -186,10 +186,13 @@ def probe(pkg, M, K, N) -> int:
         ctx.strict_matmul(da, db, out=dc)
         ctx.checked_binary(0, x, 0.0, out=y)
         ctx.strict_sgd(x, g, 0.01, out=y)
-        log("probe: one launch each")
+        log("probe: one launch each (MatMul: matrix-core products, then vector-unit engine)")
         ctx.strict_matmul(da, db, out=dc)
         ctx.checked_binary(0, x, 0.0, out=y)
         ctx.strict_sgd(x, g, 0.01, out=y)
+        ctx.set_matmul_engine("valu")
+        ctx.strict_matmul(da, db, out=dc)
+        ctx.set_matmul_engine("auto")
         ctx.synchronize()
     log("probe: done")
     return 0

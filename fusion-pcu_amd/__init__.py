@@ -191,6 +191,13 @@ class Context:
     def synchronize(self) -> None:
         self.check(self._lib.pcu_ctx_synchronize(self.handle))
 
+    MATMUL_ENGINES = {"auto": 0, "valu": 1, "mfma_products": 2}
+
+    def set_matmul_engine(self, engine: str) -> None:
+        """Main-kernel engine of the strict F32 MatMul ("auto", "valu", "mfma_products");
+        every engine gives the same bits."""
+        self.check(self._lib.pcu_ctx_set_matmul_engine(self.handle, self.MATMUL_ENGINES[engine]))
+
     @property
     def stream(self) -> int:
         return self._lib.pcu_ctx_stream(self.handle)

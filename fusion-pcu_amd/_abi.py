@@ -59,6 +59,7 @@ SIGNATURES = {
     "pcu_last_error": (_cp, [_vp]),
     "pcu_ctx_stream": (_vp, [_vp]),
     "pcu_ctx_synchronize": (_i32, [_vp]),
+    "pcu_ctx_set_matmul_engine": (_i32, [_vp, _i32]),
     "pcu_buf_alloc": (_i32, [_vp, _sz, _VPP]),
     "pcu_buf_free": (_i32, [_vp, _vp]),
     "pcu_upload": (_i32, [_vp, _vp, _vp, _sz]),

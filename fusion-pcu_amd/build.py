@@ -37,7 +37,7 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["elementwise.hip", "matmul.hip", "runtime.cpp", "graph.cpp"]
+SOURCES = ["elementwise.hip", "matmul.hip", "matmul_mfma.hip", "runtime.cpp", "graph.cpp"]
 
 
 def _compile(src: str) -> str:

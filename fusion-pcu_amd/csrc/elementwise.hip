@@ -1,11 +1,13 @@
 // Bandwidth-bound strict kernels: checked Add/Sub/Mul/Div (tensor or uniform right
 // operand), ReLU, ReLU-backward, fused Add->ReLU, strict SGD and strict MSE.
 //
-// Layout: dense row-major tensors in HBM. Each thread moves 16 bytes per operand per
-// iteration (float4 / double2) in a grid-stride loop when the pointers and length allow,
-// so one wave touches 1 KiB contiguous per operand per iteration. Faults are screened per
-// lane, resolved exactly only on flagged lanes, and reduced with one ballot per wave and
-// one atomicMin per faulting wave into the op's 64-bit fault word.
+// Layout: dense row-major tensors in HBM. One thread moves one 16-byte vector per operand
+// (4 floats or 2 doubles) and the grid covers the whole tensor in 128-thread blocks, with
+// non-temporal loads and stores: on MI355X this streams at about 85% of the 8 TB/s HBM
+// peak, ahead of every grid-stride shape tried. The last vector may be partial (scalar
+// accesses for its in-range elements). Faults are screened per lane, resolved exactly
+// only on flagged lanes, and reduced with one ballot per wave and one atomicMin per
+// faulting wave into the op's 64-bit fault word.
 #include "pcu_device.hpp"
 #include "pcu_kernels.hpp"
 
@@ -13,34 +15,75 @@
 
 namespace pcu {
 
+constexpr int kEwThreads = 128;
+
 template <typename T> struct Vec;
 template <> struct Vec<float> {
-    using type = float4;
+    typedef float type __attribute__((ext_vector_type(4)));
     static constexpr int width = 4;
 };
 template <> struct Vec<double> {
-    using type = double2;
+    typedef double type __attribute__((ext_vector_type(2)));
     static constexpr int width = 2;
 };
 
-template <typename T>
-__device__ __forceinline__ void unpack(const typename Vec<T>::type &v, T *out);
-template <>
-__device__ __forceinline__ void unpack<float>(const float4 &v, float *o)
+template <typename T, bool VEC> struct Lanes {
+    static constexpr int W = VEC ? Vec<T>::width : 1;
+};
+
+// Elements [base, base + W) of p that lie below n (the rest read as +0 and must be masked
+// by the caller). A whole vector is one non-temporal 16-byte load.
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_lanes(const T *__restrict__ p, uint64_t base, uint64_t n,
+                                           T (&v)[Lanes<T, VEC>::W])
 {
-    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    constexpr int W = Lanes<T, VEC>::W;
+    if (VEC && base + W <= n) {
+        typedef typename Vec<T>::type V;
+        const V q = __builtin_nontemporal_load(reinterpret_cast<const V *>(p + base));
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            v[j] = q[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            v[j] = base + j < n ? __builtin_nontemporal_load(p + base + j) : (T)0;
+    }
 }
-template <>
-__device__ __forceinline__ void unpack<double>(const double2 &v, double *o)
+
+template <typename T, bool VEC, bool NT = true>
+__device__ __forceinline__ void store_lanes(T *__restrict__ p, uint64_t base, uint64_t n,
+                                            const T (&v)[Lanes<T, VEC>::W])
 {
-    o[0] = v.x; o[1] = v.y;
+    constexpr int W = Lanes<T, VEC>::W;
+    if (VEC && base + W <= n) {
+        typedef typename Vec<T>::type V;
+        V q;
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            q[j] = v[j];
+        if (NT)
+            __builtin_nontemporal_store(q, reinterpret_cast<V *>(p + base));
+        else
+            *reinterpret_cast<V *>(p + base) = q;
+    } else {
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (base + j < n) {
+                if (NT)
+                    __builtin_nontemporal_store(v[j], p + base + j);
+                else
+                    p[base + j] = v[j];
+            }
+    }
 }
-template <typename T>
-__device__ __forceinline__ typename Vec<T>::type pack(const T *o);
-template <>
-__device__ __forceinline__ float4 pack<float>(const float *o) { return make_float4(o[0], o[1], o[2], o[3]); }
-template <>
-__device__ __forceinline__ double2 pack<double>(const double *o) { return make_double2(o[0], o[1]); }
+
+// First element index of this thread's vector and the distance to its next one (the grid
+// normally covers the tensor, so the loop body runs once).
+#define PCU_EW_LOOP(W)                                                                          \
+    const uint64_t pcu_stride = (uint64_t)gridDim.x * kEwThreads * (W);                         \
+    for (uint64_t base = ((uint64_t)blockIdx.x * kEwThreads + threadIdx.x) * (W); base < n;     \
+         base += pcu_stride)
 
 template <typename T, int OP>
 __device__ __forceinline__ T apply(T a, T b)
@@ -70,43 +113,38 @@ __device__ __forceinline__ uint32_t classify(T a, T b, T r, int policy)
 // ------------------------------------------------------------ checked binary
 
 template <typename T, int OP, bool UNIFORM, bool VEC>
-__global__ __launch_bounds__(256) void k_binary(const T *__restrict__ a, const T *__restrict__ b,
-                                                T b_value, T *__restrict__ out, uint64_t n,
-                                                int policy, unsigned long long *fault)
+__global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
+                                                       const T *__restrict__ b, T b_value,
+                                                       T *__restrict__ out, uint64_t n,
+                                                       int policy, unsigned long long *fault)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
+    PCU_EW_LOOP(W)
+    {
         T x[W], y[W], r[W];
-        if (VEC) {
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(a + base), x);
-            if (UNIFORM) {
+        load_lanes<T, VEC>(a, base, n, x);
+        if (UNIFORM) {
 #pragma unroll
-                for (int j = 0; j < W; j++) y[j] = b_value;
-            } else {
-                unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(b + base), y);
-            }
+            for (int j = 0; j < W; j++)
+                y[j] = b_value;
         } else {
-            x[0] = a[base];
-            y[0] = UNIFORM ? b_value : b[base];
+            load_lanes<T, VEC>(b, base, n, y);
         }
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
             r[j] = apply<T, OP>(x[j], y[j]);
-            any |= suspect<T, OP>(x[j], y[j], r[j], policy);
+            any |= base + j < n && suspect<T, OP>(x[j], y[j], r[j], policy);
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(out + base) = pack<T>(r);
-        else
-            out[base] = r[0];
+        store_lanes<T, VEC>(out, base, n, r);
         if (any && key == kNoFault) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                uint32_t kind = classify<T, OP>(x[j], y[j], r[j], policy);
-                if (kind != kOk && key == kNoFault)
+                if (base + j >= n || key != kNoFault)
+                    continue;
+                const uint32_t kind = classify<T, OP>(x[j], y[j], r[j], policy);
+                if (kind != kOk)
                     key = pack_fault(base + j, kind);
             }
         }
@@ -117,34 +155,31 @@ __global__ __launch_bounds__(256) void k_binary(const T *__restrict__ a, const T
 // -------------------------------------------------------------------- relu
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_relu(const T *__restrict__ x, T *__restrict__ out,
-                                              uint64_t n, int policy, unsigned long long *fault)
+__global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T *__restrict__ out,
+                                                     uint64_t n, int policy,
+                                                     unsigned long long *fault)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
+    PCU_EW_LOOP(W)
+    {
         T v[W], r[W];
-        if (VEC)
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(x + base), v);
-        else
-            v[0] = x[base];
+        load_lanes<T, VEC>(x, base, n, v);
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
             r[j] = relu_select(v[j]);
-            any |= !finite_bits(v[j]) || (policy == kPolicyRejectSubnormal && subnormal(r[j]));
+            any |= base + j < n &&
+                   (!finite_bits(v[j]) || (policy == kPolicyRejectSubnormal && subnormal(r[j])));
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(out + base) = pack<T>(r);
-        else
-            out[base] = r[0];
+        store_lanes<T, VEC>(out, base, n, r);
         if (any && key == kNoFault) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                uint32_t kind = classify_relu(v[j], r[j], policy);
-                if (kind != kOk && key == kNoFault)
+                if (base + j >= n || key != kNoFault)
+                    continue;
+                const uint32_t kind = classify_relu(v[j], r[j], policy);
+                if (kind != kOk)
                     key = pack_fault(base + j, kind);
             }
         }
@@ -155,40 +190,34 @@ __global__ __launch_bounds__(256) void k_relu(const T *__restrict__ x, T *__rest
 // ---------------------------------------------------------- relu backward
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_relu_backward(const T *__restrict__ x,
-                                                       const T *__restrict__ up,
-                                                       T *__restrict__ out, uint64_t n,
-                                                       int policy, unsigned long long *fault)
+__global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restrict__ x,
+                                                              const T *__restrict__ up,
+                                                              T *__restrict__ out, uint64_t n,
+                                                              int policy,
+                                                              unsigned long long *fault)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
+    PCU_EW_LOOP(W)
+    {
         T v[W], u[W], r[W];
-        if (VEC) {
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(x + base), v);
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(up + base), u);
-        } else {
-            v[0] = x[base];
-            u[0] = up[base];
-        }
+        load_lanes<T, VEC>(x, base, n, v);
+        load_lanes<T, VEC>(up, base, n, u);
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
             r[j] = strictly_positive(v[j]) ? u[j] : (T)0;
-            any |= !finite_bits(v[j]) || !finite_bits(u[j]) ||
-                   (policy == kPolicyRejectSubnormal && subnormal(r[j]));
+            any |= base + j < n && (!finite_bits(v[j]) || !finite_bits(u[j]) ||
+                                    (policy == kPolicyRejectSubnormal && subnormal(r[j])));
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(out + base) = pack<T>(r);
-        else
-            out[base] = r[0];
+        store_lanes<T, VEC>(out, base, n, r);
         if (any && key == kNoFault) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                uint32_t kind = classify_relu_backward(v[j], u[j], r[j], policy);
-                if (kind != kOk && key == kNoFault)
+                if (base + j >= n || key != kNoFault)
+                    continue;
+                const uint32_t kind = classify_relu_backward(v[j], u[j], r[j], policy);
+                if (kind != kOk)
                     key = pack_fault(base + j, kind);
             }
         }
@@ -202,50 +231,46 @@ __global__ __launch_bounds__(256) void k_relu_backward(const T *__restrict__ x,
 // (a ReLU of a successful, hence finite, sum can only fault under RejectSubnormal).
 
 template <typename T, bool UNIFORM, bool VEC>
-__global__ __launch_bounds__(256) void k_add_relu(const T *__restrict__ a, const T *__restrict__ b,
-                                                  T b_value, T *__restrict__ out, uint64_t n,
-                                                  int policy, unsigned long long *fault_add,
-                                                  unsigned long long *fault_relu)
+__global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a,
+                                                         const T *__restrict__ b, T b_value,
+                                                         T *__restrict__ out, uint64_t n,
+                                                         int policy,
+                                                         unsigned long long *fault_add,
+                                                         unsigned long long *fault_relu)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key_add = kNoFault, key_relu = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
-        T x[W], y[W], s[W], r[W];
-        if (VEC) {
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(a + base), x);
-            if (UNIFORM) {
+    PCU_EW_LOOP(W)
+    {
+        T x[W], y[W], sum[W], r[W];
+        load_lanes<T, VEC>(a, base, n, x);
+        if (UNIFORM) {
 #pragma unroll
-                for (int j = 0; j < W; j++) y[j] = b_value;
-            } else {
-                unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(b + base), y);
-            }
+            for (int j = 0; j < W; j++)
+                y[j] = b_value;
         } else {
-            x[0] = a[base];
-            y[0] = UNIFORM ? b_value : b[base];
+            load_lanes<T, VEC>(b, base, n, y);
         }
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            s[j] = x[j] + y[j];
-            r[j] = relu_select(s[j]);
-            any |= add_suspect(x[j], y[j], s[j], policy) ||
-                   (policy == kPolicyRejectSubnormal && subnormal(r[j]));
+            sum[j] = x[j] + y[j];
+            r[j] = relu_select(sum[j]);
+            any |= base + j < n && (add_suspect(x[j], y[j], sum[j], policy) ||
+                                    (policy == kPolicyRejectSubnormal && subnormal(r[j])));
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(out + base) = pack<T>(r);
-        else
-            out[base] = r[0];
+        store_lanes<T, VEC>(out, base, n, r);
         if (any) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                uint32_t ka = classify_add(x[j], y[j], s[j], policy);
+                if (base + j >= n)
+                    continue;
+                const uint32_t ka = classify_add(x[j], y[j], sum[j], policy);
                 if (ka != kOk) {
                     if (key_add == kNoFault)
                         key_add = pack_fault(base + j, ka);
                 } else {
-                    uint32_t kr = classify_relu(s[j], r[j], policy);
+                    const uint32_t kr = classify_relu(sum[j], r[j], policy);
                     if (kr != kOk && key_relu == kNoFault)
                         key_relu = pack_fault(base + j, kr);
                 }
@@ -261,44 +286,37 @@ __global__ __launch_bounds__(256) void k_add_relu(const T *__restrict__ a, const
 // w' = w (-) p; ordinal 2i (Multiply) and 2i+1 (Subtract).
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_sgd(const T *__restrict__ w, const T *__restrict__ g,
-                                             T rate, T *__restrict__ out, uint64_t n, int policy,
-                                             unsigned long long *fault)
+__global__ __launch_bounds__(kEwThreads) void k_sgd(const T *__restrict__ w,
+                                                    const T *__restrict__ g, T rate,
+                                                    T *__restrict__ out, uint64_t n, int policy,
+                                                    unsigned long long *fault)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
+    PCU_EW_LOOP(W)
+    {
         T wv[W], gv[W], p[W], r[W];
-        if (VEC) {
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(w + base), wv);
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(g + base), gv);
-        } else {
-            wv[0] = w[base];
-            gv[0] = g[base];
-        }
+        load_lanes<T, VEC>(w, base, n, wv);
+        load_lanes<T, VEC>(g, base, n, gv);
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
             p[j] = rate * gv[j];
             r[j] = wv[j] - p[j];
-            any |= mul_suspect(rate, gv[j], p[j], policy) | add_suspect(wv[j], p[j], r[j], policy);
+            any |= base + j < n && (mul_suspect(rate, gv[j], p[j], policy) |
+                                    add_suspect(wv[j], p[j], r[j], policy));
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(out + base) = pack<T>(r);
-        else
-            out[base] = r[0];
+        store_lanes<T, VEC>(out, base, n, r);
         if (any && key == kNoFault) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                if (key != kNoFault)
-                    break;
-                uint32_t km = classify_mul(rate, gv[j], p[j], policy);
+                if (base + j >= n || key != kNoFault)
+                    continue;
+                const uint32_t km = classify_mul(rate, gv[j], p[j], policy);
                 if (km != kOk) {
                     key = pack_fault(2 * (base + j), km);
                 } else {
-                    uint32_t ks = classify_add(wv[j], p[j], r[j], policy);
+                    const uint32_t ks = classify_add(wv[j], p[j], r[j], policy);
                     if (ks != kOk)
                         key = pack_fault(2 * (base + j) + 1, ks);
                 }
@@ -316,45 +334,39 @@ __global__ __launch_bounds__(256) void k_sgd(const T *__restrict__ w, const T *_
 // element whose Subtract or Multiply faulted.
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_mse_squares(const T *__restrict__ p,
-                                                     const T *__restrict__ t,
-                                                     T *__restrict__ sq, uint64_t n, int policy,
-                                                     unsigned long long *fault)
+__global__ __launch_bounds__(kEwThreads) void k_mse_squares(const T *__restrict__ p,
+                                                            const T *__restrict__ t,
+                                                            T *__restrict__ sq, uint64_t n,
+                                                            int policy,
+                                                            unsigned long long *fault)
 {
-    constexpr int W = VEC ? Vec<T>::width : 1;
+    constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * W;
-    for (uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * W; base < n;
-         base += stride) {
-        T pv[W], tv[W], d[W], s[W];
-        if (VEC) {
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(p + base), pv);
-            unpack<T>(*reinterpret_cast<const typename Vec<T>::type *>(t + base), tv);
-        } else {
-            pv[0] = p[base];
-            tv[0] = t[base];
-        }
+    PCU_EW_LOOP(W)
+    {
+        T pv[W], tv[W], d[W], sv[W];
+        load_lanes<T, VEC>(p, base, n, pv);
+        load_lanes<T, VEC>(t, base, n, tv);
         bool any = false;
 #pragma unroll
         for (int j = 0; j < W; j++) {
             d[j] = pv[j] - tv[j];
-            s[j] = d[j] * d[j];
-            any |= add_suspect(pv[j], tv[j], d[j], policy) | mul_suspect(d[j], d[j], s[j], policy);
+            sv[j] = d[j] * d[j];
+            any |= base + j < n && (add_suspect(pv[j], tv[j], d[j], policy) |
+                                    mul_suspect(d[j], d[j], sv[j], policy));
         }
-        if (VEC)
-            *reinterpret_cast<typename Vec<T>::type *>(sq + base) = pack<T>(s);
-        else
-            sq[base] = s[0];
+        // Ordinary stores: the ordered sum reads the squares next.
+        store_lanes<T, VEC, false>(sq, base, n, sv);
         if (any && key == kNoFault) {
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                if (key != kNoFault)
-                    break;
-                uint32_t ks = classify_add(pv[j], tv[j], d[j], policy);
+                if (base + j >= n || key != kNoFault)
+                    continue;
+                const uint32_t ks = classify_add(pv[j], tv[j], d[j], policy);
                 if (ks != kOk) {
                     key = pack_fault(3 * (base + j), ks);
                 } else {
-                    uint32_t km = classify_mul(d[j], d[j], s[j], policy);
+                    const uint32_t km = classify_mul(d[j], d[j], sv[j], policy);
                     if (km != kOk)
                         key = pack_fault(3 * (base + j) + 1, km);
                 }
@@ -697,9 +709,10 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; 
 
 static inline unsigned grid_for(uint64_t work_items)
 {
-    uint64_t blocks = (work_items + 255) / 256;
-    if (blocks > 16384)
-        blocks = 16384;
+    // One work item per thread; beyond 2^24 blocks the kernels' loops take the rest.
+    uint64_t blocks = (work_items + kEwThreads - 1) / kEwThreads;
+    if (blocks > (1ull << 24))
+        blocks = 1ull << 24;
     return blocks ? (unsigned)blocks : 1u;
 }
 
@@ -711,15 +724,15 @@ static hipError_t binary_t(hipStream_t s, int op, uint64_t n, const void *a, con
     T bv = b_value ? *(const T *)b_value : (T)0;
     bool uniform = b == nullptr;
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(a) && aligned16(out) && (uniform || aligned16(b));
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(a) && aligned16(out) && (uniform || aligned16(b));
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
 #define PCU_LAUNCH_BINARY(OPC)                                                                      \
     if (uniform) {                                                                                  \
-        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, true, true>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault); \
-        else hipLaunchKernelGGL((k_binary<T, OPC, true, false>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        else hipLaunchKernelGGL((k_binary<T, OPC, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
     } else {                                                                                        \
-        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, false, true>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault); \
-        else hipLaunchKernelGGL((k_binary<T, OPC, false, false>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        else hipLaunchKernelGGL((k_binary<T, OPC, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
     }
     switch (op) {
     case kOpAdd: PCU_LAUNCH_BINARY(kOpAdd) break;
@@ -746,12 +759,12 @@ static hipError_t relu_t(hipStream_t s, uint64_t n, const void *x, void *out, in
                          unsigned long long *fault)
 {
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(x) && aligned16(out);
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(x) && aligned16(out);
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_relu<T, true>), dim3(grid), dim3(256), 0, s, (const T *)x, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault);
     else
-        hipLaunchKernelGGL((k_relu<T, false>), dim3(grid), dim3(256), 0, s, (const T *)x, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault);
     return hipGetLastError();
 }
 
@@ -769,12 +782,12 @@ static hipError_t relu_backward_t(hipStream_t s, uint64_t n, const void *x, cons
                                   void *out, int policy, unsigned long long *fault)
 {
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(x) && aligned16(up) && aligned16(out);
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(x) && aligned16(up) && aligned16(out);
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_relu_backward<T, true>), dim3(grid), dim3(256), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu_backward<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
     else
-        hipLaunchKernelGGL((k_relu_backward<T, false>), dim3(grid), dim3(256), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu_backward<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
     return hipGetLastError();
 }
 
@@ -797,14 +810,14 @@ static hipError_t add_relu_t(hipStream_t s, uint64_t n, const void *a, const voi
     T bv = b_value ? *(const T *)b_value : (T)0;
     bool uniform = b == nullptr;
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(a) && aligned16(out) && (uniform || aligned16(b));
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(a) && aligned16(out) && (uniform || aligned16(b));
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (uniform) {
-        if (vec) hipLaunchKernelGGL((k_add_relu<T, true, true>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
-        else hipLaunchKernelGGL((k_add_relu<T, true, false>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        if (vec) hipLaunchKernelGGL((k_add_relu<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        else hipLaunchKernelGGL((k_add_relu<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
     } else {
-        if (vec) hipLaunchKernelGGL((k_add_relu<T, false, true>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
-        else hipLaunchKernelGGL((k_add_relu<T, false, false>), dim3(grid), dim3(256), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        if (vec) hipLaunchKernelGGL((k_add_relu<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        else hipLaunchKernelGGL((k_add_relu<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
     }
     return hipGetLastError();
 }
@@ -824,12 +837,12 @@ static hipError_t sgd_t(hipStream_t s, uint64_t n, const void *w, const void *g,
                         void *out, int policy, unsigned long long *fault)
 {
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(w) && aligned16(g) && aligned16(out);
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(w) && aligned16(g) && aligned16(out);
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(256), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
     else
-        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(256), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
     return hipGetLastError();
 }
 
@@ -847,12 +860,12 @@ static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
                         T count, void *out, int policy, unsigned long long *fault)
 {
     constexpr int Wd = Vec<T>::width;
-    bool vec = n % Wd == 0 && aligned16(p) && aligned16(t) && aligned16(squares);
-    unsigned grid = grid_for(vec ? n / Wd : n);
+    bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
+    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(256), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
+        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
     else
-        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(256), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
+        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;

@@ -418,7 +418,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault,
                                   const unsigned long long *prior, unsigned n_prior,
-                                  hipEvent_t *ev)
+                                  hipEvent_t *ev, int engine)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -442,7 +442,10 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const int m = (int)M, n = (int)N, k = (int)K;
     if (ev)
         (void)hipEventRecord(ev[1], s);
-    if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    if (f32 && engine != kEngineValu) {
+        (void)launch_gemm_mfma_f32(s, m, n, k, ta, tb, (const float *)A, (const float *)B,
+                                   (float *)C, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+    } else if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
     else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
     else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
     else gemm_dispatch<T, true, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
@@ -464,17 +467,17 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault,
                                 const unsigned long long *prior, unsigned n_prior,
-                                hipEvent_t *ev)
+                                hipEvent_t *ev, int engine)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (dtype == 0)
         return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                       (const float *)a, (const float *)b, (float *)c, policy,
-                                      scratch, fault, prior, n_prior, ev);
+                                      scratch, fault, prior, n_prior, ev, engine);
     return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                    (const double *)a, (const double *)b, (double *)c, policy,
-                                   scratch, fault, prior, n_prior, ev);
+                                   scratch, fault, prior, n_prior, ev, kEngineValu);
 }
 
 } // namespace pcu

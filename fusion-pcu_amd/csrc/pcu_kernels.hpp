@@ -37,6 +37,16 @@ struct MatmulScratch {
 size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);
 MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
 
+// Main-kernel engine of the strict F32 MatMul: products from the vector unit (v_mul_f32),
+// or from the matrix cores used as a K=1 multiplier array with a +0 accumulator (bit-equal
+// products; the ordered sums stay on the vector unit). F64 always uses the vector unit.
+enum : int { kEngineAuto = 0, kEngineValu = 1, kEngineMfmaProducts = 2 };
+
+hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
+                                const float *A, const float *B, float *C, const int *row_exp,
+                                const int *col_exp, int thr, int risk,
+                                unsigned long long *suspect);
+
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
 // `prior`/`n_prior` are the fault words of the ops enqueued before this one: the exact
 // replay skips its work once one of them holds a fault (that earlier fault is reported).
@@ -47,7 +57,7 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault,
                                 const unsigned long long *prior, unsigned n_prior,
-                                hipEvent_t *ev = nullptr);
+                                hipEvent_t *ev = nullptr, int engine = kEngineAuto);
 
 // Small device utilities (fill kernels rather than memsets, so a captured graph replays
 // them as kernels).

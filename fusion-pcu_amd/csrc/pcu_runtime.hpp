@@ -51,6 +51,7 @@ struct Ctx {
         hipEvent_t a, b;
     };
     bool profiling = false;
+    int matmul_engine = 0; // pcu_matmul_engine
     std::vector<Timing> timings;
     std::vector<hipEvent_t> event_pool;
     double prof_ms[PCU_KERNEL_COUNT] = {};

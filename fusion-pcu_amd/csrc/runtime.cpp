@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <unordered_set>
 
 namespace pcu {
 
@@ -441,14 +442,18 @@ pcu_status Ctx::resolve_timings()
         return st;
     if ((st = hip(hipStreamSynchronize(stream), "hipStreamSynchronize")))
         return st;
+    // Adjacent regions may share an event (the MatMul's prefilter/main/replay marks), so
+    // every event goes back to the pool once, or two later timers would share it.
+    std::unordered_set<hipEvent_t> returned;
     for (const Timing &t : timings) {
         float ms = 0.0f;
         if ((st = hip(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime")))
             return st;
         prof_ms[t.kernel] += ms;
         prof_n[t.kernel] += 1;
-        event_pool.push_back(t.a);
-        event_pool.push_back(t.b);
+        for (hipEvent_t e : {t.a, t.b})
+            if (returned.insert(e).second)
+                event_pool.push_back(e);
     }
     timings.clear();
     return PCU_OK;
@@ -486,7 +491,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
             x = take_event();
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, fault_words, prior,
-                                        profiling ? ev : nullptr);
+                                        profiling ? ev : nullptr, matmul_engine);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
     if (profiling) {
@@ -862,6 +867,19 @@ pcu_status pcu_program_end(pcu_ctx *ctx, pcu_fault *first_fault)
 uint32_t pcu_program_next_node(const pcu_ctx *ctx)
 {
     return ctx ? (uint32_t)reinterpret_cast<const Ctx *>(ctx)->nodes.size() : 0;
+}
+
+pcu_status pcu_ctx_set_matmul_engine(pcu_ctx *ctx, pcu_matmul_engine engine)
+{
+    if (!ctx)
+        return bad_ctx();
+    if (engine < PCU_MATMUL_AUTO || engine > PCU_MATMUL_MFMA_PRODUCTS)
+        return PCU_ERR_ARGUMENT;
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (engine == PCU_MATMUL_MFMA_PRODUCTS)
+        engine = PCU_MATMUL_AUTO; // F64 has no K=1 matrix form: AUTO is the same choice
+    c->matmul_engine = (int)engine;
+    return PCU_OK;
 }
 
 pcu_status pcu_profile_enable(pcu_ctx *ctx, int on)

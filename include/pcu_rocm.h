@@ -109,6 +109,22 @@ int pcu_abi_version(void);
 void *pcu_ctx_stream(pcu_ctx *ctx);
 pcu_status pcu_ctx_synchronize(pcu_ctx *ctx);
 
+/* Engine of the strict F32 MatMul's main kernel. Both give the same bits.
+ *  PCU_MATMUL_VALU: each product is a v_mul_f32 and each sum a v_add_f32.
+ *  PCU_MATMUL_MFMA_PRODUCTS: the matrix cores act as a multiplier array only
+ *   (v_mfma_f32_32x32x1_2b_f32, K = 1, +0 accumulator input): every element is one
+ *   product rounded once. The ordered sums stay separate v_add_f32 in k order, and no
+ *   sum is formed in the matrix core.
+ *  PCU_MATMUL_AUTO (default): MFMA products for F32; F64 always uses the vector unit.
+ * No counterpart in the reference, whose strict MatMul is one integer-emulated thread
+ * per cell (backends/rocm/tensor/strict_matmul/strict_matmul.rs:187-239). */
+typedef enum pcu_matmul_engine {
+    PCU_MATMUL_AUTO = 0,
+    PCU_MATMUL_VALU = 1,
+    PCU_MATMUL_MFMA_PRODUCTS = 2
+} pcu_matmul_engine;
+pcu_status pcu_ctx_set_matmul_engine(pcu_ctx *ctx, pcu_matmul_engine engine);
+
 /* ------------------------------------------------------------------- memory
  * Device buffers come from the context's stream-ordered pool (released memory is
  * retained for reuse); uploads and downloads go through the pinned staging buffer. */

@@ -307,10 +307,23 @@ def test_mse_ordered_sum_rounding_stress(ctx, pcu_pkg, dtype):
 # ------------------------------------------------------------------- MatMul
 
 
+ENGINES = ["valu", "mfma_products"]
+
+
+@pytest.fixture(params=ENGINES)
+def engine(request, ctx):
+    """Runs a MatMul test once per main-kernel engine of the F32 MatMul (F64 always uses
+    the vector unit); every engine must give the oracle's bits."""
+    ctx.set_matmul_engine(request.param)
+    yield request.param
+    ctx.set_matmul_engine("auto")
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 @pytest.mark.parametrize("shape", [(1, 1, 1), (2, 3, 2), (65, 3, 17), (128, 128, 128),
-                                   (129, 67, 255), (300, 257, 130), (512, 1024, 256)])
-def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape):
+                                   (129, 67, 255), (300, 257, 130), (512, 1024, 256),
+                                   (33, 1, 257), (1, 513, 1), (255, 17, 129)])
+def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape, engine):
     m, k, n = shape
     rng = np.random.default_rng(m * 7 + k * 3 + n)
     for tl in (False, True):
@@ -350,7 +363,7 @@ KIND = {"ArithmeticOverflow": 3, "ArithmeticUnderflow": 4, "InvalidFloatingOpera
 
 @pytest.mark.parametrize("case", json.load(open(os.path.join(GOLDEN, "tensor_kat.json")))["cases"],
                          ids=lambda c: f"{c['op']}-{c['dtype']}-{c['source']}")
-def test_reference_tensor_known_answers_on_gpu(ctx, pcu_pkg, case):
+def test_reference_tensor_known_answers_on_gpu(ctx, pcu_pkg, case, engine):
     fn, itype = _run_tensor_case(ctx, pcu_pkg, case)
     got, gf = _gpu_fault(pcu_pkg, fn)
     if case["fault"] is not None:
@@ -362,7 +375,7 @@ def test_reference_tensor_known_answers_on_gpu(ctx, pcu_pkg, case):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
-def test_matmul_fault_variants_parity(ctx, pcu_pkg, dtype):
+def test_matmul_fault_variants_parity(ctx, pcu_pkg, dtype, engine):
     """The C2 fault variants at 256^3: 0.1% of A set to 3.0e38 (Add overflow) and 0.1% of
     B set to NaN (Multiply invalid at the lowest cell), plus tiny operands (underflow)."""
     rng = np.random.default_rng(2024)
@@ -387,6 +400,34 @@ def test_matmul_fault_variants_parity(ctx, pcu_pkg, dtype):
             assert gf == _ofault(rf), (variant, policy, gf, rf)
             if rf is None:
                 np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_matmul_signed_zero_and_subnormal_products(ctx, pcu_pkg, policy, engine):
+    """Operands whose products are exact zeros of either sign, subnormal, or straddle the
+    smallest normal, with subnormal inputs on both sides: under every underflow policy the
+    F32 MatMul must give the oracle's bits and first fault (the matrix-core engine returns
+    +0 for a -0 product, which must never show in a result)."""
+    rng = np.random.default_rng(99 + policy)
+    m, k, n = 96, 70, 80
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    a[rng.random((m, k)) < 0.3] = np.float32(-0.0)
+    b[rng.random((k, n)) < 0.3] = np.float32(0.0)
+    a[::3] *= np.float32(2.0 ** -70)
+    b[:, ::5] *= np.float32(2.0 ** -60)
+    sub = np.array([1, 3, 0x7fffff, 0x400000, 0x12345], np.uint32).view(np.float32)
+    a[5, :5] = sub
+    b[:5, 7] = sub * np.float32(2.0 ** 100)
+    a[-1] = np.float32(-0.0)
+    for tl, tr in ((False, False), (True, True)):
+        aa = np.ascontiguousarray(a.T) if tl else a
+        bb = np.ascontiguousarray(b.T) if tr else b
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), tl, tr, policy).numpy())
+        ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+        assert gf == _ofault(rf), (policy, tl, tr, gf, rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
 # ------------------------------------------------------------------ program
