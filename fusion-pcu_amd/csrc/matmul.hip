@@ -140,7 +140,7 @@ __device__ __forceinline__ void load4(const T *__restrict__ p, int valid, T (&v)
 }
 
 template <typename T, bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(256) void k_strict_gemm(
+__global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
     int vec_c, unsigned long long *suspect)
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void k_strict_gemm(
         const int cur = kt & 1;
         if (kt + 1 < ktiles)
             fetch((kt + 1) * BK);
-#pragma unroll
+#pragma unroll(sizeof(T) == 4 ? BK : 2)
         for (int k = 0; k < BK; k++) {
             T a[8], b[8];
 #pragma unroll

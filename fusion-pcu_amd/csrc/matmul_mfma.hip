@@ -30,30 +30,38 @@ namespace pcu {
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-namespace mf {
-constexpr int BM = 128, BN = 128, BK = 16;
-constexpr int LDA = BM + 4, LDB = BN + 4; // row pitch of the k-major LDS tiles
-constexpr int kThreads = 256;              // 4 waves, each a 64x64 quarter of the tile
-}
+// Workgroup shape: WM x WN waves, each owning SM x SN output subtiles of 32 x 32; k-slabs
+// of BK are staged through double-buffered k-major LDS tiles.
+template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> struct MfmaCfg {
+    static constexpr int WM = WM_, WN = WN_, SM = SM_, SN = SN_, BK = BK_;
+    static constexpr int kWavesPerSimd = WAVES_PER_SIMD_; // occupancy the registers allow
+    static constexpr int BM = WM * SM * 32, BN = WN * SN * 32;
+    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int LDA = BM + 4, LDB = BN + 4; // row pitch of the k-major LDS tiles
+    static constexpr int EA = BM * BK / kThreads;    // A elements one thread stages per slab
+    static constexpr int EB = BN * BK / kThreads;
+    static_assert(EA % 4 == 0 && EB % 4 == 0, "staging moves whole float4s");
+};
 
-// 8 consecutive elements of a row-major operand at p; `valid` of them in bounds (the rest
+// E consecutive elements of a row-major operand at p; `valid` of them in bounds (the rest
 // read as +0: a zero product leaves every accumulator unchanged).
-template <bool VEC>
-__device__ __forceinline__ void load8(const float *__restrict__ p, int valid, float (&v)[8])
+template <int E, bool VEC>
+__device__ __forceinline__ void load_run(const float *__restrict__ p, int valid, float (&v)[E])
 {
-    if (VEC && valid >= 8) {
-        float4 q0 = *reinterpret_cast<const float4 *>(p);
-        float4 q1 = *reinterpret_cast<const float4 *>(p + 4);
-        v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-        v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+    if (VEC && valid >= E) {
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            const float4 x = reinterpret_cast<const float4 *>(p)[q];
+            v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+        }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+        for (int i = 0; i < E; i++)
             v[i] = i < valid ? p[i] : 0.0f;
     }
 }
 
-__device__ __forceinline__ int clamp_valid(int rem) { return rem < 0 ? 0 : (rem > 8 ? 8 : rem); }
+__device__ __forceinline__ int clamp_valid(int rem, int e) { return rem < 0 ? 0 : (rem > e ? e : rem); }
 
 // Output tile of workgroup `bid`: blocks are dealt round-robin to the 8 XCDs, so each XCD
 // is given one contiguous run of the tile order (its L2 then holds that run's panels),
@@ -72,70 +80,73 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &
     tn = (L % per_group) / gsize;
 }
 
-template <bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(mf::kThreads, 2) void k_strict_gemm_mfma(
+template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr,
     int check_risk, unsigned long long *suspect)
 {
-    using namespace mf;
-    __shared__ __align__(16) float As[2][BK][LDA];
-    __shared__ __align__(16) float Bs[2][BK][LDB];
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
+    constexpr int S = SM * SN, EA = Cfg::EA, EB = Cfg::EB;
+    __shared__ __align__(16) float As[2][BK][Cfg::LDA];
+    __shared__ __align__(16) float Bs[2][BK][Cfg::LDB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
-    float acc[2][2][16];
+    float acc[S][16];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int t = 0; t < S; t++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; r++)
+            acc[t][r] = 0.0f;
 
-    float ra[8], rb[8];
-    // Global -> registers for the k-slab starting at k0 (8 elements of each operand).
+    float ra[EA], rb[EB];
+    // Global -> registers for the k-slab starting at k0.
     auto fetch = [&](int k0) {
-        if (!TA) { // A is M x K: row m0 + tid/2, k0 + (tid&1)*8 .. +7
-            const int m = m0 + (tid >> 1), k = k0 + (tid & 1) * 8;
-            load8<VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k) : 0, ra);
-        } else {   // A is K x M: row k0 + tid/16, m0 + (tid%16)*8 .. +7
-            const int k = k0 + (tid >> 4), m = m0 + (tid & 15) * 8;
-            load8<VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m) : 0, ra);
+        if (!TA) { // A is M x K: BK/EA threads per row
+            const int m = m0 + tid / (BK / EA), k = k0 + (tid % (BK / EA)) * EA;
+            load_run<EA, VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k, EA) : 0, ra);
+        } else {   // A is K x M: BM/EA threads per k-row
+            const int k = k0 + tid / (BM / EA), m = m0 + (tid % (BM / EA)) * EA;
+            load_run<EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
         }
-        if (!TB) { // B is K x N: row k0 + tid/16, n0 + (tid%16)*8 .. +7
-            const int k = k0 + (tid >> 4), n = n0 + (tid & 15) * 8;
-            load8<VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n) : 0, rb);
-        } else {   // B is N x K: row n0 + tid/2, k0 + (tid&1)*8 .. +7
-            const int n = n0 + (tid >> 1), k = k0 + (tid & 1) * 8;
-            load8<VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k) : 0, rb);
+        if (!TB) { // B is K x N: BN/EB threads per k-row
+            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
+            load_run<EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
+        } else {   // B is N x K: BK/EB threads per row
+            const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
+            load_run<EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
         }
     };
     // Registers -> k-major LDS stage `buf`.
     auto stash = [&](int buf) {
         if (!TA) {
-            const int m = tid >> 1, k = (tid & 1) * 8;
+            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < EA; i++)
                 As[buf][k + i][m] = ra[i];
         } else {
-            const int k = tid >> 4, m = (tid & 15) * 8;
-            *reinterpret_cast<float4 *>(&As[buf][k][m]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-            *reinterpret_cast<float4 *>(&As[buf][k][m + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
+            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
+#pragma unroll
+            for (int q = 0; q < EA / 4; q++)
+                *reinterpret_cast<float4 *>(&As[buf][k][m + 4 * q]) =
+                    make_float4(ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
         }
         if (!TB) {
-            const int k = tid >> 4, n = (tid & 15) * 8;
-            *reinterpret_cast<float4 *>(&Bs[buf][k][n]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-            *reinterpret_cast<float4 *>(&Bs[buf][k][n + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
-        } else {
-            const int n = tid >> 1, k = (tid & 1) * 8;
+            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int q = 0; q < EB / 4; q++)
+                *reinterpret_cast<float4 *>(&Bs[buf][k][n + 4 * q]) =
+                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+        } else {
+            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
                 Bs[buf][k + i][n] = rb[i];
         }
     };
@@ -144,14 +155,6 @@ __global__ __launch_bounds__(mf::kThreads, 2) void k_strict_gemm_mfma(
 #pragma unroll
     for (int r = 0; r < 32; r++)
         zero[r] = 0.0f;
-
-    const int ktiles = (K + BK - 1) / BK;
-    if (ktiles > 0) {
-        fetch(0);
-        stash(0);
-    }
-    __syncthreads();
-    const int half = lane >> 5, col = lane & 31;
     auto mma = [&](float a, float b) {
         return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, zero, 0, 0, 0);
     };
@@ -164,109 +167,143 @@ __global__ __launch_bounds__(mf::kThreads, 2) void k_strict_gemm_mfma(
             c[r] = c[r] + p[16 + r];
         }
     };
+
+    const int ktiles = (K + BK - 1) / BK;
+    if (ktiles > 0) {
+        fetch(0);
+        stash(0);
+    }
+    __syncthreads();
+    const int half = lane >> 5, col = lane & 31;
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < ktiles)
             fetch((kt + 1) * BK);
-        // Software pipeline: one MFMA is always in flight while the vector unit folds the
-        // previous one (the group barriers ask the scheduler for exactly that alternation).
-        // Lanes 0-31 carry k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
-        float a0 = As[cur][half][wm + col], a1 = As[cur][half][wm + 32 + col];
-        float b0 = Bs[cur][half][wn + col], b1 = Bs[cur][half][wn + 32 + col];
-        v32f p = mma(a0, b0);
+        // Software pipeline: one MFMA is in flight while the vector unit folds the previous
+        // one (the group barriers ask the scheduler for that alternation). Lanes 0-31 carry
+        // k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
+        float a[SM], b[SN];
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+            a[i] = As[cur][half][wm + 32 * i + col];
+#pragma unroll
+        for (int j = 0; j < SN; j++)
+            b[j] = Bs[cur][half][wn + 32 * j + col];
+        v32f p = mma(a[0], b[0]);
 #pragma unroll 1
         for (int kk = 0; kk < BK - 2; kk += 2) {
-            const float na0 = As[cur][kk + 2 + half][wm + col];
-            const float na1 = As[cur][kk + 2 + half][wm + 32 + col];
-            const float nb0 = Bs[cur][kk + 2 + half][wn + col];
-            const float nb1 = Bs[cur][kk + 2 + half][wn + 32 + col];
-            v32f q = mma(a0, b1);
-            fold(acc[0][0], p);
-            p = mma(a1, b0);
-            fold(acc[0][1], q);
-            q = mma(a1, b1);
-            fold(acc[1][0], p);
-            p = mma(na0, nb0);
-            fold(acc[1][1], q);
+            float na[SM], nb[SN];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
+            for (int i = 0; i < SM; i++)
+                na[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
+#pragma unroll
+            for (int j = 0; j < SN; j++)
+                nb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
+#pragma unroll
+            for (int t = 0; t < S; t++) {
+                const v32f q = t + 1 < S ? mma(a[(t + 1) / SN], b[(t + 1) % SN]) : mma(na[0], nb[0]);
+                fold(acc[t], p);
+                p = q;
+            }
+#pragma unroll
+            for (int t = 0; t < S; t++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 32, 0); // 32 VALU (a fold)
             }
-            a0 = na0; a1 = na1; b0 = nb0; b1 = nb1;
+#pragma unroll
+            for (int i = 0; i < SM; i++)
+                a[i] = na[i];
+#pragma unroll
+            for (int j = 0; j < SN; j++)
+                b[j] = nb[j];
         }
-        {   // last k-pair of the stage: nothing further to issue
-            v32f q = mma(a0, b1);
-            fold(acc[0][0], p);
-            p = mma(a1, b0);
-            fold(acc[0][1], q);
-            q = mma(a1, b1);
-            fold(acc[1][0], p);
-            fold(acc[1][1], q);
+        // Last k-pair of the stage: nothing further to issue after its final subtile.
+#pragma unroll
+        for (int t = 0; t < S; t++) {
+            if (t + 1 < S) {
+                const v32f q = mma(a[(t + 1) / SN], b[(t + 1) % SN]);
+                fold(acc[t], p);
+                p = q;
+            } else {
+                fold(acc[t], p);
+            }
         }
         if (kt + 1 < ktiles)
             stash(cur ^ 1);
         __syncthreads();
     }
 
-    // Epilogue: lane owns column n0+wn+32j+col of rows m0+wm+32i+8(r/4)+4*half+(r%4).
+    // Epilogue: for subtile (i, j) the lane owns column n0+wn+32j+col of rows
+    // m0+wm+32i+8(r/4)+4*half+(r%4).
     uint64_t key = kNoFault;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int t = 0; t < S; t++) {
+        const int i = t / SN, j = t % SN;
         const int c = n0 + wn + 32 * j + col;
         const bool cin = c < N;
         const int cexp = (check_risk && cin) ? col_exp[c] : 0;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (!cin || row >= M)
-                    continue;
-                const float v = acc[i][j][r];
-                C[(size_t)row * N + c] = v;
-                bool bad = !finite_bits(v);
-                if (check_risk)
-                    bad |= row_exp[row] + cexp < thr;
-                if (bad) {
-                    const uint64_t cell = (uint64_t)row * N + c;
-                    key = cell < key ? cell : key;
-                }
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (!cin || row >= M)
+                continue;
+            const float v = acc[t][r];
+            C[(size_t)row * N + c] = v;
+            bool bad = !finite_bits(v);
+            if (check_risk)
+                bad |= row_exp[row] + cexp < thr;
+            if (bad) {
+                const uint64_t cell = (uint64_t)row * N + c;
+                key = cell < key ? cell : key;
             }
+        }
     }
     wave_record_fault(key, suspect);
 }
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <bool TA, bool TB>
-static void mfma_dispatch(hipStream_t s, dim3 grid, const float *A, const float *B, float *C,
-                          int M, int N, int K, const int *re, const int *ce, int thr, int risk,
+template <class Cfg, bool TA, bool TB>
+static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
+                          int K, const int *re, const int *ce, int thr, int risk,
                           unsigned long long *suspect)
 {
+    const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
+    const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    const dim3 block(mf::kThreads);
     if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
     else
-        hipLaunchKernelGGL((k_strict_gemm_mfma<TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
 }
+
+template <class Cfg>
+static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, const float *A,
+                        const float *B, float *C, const int *re, const int *ce, int thr,
+                        int risk, unsigned long long *suspect)
+{
+    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+}
+
+// 8 waves of 32 x 64 over a 128 x 128 tile, 127 VGPRs (4 waves per SIMD). On MI355X at
+// 4096^3 this measured ahead of 4 waves of 64 x 64 (2 waves per SIMD), 16 waves of
+// 32 x 32, a 256 x 128 tile, and BK = 32.
+using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C, const int *row_exp,
                                 const int *col_exp, int thr, int risk,
                                 unsigned long long *suspect)
 {
-    const dim3 grid((unsigned)(((M + mf::BM - 1) / mf::BM) * ((N + mf::BN - 1) / mf::BN)));
-    if (!ta && !tb) mfma_dispatch<false, false>(s, grid, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect);
-    else if (!ta && tb) mfma_dispatch<false, true>(s, grid, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect);
-    else if (ta && !tb) mfma_dispatch<true, false>(s, grid, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect);
-    else mfma_dispatch<true, true>(s, grid, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect);
+    mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect);
     return hipGetLastError();
 }
 
