@@ -11,6 +11,8 @@
 #include "pcu_device.hpp"
 #include "pcu_kernels.hpp"
 
+#include <limits.h>
+
 #pragma clang fp contract(off)
 
 namespace pcu {
@@ -526,170 +528,326 @@ __device__ __forceinline__ float from_bits<float>(uint32_t b) { return __uint_as
 template <>
 __device__ __forceinline__ double from_bits<double>(uint64_t b) { return __longlong_as_double((long long)b); }
 
-// One workgroup of 512 threads; thread t holds elements [base + P*t, base + P*t + P) of
-// each chunk of 512*P (P = 16 for binary32, 8 for binary64), and the next chunk is
-// fetched while the current one is scanned.
+// ----------------------------------------------------- ordered sum: pipeline
+// The squares are cut into chunks of 512*P elements (P = 16 for binary32, 8 for binary64;
+// thread t of a workgroup holds elements [base + P*t, base + P*t + P)).
+//  A  k_mse_chunk_sums       per-chunk sum in binary64: the prefix of these estimates
+//                            where the running total stands at each chunk start;
+//  B  k_mse_chunk_summaries  per chunk, in parallel, the summary (count added for an even
+//                            and an odd start) of the whole chunk inside one binade, for
+//                            the one or two binades the estimate allows;
+//  C  k_mse_ordered_walk     one workgroup walks the chunks in order: where a summary
+//                            exists for the running binade and does not reach its end,
+//                            the chunk folds in O(1); any other chunk (a binade crossing,
+//                            or an estimate that missed) is run exactly, element by
+//                            element in parallel, with the crossing steps as real Adds.
+// The estimate only decides how fast a chunk goes, never its value.
+
+struct ChunkSummary {
+    uint64_t r0, r1;   // count added starting from an even / odd count
+    int32_t ue;        // quantum exponent the summary was made for (kNoPhase: none)
+    uint32_t pad;
+};
+constexpr int32_t kNoPhase = INT32_MIN;
+constexpr int kWalkBatch = kSumThreads / 2; // chunks whose summaries are staged per pass
+
+template <typename T> __device__ __forceinline__ uint64_t sum_chunk_len() { return (uint64_t)kSumThreads * SumBits<T>::kPer; }
+
+__device__ __forceinline__ uint64_t sum_limit(const unsigned long long *fault, uint64_t n)
+{
+    // Elements at or after the first Subtract/Multiply fault are never summed.
+    const uint64_t w = __atomic_load_n(fault, __ATOMIC_RELAXED);
+    return w == kNoFault ? n : (w >> 3) / 3;
+}
+
+// Quantum exponent of the binade a total of about x lies in.
 template <typename T>
-__global__ __launch_bounds__(kSumThreads) void k_mse_ordered_sum(
-    const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
-    unsigned long long *fault)
+__device__ __forceinline__ int32_t phase_ue_of(double x)
+{
+    using B = SumBits<T>;
+    const double min_normal = ldexp(1.0, B::kQmin + B::kFrac);
+    if (!(x >= min_normal))
+        return B::kQmin;
+    int e;
+    (void)frexp(x, &e); // x = f * 2^e, f in [1/2, 1): floor(log2 x) = e - 1
+    return e - 1 - B::kFrac;
+}
+
+// Thread t's P elements of the chunk at base (elements at or past limit read as 0).
+template <typename T>
+__device__ __forceinline__ void load_chunk(const typename SumBits<T>::U *__restrict__ src,
+                                           bool vec_ok, uint64_t base, uint64_t limit, int tid,
+                                           typename SumBits<T>::U (&dst)[SumBits<T>::kPer])
 {
     using U = typename SumBits<T>::U;
-    constexpr int kSumPer = SumBits<T>::kPer;
-    constexpr uint64_t kSumChunk = (uint64_t)kSumThreads * kSumPer;
+    constexpr int P = SumBits<T>::kPer;
+    const uint64_t first = base + (uint64_t)tid * P;
+    if (vec_ok && base + sum_chunk_len<T>() <= limit) {
+        const uint4 *v = reinterpret_cast<const uint4 *>(src + first);
+        constexpr int per16 = 16 / sizeof(U);
+#pragma unroll
+        for (int q = 0; q < P / per16; q++) {
+            const uint4 x = v[q];
+            const U *xs = reinterpret_cast<const U *>(&x);
+#pragma unroll
+            for (int j = 0; j < per16; j++)
+                dst[q * per16 + j] = xs[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < P; j++)
+            dst[j] = first + j < limit ? src[first + j] : (U)0;
+    }
+}
+
+// Ordered composition over the workgroup: every thread gets the summary of all threads
+// before it (excl) and of the whole workgroup (total).
+__device__ __forceinline__ void block_scan(SumScan mine, int lane, int wave, SumScan *wave_tot,
+                                           SumScan &excl, SumScan &total)
+{
+    constexpr int kWaves = kSumThreads / 64;
+    SumScan inc = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const SumScan o = scan_shfl_up(inc, d);
+        if (lane >= d)
+            inc = scan_compose(o, inc);
+    }
+    SumScan lane_excl = scan_shfl_up(inc, 1);
+    if (lane == 0)
+        lane_excl = scan_identity();
+    if (lane == 63)
+        wave_tot[wave] = inc;
+    __syncthreads();
+    // Every wave scans the per-wave totals on its first lanes (one LDS read each).
+    SumScan wt = lane < kWaves ? wave_tot[lane] : scan_identity();
+#pragma unroll
+    for (int d = 1; d < kWaves; d <<= 1) {
+        const SumScan o = scan_shfl_up(wt, d);
+        if (lane >= d)
+            wt = scan_compose(o, wt);
+    }
+    total.r0 = __shfl(wt.r0, kWaves - 1, 64);
+    total.r1 = __shfl(wt.r1, kWaves - 1, 64);
+    total.p = __shfl(wt.p, kWaves - 1, 64);
+    const int pw = wave > 0 ? wave - 1 : 0;
+    SumScan before;
+    before.r0 = __shfl(wt.r0, pw, 64);
+    before.r1 = __shfl(wt.r1, pw, 64);
+    before.p = __shfl(wt.p, pw, 64);
+    if (wave == 0)
+        before = scan_identity();
+    excl = scan_compose(before, lane_excl);
+}
+
+// Exact fold of one chunk from the phase (ue, m, mmax): the scan finds the first step that
+// would reach the binade's end, that step runs as a real checked Add, and the rest of the
+// chunk is scanned again in the new binade. Returns false when an Add faulted (recorded).
+template <typename T>
+__device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, bool vec_ok,
+                            uint64_t base, uint64_t limit, int policy,
+                            unsigned long long *fault, int &ue, uint64_t &m, uint64_t &mmax,
+                            SumScan *wave_tot, uint64_t *wave_key,
+                            typename SumBits<T>::U *s_total, int *s_stop)
+{
+    using U = typename SumBits<T>::U;
+    constexpr int P = SumBits<T>::kPer;
+    constexpr int kWaves = kSumThreads / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    U cur[P];
+    load_chunk<T>(src, vec_ok, base, limit, tid, cur);
+    const uint64_t first = base + (uint64_t)tid * P;
+    uint64_t start = base; // first element of the chunk not yet folded into m
+    for (;;) {
+        SumScan mine = scan_identity();
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            uint64_t nn;
+            uint32_t cls;
+            sum_elem<T>(cur[j], ue, nn, cls);
+            if (first + j >= start && first + j < limit)
+                mine = scan_compose(mine, scan_elem(nn, cls));
+        }
+        SumScan before, total;
+        block_scan(mine, lane, wave, wave_tot, before, total);
+        // Walk this thread's elements from its exact starting state.
+        const uint32_t p0 = (uint32_t)(m & 1u);
+        uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+        uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
+        uint64_t key = kNoFault, key_m = 0;
+        U key_bits = 0;
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            uint64_t nn;
+            uint32_t cls;
+            sum_elem<T>(cur[j], ue, nn, cls);
+            if (first + j >= start && first + j < limit && key == kNoFault) {
+                const uint64_t r = sum_step(nn, cls, pt);
+                if (cls == kRForce || mt + r >= mmax) {
+                    key = first + j;
+                    key_bits = cur[j];
+                    key_m = mt;
+                } else {
+                    mt += r;
+                    pt = (pt + (uint32_t)r) & 1u;
+                }
+            }
+        }
+        const uint64_t wk = wave_min_u64(key);
+        if (lane == 0)
+            wave_key[wave] = wk;
+        __syncthreads();
+        const uint64_t cross = wave_min_u64(lane < kWaves ? wave_key[lane] : kNoFault);
+        if (cross == kNoFault) {
+            m = sat_add(m, p0 ? total.r1 : total.r0);
+            return true;
+        }
+        if (key == cross) {
+            // The crossing step, executed and checked as the contract's Add.
+            const T acc = from_bits<T>(sum_bits<T>(ue, key_m));
+            const T s_i = from_bits<T>(key_bits);
+            const T r = acc + s_i;
+            const uint32_t kind = classify_add(acc, s_i, r, policy);
+            if (kind != kOk) {
+                atomicMin(fault, (unsigned long long)pack_fault(3 * cross + 2, kind));
+                *s_stop = 1;
+            } else {
+                *s_stop = 0;
+                *s_total = (U)bits_of(r);
+            }
+        }
+        __syncthreads();
+        if (*s_stop)
+            return false;
+        sum_phase<T>(*s_total, ue, m, mmax);
+        start = cross + 1;
+    }
+}
+
+// A: chunk sums in binary64 (order inside a chunk does not matter: only an estimate).
+template <typename T>
+__global__ __launch_bounds__(256) void k_mse_chunk_sums(const T *__restrict__ sq, uint64_t n,
+                                                        const unsigned long long *fault,
+                                                        double *__restrict__ chunk_sum)
+{
+    __shared__ double part[4];
+    const uint64_t limit = sum_limit(fault, n);
+    const uint64_t base = (uint64_t)blockIdx.x * sum_chunk_len<T>();
+    const uint64_t end = base + sum_chunk_len<T>() < limit ? base + sum_chunk_len<T>() : limit;
+    double acc = 0.0;
+    for (uint64_t i = base + threadIdx.x; i < end; i += 256)
+        acc += (double)sq[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0)
+        part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        chunk_sum[blockIdx.x] = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// B: summary of chunk blockIdx.x for candidate blockIdx.y (0: the binade of the estimate
+// less 1/512 of it, 1: plus 1/512; the second is skipped when both agree).
+template <typename T>
+__global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
+    const T *__restrict__ sq, uint64_t n, const unsigned long long *fault,
+    const double *__restrict__ chunk_sum, ChunkSummary *__restrict__ summ)
+{
+    using U = typename SumBits<T>::U;
+    constexpr int P = SumBits<T>::kPer;
+    __shared__ SumScan wave_tot[kSumThreads / 64];
+    __shared__ double part[kSumThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t c = blockIdx.x;
+    const uint64_t limit = sum_limit(fault, n);
+    double pre = 0.0;
+    for (uint64_t j = tid; j < c; j += kSumThreads)
+        pre += chunk_sum[j];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        pre += __shfl_xor(pre, off, 64);
+    if (lane == 0)
+        part[wave] = pre;
+    __syncthreads();
+    pre = 0.0;
+    for (int w = 0; w < kSumThreads / 64; w++)
+        pre += part[w];
+    const int32_t lo = phase_ue_of<T>(pre * (1.0 - 1.0 / 512)), hi = phase_ue_of<T>(pre * (1.0 + 1.0 / 512));
+    ChunkSummary *out = summ + 2 * c + blockIdx.y;
+    if (blockIdx.y == 1 && hi == lo) {
+        if (tid == 0)
+            *out = ChunkSummary{0, 0, kNoPhase, 0};
+        return;
+    }
+    const int ue = blockIdx.y ? hi : lo;
+    const U *src = reinterpret_cast<const U *>(sq);
+    U cur[P];
+    const uint64_t base = c * sum_chunk_len<T>();
+    load_chunk<T>(src, ((uintptr_t)sq & 15u) == 0, base, limit, tid, cur);
+    const uint64_t first = base + (uint64_t)tid * P;
+    SumScan mine = scan_identity();
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        uint64_t nn;
+        uint32_t cls;
+        sum_elem<T>(cur[j], ue, nn, cls);
+        if (first + j < limit)
+            mine = scan_compose(mine, scan_elem(nn, cls));
+    }
+    SumScan excl, total;
+    block_scan(mine, lane, wave, wave_tot, excl, total);
+    if (tid == 0)
+        *out = ChunkSummary{total.r0, total.r1, ue, 0};
+}
+
+// C: the ordered walk (one workgroup), then total (/) count.
+template <typename T>
+__global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
+    const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
+    unsigned long long *fault, const ChunkSummary *__restrict__ summ)
+{
+    using U = typename SumBits<T>::U;
     __shared__ SumScan wave_tot[kSumThreads / 64];
     __shared__ uint64_t wave_key[kSumThreads / 64];
+    __shared__ ChunkSummary staged[2 * kWalkBatch];
     __shared__ uint64_t s_limit;
-    __shared__ U s_total;     // total after a crossing step
+    __shared__ U s_total;
     __shared__ int s_stop;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) {
-        // Elements at or after the first Subtract/Multiply fault are never summed.
-        const uint64_t w = __atomic_load_n(fault, __ATOMIC_RELAXED);
-        s_limit = w == kNoFault ? n : (w >> 3) / 3;
-    }
+    const int tid = threadIdx.x;
+    if (tid == 0)
+        s_limit = sum_limit(fault, n);
     __syncthreads();
     const uint64_t limit = s_limit;
     const U *src = reinterpret_cast<const U *>(sq);
     const bool vec_ok = ((uintptr_t)sq & 15u) == 0;
+    const uint64_t L = sum_chunk_len<T>();
+    const uint64_t chunks = (limit + L - 1) / L;
 
     int ue;
     uint64_t m, mmax;
     sum_phase<T>((U)0, ue, m, mmax); // the total starts at +0
-
-    U cur[kSumPer], nxt[kSumPer];
-    auto fetch = [&](uint64_t base, U (&dst)[kSumPer]) {
-        const uint64_t first = base + (uint64_t)tid * kSumPer;
-        if (vec_ok && base + kSumChunk <= limit) {
-            const uint4 *v = reinterpret_cast<const uint4 *>(src + first);
-            constexpr int per16 = 16 / sizeof(U);
-#pragma unroll
-            for (int q = 0; q < kSumPer / per16; q++) {
-                uint4 x = v[q];
-                const U *xs = reinterpret_cast<const U *>(&x);
-#pragma unroll
-                for (int j = 0; j < per16; j++)
-                    dst[q * per16 + j] = xs[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < kSumPer; j++)
-                dst[j] = first + j < limit ? src[first + j] : (U)0;
-        }
-    };
-
-    if (limit > 0)
-        fetch(0, cur);
-    for (uint64_t base = 0; base < limit; base += kSumChunk) {
-        if (base + kSumChunk < limit)
-            fetch(base + kSumChunk, nxt);
-        const uint64_t first = base + (uint64_t)tid * kSumPer;
-        uint64_t start = base; // first element of the chunk not yet folded into m
-        for (;;) {
-            // Thread summary over its live elements.
-            SumScan mine = scan_identity();
-#pragma unroll
-            for (int j = 0; j < kSumPer; j++) {
-                uint64_t nn;
-                uint32_t cls;
-                sum_elem<T>(cur[j], ue, nn, cls);
-                const bool live = first + j >= start && first + j < limit;
-                if (live)
-                    mine = scan_compose(mine, scan_elem(nn, cls));
-            }
-            // Inclusive scan over the wave, then over the waves.
-            SumScan inc = mine;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                SumScan o = scan_shfl_up(inc, d);
-                if (lane >= d)
-                    inc = scan_compose(o, inc);
-            }
-            SumScan excl = scan_shfl_up(inc, 1);
-            if (lane == 0)
-                excl = scan_identity();
-            if (lane == 63)
-                wave_tot[wave] = inc;
-            __syncthreads();
-            // Every wave scans the per-wave totals on its first lanes (one LDS read each).
-            constexpr int kWaves = kSumThreads / 64;
-            SumScan wt = lane < kWaves ? wave_tot[lane] : scan_identity();
-#pragma unroll
-            for (int d = 1; d < kWaves; d <<= 1) {
-                SumScan o = scan_shfl_up(wt, d);
-                if (lane >= d)
-                    wt = scan_compose(o, wt);
-            }
-            SumScan total, before;
-            total.r0 = __shfl(wt.r0, kWaves - 1, 64);
-            total.r1 = __shfl(wt.r1, kWaves - 1, 64);
-            total.p = __shfl(wt.p, kWaves - 1, 64);
-            const int pw = wave > 0 ? wave - 1 : 0;
-            before.r0 = __shfl(wt.r0, pw, 64);
-            before.r1 = __shfl(wt.r1, pw, 64);
-            before.p = __shfl(wt.p, pw, 64);
-            if (wave == 0)
-                before = scan_identity();
-            before = scan_compose(before, excl);
-            // Walk this thread's elements from its exact starting state.
+    for (uint64_t c0 = 0; c0 < chunks; c0 += kWalkBatch) {
+        const uint64_t c1 = c0 + kWalkBatch < chunks ? c0 + kWalkBatch : chunks;
+        __syncthreads(); // everyone is done with the previous batch
+        if (c0 * 2 + tid < c1 * 2)
+            staged[tid] = summ[c0 * 2 + tid];
+        __syncthreads();
+        for (uint64_t c = c0; c < c1; c++) {
+            // Uniform across the workgroup: every thread reads the same staged entries.
+            const ChunkSummary a = staged[2 * (c - c0)], b = staged[2 * (c - c0) + 1];
             const uint32_t p0 = (uint32_t)(m & 1u);
-            uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
-            uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
-            uint64_t key = kNoFault;
-            U key_bits = 0;
-            uint64_t key_m = 0;
-#pragma unroll
-            for (int j = 0; j < kSumPer; j++) {
-                uint64_t nn;
-                uint32_t cls;
-                sum_elem<T>(cur[j], ue, nn, cls);
-                const bool live = first + j >= start && first + j < limit;
-                if (live && key == kNoFault) {
-                    const uint64_t r = sum_step(nn, cls, pt);
-                    if (cls == kRForce || mt + r >= mmax) {
-                        key = first + j;
-                        key_bits = cur[j];
-                        key_m = mt;
-                    } else {
-                        mt += r;
-                        pt = (pt + (uint32_t)r) & 1u;
-                    }
+            const bool ha = a.ue == ue, hb = b.ue == ue;
+            if (ha || hb) {
+                const uint64_t r = ha ? (p0 ? a.r1 : a.r0) : (p0 ? b.r1 : b.r0);
+                if (m + r < mmax) {
+                    m += r;
+                    continue;
                 }
             }
-            const uint64_t wk = wave_min_u64(key);
-            if (lane == 0)
-                wave_key[wave] = wk;
-            __syncthreads();
-            const uint64_t cross = wave_min_u64(lane < kWaves ? wave_key[lane] : kNoFault);
-            if (cross == kNoFault) {
-                m = sat_add(m, p0 ? total.r1 : total.r0);
-                break;
-            }
-            if (key == cross) {
-                // The crossing step, executed and checked as the contract's Add.
-                const T acc = from_bits<T>(sum_bits<T>(ue, key_m));
-                const T s_i = from_bits<T>(key_bits);
-                const T r = acc + s_i;
-                const uint32_t kind = classify_add(acc, s_i, r, policy);
-                if (kind != kOk) {
-                    atomicMin(fault, (unsigned long long)pack_fault(3 * cross + 2, kind));
-                    s_stop = 1;
-                } else {
-                    s_stop = 0;
-                    s_total = (U)bits_of(r);
-                }
-            }
-            __syncthreads();
-            if (s_stop)
+            if (!exact_chunk<T>(src, vec_ok, c * L, limit, policy, fault, ue, m, mmax, wave_tot,
+                                wave_key, &s_total, &s_stop))
                 return;
-            sum_phase<T>(s_total, ue, m, mmax);
-            start = cross + 1;
-        }
-        if (base + kSumChunk < limit) {
-#pragma unroll
-            for (int j = 0; j < kSumPer; j++)
-                cur[j] = nxt[j];
         }
     }
     if (limit < n || tid != 0)
@@ -855,32 +1013,54 @@ hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const
                       : sgd_t<double>(s, n, w, g, rate, out, policy, fault);
 }
 
+// Scratch of one MSE call: the squares, then the chunk sums and the chunk summaries.
+static inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
 template <typename T>
-static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t, void *squares,
+static size_t mse_chunks(uint64_t n)
+{
+    const uint64_t L = (uint64_t)kSumThreads * SumBits<T>::kPer;
+    return (size_t)((n + L - 1) / L);
+}
+
+size_t mse_scratch_bytes(int dtype, uint64_t n)
+{
+    const size_t es = dtype == 0 ? 4 : 8;
+    const size_t chunks = dtype == 0 ? mse_chunks<float>(n) : mse_chunks<double>(n);
+    return round256(n * es) + round256(chunks * sizeof(double)) +
+           round256(2 * chunks * sizeof(ChunkSummary));
+}
+
+template <typename T>
+static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t, void *scratch,
                         T count, void *out, int policy, unsigned long long *fault)
 {
     constexpr int Wd = Vec<T>::width;
-    bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
-    unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
+    char *base = (char *)scratch;
+    T *squares = (T *)base;
+    const size_t chunks = mse_chunks<T>(n);
+    double *chunk_sum = (double *)(base + round256(n * sizeof(T)));
+    ChunkSummary *summ = (ChunkSummary *)((char *)chunk_sum + round256(chunks * sizeof(double)));
+    const bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
+    const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
+        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault);
     else
-        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)squares, n, policy, fault);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return e;
-    hipLaunchKernelGGL((k_mse_ordered_sum<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault);
+        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault);
+    hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)chunks), dim3(256), 0, s, (const T *)squares, n, (const unsigned long long *)fault, chunk_sum);
+    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_sum, summ);
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const ChunkSummary *)summ);
     return hipGetLastError();
 }
 
 hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                      void *squares, double count, void *out, int policy,
+                      void *scratch, double count, void *out, int policy,
                       unsigned long long *fault)
 {
     if (n == 0)
         return hipErrorInvalidValue;
-    return dtype == 0 ? mse_t<float>(s, n, p, t, squares, (float)count, out, policy, fault)
-                      : mse_t<double>(s, n, p, t, squares, count, out, policy, fault);
+    return dtype == 0 ? mse_t<float>(s, n, p, t, scratch, (float)count, out, policy, fault)
+                      : mse_t<double>(s, n, p, t, scratch, count, out, policy, fault);
 }
 
 } // namespace pcu

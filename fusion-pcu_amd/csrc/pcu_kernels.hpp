@@ -23,9 +23,11 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                            unsigned long long *fault_add, unsigned long long *fault_relu);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
                       double rate, void *out, int policy, unsigned long long *fault);
-// `squares` is n elements of scratch; `count` is the element count rounded to the dtype.
+// `scratch` holds mse_scratch_bytes(dtype, n) bytes; `count` is the element count
+// rounded to the dtype.
+size_t mse_scratch_bytes(int dtype, uint64_t n);
 hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                      void *squares, double count, void *out, int policy,
+                      void *scratch, double count, void *out, int policy,
                       unsigned long long *fault);
 
 // Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.

@@ -652,7 +652,7 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
         side_pending = true;
     }
     void *sq = nullptr;
-    if ((st = scratch(n * dsize(dtype), s, &sq)))
+    if ((st = scratch(mse_scratch_bytes(dtype, n), s, &sq)))
         return st;
     hipEvent_t t0 = timer_start(s);
     if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word),
