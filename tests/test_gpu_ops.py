@@ -304,6 +304,24 @@ def test_mse_ordered_sum_rounding_stress(ctx, pcu_pkg, dtype):
                 assert _bits(got).item() == _bits(ref).item(), (n, i, got, ref)
 
 
+def test_mse_ordered_sum_estimate_misses(ctx, pcu_pkg):
+    """The ordered sum steps over whole chunks using summaries made for the binade that a
+    binary64 estimate of the running total predicts. Here the binary32 total sits at
+    5792^2 = 2^25 - 7168 and every further square (0.99^2 < half an ulp) is absorbed,
+    while the exact sum keeps growing past 2^25 (1 + 1/512): from about the ninth chunk on,
+    no summary matches the true binade and every chunk takes the exact path. The result
+    must still be the dependent chain's, bit for bit."""
+    n = 150_000
+    p = np.full(n, 0.99, np.float32)
+    p[0] = np.float32(5792.0)
+    t = np.zeros(n, np.float32)
+    got = ctx.strict_mse(ctx.upload(p), ctx.upload(t)).numpy()
+    ref, rf = oracle.mse(p, t)
+    assert rf is None
+    assert _bits(got).item() == _bits(ref).item()
+    assert ref * np.float32(n) == np.float32(5792.0 ** 2)  # the total never moved
+
+
 # ------------------------------------------------------------------- MatMul
 
 
