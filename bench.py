@@ -109,9 +109,34 @@ def bench_sgd(pkg, ctx, n, steps, warmup):
             "kernel_hbm_frac": 12.0 * n / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def bench_mlp(pkg, ctx, steps, warmup):
+def bench_native_matmul(pkg, ctx, m, k, n, dtype, steps, warmup):
+    """Native (BackendDefined) MatMul: matrix-core accumulation for F32."""
+    from fusion_pcu_amd import synthetic as syn
+    da = ctx.upload(syn.uniform(11, (m, k), dtype))
+    db = ctx.upload(syn.uniform(12, (k, n), dtype))
+    dc = ctx.empty((m, n), dtype)
+    for _ in range(warmup):
+        ctx.native_matmul(da, db, out=dc)
+    ctx.synchronize()
+    ctx.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.native_matmul(da, db, out=dc)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    k_ms, k_n = ctx.kernel_time("native_gemm")
+    ctx.profile(False)
+    for x in (da, db, dc):
+        x.free()
+    avg = k_ms / max(k_n, 1)
+    return {"gflops": 2.0 * m * n * k / ((t1 - t0) / steps) / 1e9, "kernel_avg_ms": avg,
+            "kernel_tflops": 2.0 * m * n * k / (avg * 1e-3) / 1e12}
+
+
+def bench_mlp(pkg, ctx, steps, warmup, native=False):
     """C5: strict F32 MLP 1024->4096->4096->1024, batch 4096, lr 1e-3, Xavier weights,
-    inputs and weights resident; one step = forward, MSE, backward, three SGD updates."""
+    inputs and weights resident; one step = forward, MSE, backward, three SGD updates.
+    ``native`` captures the same step with flag(native_compound) (Boundary mode)."""
     from fusion_pcu_amd import graph as G
     from fusion_pcu_amd import synthetic as syn
     dims, batch = (1024, 4096, 4096, 1024), 4096
@@ -119,7 +144,7 @@ def bench_mlp(pkg, ctx, steps, warmup):
     y = G.PcuTensor(ctx.upload(syn.uniform(52, (batch, dims[3]), np.float32)))
     ws = [G.PcuTensor(ctx.upload(syn.xavier_uniform(53 + i, dims[i], dims[i + 1], np.float32)))
           for i in range(3)]
-    step = G.mlp_training_step(1e-3)
+    step = G.mlp_training_step(1e-3, native=native)
     for _ in range(warmup):
         *ws, loss = step(x, *ws, y)
     ctx.synchronize()
@@ -130,7 +155,8 @@ def bench_mlp(pkg, ctx, steps, warmup):
     ctx.synchronize()
     t1 = time.perf_counter()
     kern = {k: ctx.kernel_time(k) for k in ("strict_gemm", "gemm_prefilter", "gemm_replay",
-                                            "sgd", "binary", "relu", "relu_backward", "mse")}
+                                            "sgd", "binary", "relu", "relu_backward", "mse",
+                                            "native_gemm", "native_sgd", "native_mse")}
     ctx.profile(False)
     flops = 2.0 * batch * (dims[0] * dims[1] + dims[1] * dims[2] + dims[2] * dims[3]) * 3 \
         - 2.0 * batch * dims[0] * dims[1]  # no input-gradient MatMul for X
@@ -139,9 +165,10 @@ def bench_mlp(pkg, ctx, steps, warmup):
         "steps_per_s": 1e3 / ms,
         "ms_per_step": ms,
         "matmul_gflop_per_step": flops / 1e9,
-        "gemm_ms_per_step": kern["strict_gemm"][0] / steps,
-        "mse_ms_per_step": kern["mse"][0] / steps,
-        "elementwise_ms_per_step": sum(kern[k][0] for k in ("sgd", "binary", "relu", "relu_backward")) / steps,
+        "gemm_ms_per_step": (kern["native_gemm"] if native else kern["strict_gemm"])[0] / steps,
+        "mse_ms_per_step": (kern["native_mse"] if native else kern["mse"])[0] / steps,
+        "elementwise_ms_per_step": sum(kern[k][0] for k in ("sgd", "binary", "relu", "relu_backward",
+                                                            "native_sgd")) / steps,
         "loss": float(loss.numpy()),
     }
 
@@ -239,6 +266,11 @@ def main() -> int:
         if not args.no_extra:
             log("strict F32 MLP training step (C5)")
             extra["mlp_c5"] = bench_mlp(pkg, ctx, max(5, args.steps), 2)
+            log("native (BackendDefined) F32 MatMul 4096^3")
+            extra["native_f32_matmul_4096"] = bench_native_matmul(pkg, ctx, M, K, N, np.float32,
+                                                                  args.steps, args.warmup)
+            log("native (BackendDefined) C5 MLP training step")
+            extra["mlp_c5_native"] = bench_mlp(pkg, ctx, max(5, args.steps), 2, native=True)
             log("strict F32 MatMul 4096^3, vector-unit engine")
             ctx.set_matmul_engine("valu")
             v = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup)

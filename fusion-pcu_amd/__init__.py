@@ -337,3 +337,37 @@ class Context:
         self._call(self._lib.pcu_strict_mse, dtype_code(p.dtype), p.size, p.ptr, t.ptr,
                    out.ptr, int(policy))
         return out
+
+    # ------------------------------------------------ native compound arithmetic
+    # Explicitly permitted native compounds (Boundary + BackendDefined): backend-defined
+    # order, contraction and special values; no arithmetic fault is raised.
+    def native_matmul(self, a: DeviceArray, b: DeviceArray, transpose_left=False,
+                      transpose_right=False, out: Optional[DeviceArray] = None):
+        if len(a.shape) != 2 or len(b.shape) != 2 or a.dtype != b.dtype:
+            raise PcuExecutionError(_abi.PCU_ERR_SHAPE, f"MatMulShape {a.shape} x {b.shape}")
+        rows, inner = (a.shape[1], a.shape[0]) if transpose_left else a.shape
+        inner_b, cols = (b.shape[1], b.shape[0]) if transpose_right else b.shape
+        if inner != inner_b:
+            raise PcuExecutionError(_abi.PCU_ERR_SHAPE, f"MatMulShape {a.shape} x {b.shape}")
+        if out is None:
+            out = self.empty((rows, cols), a.dtype)
+        self.check(self._lib.pcu_native_matmul(self.handle, dtype_code(a.dtype), rows, inner, cols,
+                                               int(transpose_left), int(transpose_right), a.ptr,
+                                               b.ptr, out.ptr))
+        return out
+
+    def native_mse(self, p: DeviceArray, t: DeviceArray, out=None):
+        if out is None:
+            out = self.empty((), p.dtype)
+        self.check(self._lib.pcu_native_mse(self.handle, dtype_code(p.dtype), p.size, p.ptr, t.ptr,
+                                            out.ptr))
+        return out
+
+    def native_sgd(self, w: DeviceArray, g: DeviceArray, learning_rate: float, contracted=False,
+                   out=None):
+        if out is None:
+            out = self.empty(w.shape, w.dtype)
+        self.check(self._lib.pcu_native_sgd(self.handle, dtype_code(w.dtype), w.size, w.ptr, g.ptr,
+                                            float(np.float32(learning_rate)), int(contracted),
+                                            out.ptr))
+        return out

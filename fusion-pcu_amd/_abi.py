@@ -72,6 +72,9 @@ SIGNATURES = {
     "pcu_checked_add_relu": (_i32, [_vp, _i32, _u64, _vp, _vp, _vp, _i32, _FP]),
     "pcu_strict_sgd": (_i32, [_vp, _i32, _u64, _vp, _vp, _f32, _vp, _i32, _FP]),
     "pcu_strict_mse": (_i32, [_vp, _i32, _u64, _vp, _vp, _vp, _i32, _FP]),
+    "pcu_native_matmul": (_i32, [_vp, _i32, _u64, _u64, _u64, _i32, _i32, _vp, _vp, _vp]),
+    "pcu_native_mse": (_i32, [_vp, _i32, _u64, _vp, _vp, _vp]),
+    "pcu_native_sgd": (_i32, [_vp, _i32, _u64, _vp, _vp, _f32, _i32, _vp]),
     "pcu_program_begin": (_i32, [_vp]),
     "pcu_program_end": (_i32, [_vp, _FP]),
     "pcu_program_next_node": (_u32, [_vp]),
@@ -80,6 +83,15 @@ SIGNATURES = {
     "pcu_profile_enable": (_i32, [_vp, _i32]),
     "pcu_profile_read": (_i32, [_vp, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]),
 }
+
+
+class NumericalOptions(ctypes.Structure):
+    """pcu_numerical_options (PcuNumericalOptions, core/numerical/numerical.rs:71-78)."""
+    _fields_ = [
+        ("compound_arithmetic", ctypes.c_uint32),  # 0 Checked, 1 BackendDefined
+        ("precision", ctypes.c_uint32),            # 0 Preserve, 1 BackendOptimized
+        ("reproducibility", ctypes.c_uint32),      # 0 Unspecified, 1 PortableV1
+    ]
 
 
 class NodeDesc(ctypes.Structure):
@@ -96,6 +108,8 @@ class NodeDesc(ctypes.Structure):
         ("rank", ctypes.c_uint32),
         ("value_bits", ctypes.c_uint64),
         ("shape", ctypes.c_uint64 * 8),
+        ("options", NumericalOptions),
+        ("reserved", ctypes.c_uint32),
     ]
 
 
@@ -115,6 +129,8 @@ SIGNATURES.update({
     "pcu_graph_sgd_update": (_i32, [_vp, _u32, _u32, _f32, _U32P]),
     "pcu_graph_set_underflow_policy": (_i32, [_vp, _u32, _i32]),
     "pcu_graph_set_value_numerical_mode": (_i32, [_vp, _u32, _i32]),
+    "pcu_graph_set_numerical_options": (_i32, [_vp, ctypes.POINTER(NumericalOptions)]),
+    "pcu_graph_set_value_numerical_options": (_i32, [_vp, _u32, ctypes.POINTER(NumericalOptions)]),
     "pcu_graph_backward_mse": (_i32, [_vp, _u32, _U32P, _u32]),
     "pcu_graph_backward_mse_for_targets": (_i32, [_vp, _u32, _u32, _U32P, _U32P]),
     "pcu_graph_node_count": (_u32, [_vp]),
@@ -135,6 +151,7 @@ GRAPH_OPS = ["Input", "Uniform", "Add", "Sub", "Mul", "Div", "SgdUpdate", "MatMu
 KERNEL_IDS = {
     "strict_gemm": 0, "gemm_prefilter": 1, "gemm_replay": 2, "sgd": 3, "binary": 4,
     "relu": 5, "relu_backward": 6, "add_relu": 7, "mse": 8,
+    "native_gemm": 9, "native_sgd": 10, "native_mse": 11,
 }
 
 _lib = None

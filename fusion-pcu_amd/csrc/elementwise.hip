@@ -861,6 +861,98 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
         *out = r;
 }
 
+// ------------------------------------------------------------- native compounds
+// Explicitly permitted native compound arithmetic (Boundary + BackendDefined): no fault is
+// classified; special values and subnormals flow through as the hardware produces them.
+
+// SGD (backends/rocm/tensor/native_sgd/native_sgd.rs:100-145): the product rounded before
+// the subtraction, or one fused multiply-add when contraction is permitted.
+template <typename T, bool VEC, bool CONTRACT>
+__global__ __launch_bounds__(kEwThreads) void k_native_sgd(const T *__restrict__ w,
+                                                           const T *__restrict__ g, T rate,
+                                                           T *__restrict__ out, uint64_t n)
+{
+    constexpr int W = Lanes<T, VEC>::W;
+    PCU_EW_LOOP(W)
+    {
+        T wv[W], gv[W], r[W];
+        load_lanes<T, VEC>(w, base, n, wv);
+        load_lanes<T, VEC>(g, base, n, gv);
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            if (CONTRACT) {
+                r[j] = fma(-rate, gv[j], wv[j]);
+            } else {
+                const T p = rate * gv[j];
+                r[j] = wv[j] - p;
+            }
+        }
+        store_lanes<T, VEC>(out, base, n, r);
+    }
+}
+
+// MSE (backends/rocm/tensor/native_loss/native_loss.rs, tensor.rs:5020-5070): rounded
+// difference and square, a sum in the declared precision, times the rounded reciprocal
+// count. The sum is a fixed-shape tree (per thread, wave, block, then over the blocks), so
+// it repeats bit for bit from run to run.
+template <typename T>
+__device__ __forceinline__ T block_tree_sum(T v, T *part)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v = v + __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0)
+        part[wave] = v;
+    __syncthreads();
+    T total = (T)0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++)
+        total = total + part[w];
+    return total;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_native_mse_partial(const T *__restrict__ p,
+                                                                   const T *__restrict__ t,
+                                                                   T *__restrict__ partial,
+                                                                   uint64_t n)
+{
+    __shared__ T part[kEwThreads / 64];
+    constexpr int W = Lanes<T, VEC>::W;
+    T acc = (T)0;
+    PCU_EW_LOOP(W)
+    {
+        T pv[W], tv[W];
+        load_lanes<T, VEC>(p, base, n, pv);
+        load_lanes<T, VEC>(t, base, n, tv);
+        T local = (T)0;
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T d = pv[j] - tv[j];
+            const T sq = d * d;
+            local = local + (base + j < n ? sq : (T)0);
+        }
+        acc = acc + local;
+    }
+    const T total = block_tree_sum(acc, part);
+    if (threadIdx.x == 0)
+        partial[blockIdx.x] = total;
+}
+
+template <typename T>
+__global__ __launch_bounds__(1024) void k_native_mse_final(const T *__restrict__ partial,
+                                                           uint64_t blocks, T scale,
+                                                           T *__restrict__ out)
+{
+    __shared__ T part[16];
+    T acc = (T)0;
+    for (uint64_t i = threadIdx.x; i < blocks; i += 1024)
+        acc = acc + partial[i];
+    const T total = block_tree_sum(acc, part);
+    if (threadIdx.x == 0)
+        *out = total * scale;
+}
+
 // ================================================================ launchers
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1063,4 +1155,67 @@ hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const
                       : mse_t<double>(s, n, p, t, scratch, count, out, policy, fault);
 }
 
+// ------------------------------------------------------------ native launchers
+
+template <typename T>
+static hipError_t native_sgd_t(hipStream_t s, uint64_t n, const void *w, const void *g, T rate,
+                               bool contracted, void *out)
+{
+    constexpr int Wd = Vec<T>::width;
+    const bool vec = aligned16(w) && aligned16(g) && aligned16(out);
+    const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
+    const T *W = (const T *)w, *G = (const T *)g;
+    T *O = (T *)out;
+    if (vec && contracted) hipLaunchKernelGGL((k_native_sgd<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
+    else if (vec) hipLaunchKernelGGL((k_native_sgd<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
+    else if (contracted) hipLaunchKernelGGL((k_native_sgd<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
+    else hipLaunchKernelGGL((k_native_sgd<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_native_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
+                             double rate, bool contracted, void *out)
+{
+    if (n == 0)
+        return hipSuccess;
+    return dtype == 0 ? native_sgd_t<float>(s, n, w, g, (float)rate, contracted, out)
+                      : native_sgd_t<double>(s, n, w, g, rate, contracted, out);
+}
+
+static uint64_t native_mse_blocks(int dtype, uint64_t n)
+{
+    const uint64_t w = dtype == 0 ? 4 : 2;
+    return grid_for((n + w - 1) / w);
+}
+
+size_t native_mse_scratch_bytes(int dtype, uint64_t n)
+{
+    return (size_t)native_mse_blocks(dtype, n) * (dtype == 0 ? 4 : 8);
+}
+
+template <typename T>
+static hipError_t native_mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
+                               void *scratch, T scale, void *out)
+{
+    constexpr int Wd = Vec<T>::width;
+    const bool vec = aligned16(p) && aligned16(t);
+    const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
+    if (vec)
+        hipLaunchKernelGGL((k_native_mse_partial<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n);
+    else
+        hipLaunchKernelGGL((k_native_mse_partial<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n);
+    hipLaunchKernelGGL((k_native_mse_final<T>), dim3(1), dim3(1024), 0, s, (const T *)scratch, (uint64_t)grid, scale, (T *)out);
+    return hipGetLastError();
+}
+
+hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                             void *scratch, double scale, void *out)
+{
+    if (n == 0)
+        return hipErrorInvalidValue;
+    return dtype == 0 ? native_mse_t<float>(s, n, p, t, scratch, (float)scale, out)
+                      : native_mse_t<double>(s, n, p, t, scratch, scale, out);
+}
+
 } // namespace pcu
+

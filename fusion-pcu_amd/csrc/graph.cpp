@@ -29,6 +29,7 @@ uint32_t Graph::push(Node n)
     bool elementwise = n.op == Op::Add || n.op == Op::Sub || n.op == Op::Mul || n.op == Op::Div ||
                        n.op == Op::Relu;
     n.policy = (is_float(n.dtype) && (elementwise || compound)) ? 0 : -1;
+    n.options = options; // tensor.rs:3612-3618: every node captures the graph's options
     nodes.push_back(std::move(n));
     return (uint32_t)(nodes.size() - 1);
 }
@@ -433,14 +434,17 @@ struct Backward {
 };
 
 // with_source_scope (gradients.rs:448-474): derived nodes take the source node's numerical
-// mode (Boundary when it has none) and, where they carry a policy, its underflow policy.
+// mode (Boundary when it has none), its numerical options and, where they carry a policy,
+// its underflow policy.
 template <typename F>
 static pcu_status with_source_scope(Graph &g, uint32_t source, F &&append)
 {
     Mode mode = g.nodes[source].mode == Mode::None ? Mode::Boundary : g.nodes[source].mode;
     int policy = g.nodes[source].policy;
     Mode previous = g.mode;
+    NumOptions previous_options = g.options;
     g.mode = mode;
+    g.options = g.nodes[source].options;
     size_t first_new = g.nodes.size();
     pcu_status st = append();
     if (policy >= 0)
@@ -448,6 +452,7 @@ static pcu_status with_source_scope(Graph &g, uint32_t source, F &&append)
             if (g.nodes[i].policy >= 0)
                 g.nodes[i].policy = policy;
     g.mode = previous;
+    g.options = previous_options;
     return st;
 }
 
@@ -633,14 +638,30 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
         if (nd.b != UINT32_MAX)
             uses[nd.b]++;
     }
+    route.assign(n, Route::Scalar);
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
-        // Admission: compound primitives only in Strict mode (the Boundary/native-compound
-        // route is a different numerical contract, out of this backend's scope).
-        if ((nd.op == Op::MatMul || nd.op == Op::MeanSquaredError || nd.op == Op::SgdUpdate) &&
-            nd.mode != Mode::Strict) {
-            error = "prepare: Boundary compound arithmetic is not admitted by the strict backend";
-            return PCU_ERR_UNSUPPORTED;
+        // Admission of compound primitives (backends/rocm/tensor.rs:9016-9058,
+        // tensor/native_loss/native_loss.rs:66-120, tensor/native_sgd/native_sgd.rs:46-100):
+        // Strict runs the checked ordered kernels; Boundary runs only under explicitly
+        // permitted native compound arithmetic with unspecified reproducibility and the IEEE
+        // (or no) underflow policy; a checked result-boundary compound is not implemented.
+        if (nd.op == Op::MatMul || nd.op == Op::MeanSquaredError || nd.op == Op::SgdUpdate) {
+            if (nd.mode == Mode::Strict) {
+                route[i] = Route::Strict;
+            } else if (nd.options.compound != 1) {
+                error = "prepare: checked result-boundary compound arithmetic is not implemented; "
+                        "select strict checking or explicitly permit native compound arithmetic";
+                return PCU_ERR_UNSUPPORTED;
+            } else if (nd.options.reproducibility != 0) {
+                error = "prepare: native compound arithmetic has no portable reproducibility profile";
+                return PCU_ERR_UNSUPPORTED;
+            } else if (nd.policy > 0) {
+                error = "prepare: native compound arithmetic admits only the IEEE underflow policy";
+                return PCU_ERR_UNSUPPORTED;
+            } else {
+                route[i] = Route::Native;
+            }
         }
         if (nd.op == Op::Input)
             inputs.push_back(i);
@@ -656,10 +677,10 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
                 fused_into[a] = (int)i;
         }
     }
-    // The serial MSE sum runs on the side stream when nothing in the plan consumes its
+    // The ordered MSE sum runs on the side stream when nothing in the plan consumes its
     // value (the training-loss case): it then overlaps the backward pass.
     for (uint32_t i : order)
-        if (graph.nodes[i].op == Op::MeanSquaredError && uses[i] == 0)
+        if (graph.nodes[i].op == Op::MeanSquaredError && uses[i] == 0 && route[i] == Route::Strict)
             mse_side[i] = 1;
     // Device storage: one buffer per computed node; outputs get two banks so a faulting
     // execution never overwrites the published results.
@@ -780,18 +801,29 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
         case Op::MatMul: {
             const auto &sa = graph.nodes[nd.a].shape;
             uint64_t inner = nd.tl ? sa[0] : sa[1];
-            st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr, ptr(nd.a),
-                                ptr(nd.b), ptr(i), policy);
+            if (route[i] == Route::Native)
+                st = ctx->op_native_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
+                                           ptr(nd.a), ptr(nd.b), ptr(i));
+            else
+                st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
+                                    ptr(nd.a), ptr(nd.b), ptr(i), policy);
             prog_to_graph.push_back(i);
             break;
         }
         case Op::MeanSquaredError:
-            st = ctx->op_mse(nd.dtype, graph.elements(nd.a), ptr(nd.a), ptr(nd.b), ptr(i), policy,
-                             mse_side[i] != 0);
+            if (route[i] == Route::Native)
+                st = ctx->op_native_mse(nd.dtype, graph.elements(nd.a), ptr(nd.a), ptr(nd.b), ptr(i));
+            else
+                st = ctx->op_mse(nd.dtype, graph.elements(nd.a), ptr(nd.a), ptr(nd.b), ptr(i),
+                                 policy, mse_side[i] != 0);
             prog_to_graph.push_back(i);
             break;
         case Op::SgdUpdate:
-            st = ctx->op_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr, ptr(i), policy);
+            if (route[i] == Route::Native)
+                st = ctx->op_native_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr,
+                                        nd.options.precision == 1, ptr(i));
+            else
+                st = ctx->op_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr, ptr(i), policy);
             prog_to_graph.push_back(i);
             break;
         default:
@@ -951,7 +983,45 @@ pcu_status pcu_graph_set_value_numerical_mode(pcu_graph *gh, uint32_t id, int st
     Graph *g = reinterpret_cast<Graph *>(gh);
     if (!g || g->check_id(id))
         return PCU_ERR_ARGUMENT;
+    if (g->nodes[id].mode == pcu::Mode::None) {
+        // tensor.rs:3154-3166: scalar nodes carry no mode (UnsupportedNumericalMode).
+        g->error = "set_value_numerical_mode: UnsupportedNumericalMode (not a compound node)";
+        return graph_fail(g, PCU_ERR_UNSUPPORTED);
+    }
     g->nodes[id].mode = strict ? pcu::Mode::Strict : pcu::Mode::Boundary;
+    return PCU_OK;
+}
+
+static bool valid_options(const pcu_numerical_options *o)
+{
+    return o && o->compound_arithmetic <= 1 && o->precision <= 1 && o->reproducibility <= 1;
+}
+
+static pcu::NumOptions to_options(const pcu_numerical_options *o)
+{
+    pcu::NumOptions r;
+    r.compound = o->compound_arithmetic;
+    r.precision = o->precision;
+    r.reproducibility = o->reproducibility;
+    return r;
+}
+
+pcu_status pcu_graph_set_numerical_options(pcu_graph *gh, const pcu_numerical_options *options)
+{
+    Graph *g = reinterpret_cast<Graph *>(gh);
+    if (!g || !valid_options(options))
+        return PCU_ERR_ARGUMENT;
+    g->options = to_options(options);
+    return PCU_OK;
+}
+
+pcu_status pcu_graph_set_value_numerical_options(pcu_graph *gh, uint32_t id,
+                                                 const pcu_numerical_options *options)
+{
+    Graph *g = reinterpret_cast<Graph *>(gh);
+    if (!g || g->check_id(id) || !valid_options(options))
+        return PCU_ERR_ARGUMENT;
+    g->nodes[id].options = to_options(options);
     return PCU_OK;
 }
 
@@ -1016,6 +1086,9 @@ pcu_status pcu_graph_describe(const pcu_graph *gh, uint32_t id, pcu_node_desc *o
     out->rank = (uint32_t)n.shape.size();
     for (size_t k = 0; k < n.shape.size() && k < 8; k++)
         out->shape[k] = n.shape[k];
+    out->options.compound_arithmetic = n.options.compound;
+    out->options.precision = n.options.precision;
+    out->options.reproducibility = n.options.reproducibility;
     return PCU_OK;
 }
 

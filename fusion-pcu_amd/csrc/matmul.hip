@@ -139,7 +139,9 @@ __device__ __forceinline__ void load4(const T *__restrict__ p, int valid, T (&v)
     }
 }
 
-template <typename T, bool TA, bool TB, bool VA, bool VB>
+// NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per
+// (cell, k) and no fault screen.
+template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false>
 __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
@@ -243,8 +245,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             for (int i = 0; i < 8; i++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    T p = a[i] * b[j];
-                    acc[i][j] = acc[i][j] + p;
+                    if (NATIVE) {
+                        acc[i][j] = fma(a[i], b[j], acc[i][j]);
+                    } else {
+                        T p = a[i] * b[j];
+                        acc[i][j] = acc[i][j] + p;
+                    }
                 }
         }
         if (kt + 1 < ktiles)
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 int c = c0 + j;
-                if (c >= N)
+                if (NATIVE || c >= N)
                     continue;
                 bool bad = !finite_bits(acc[i][h * 4 + j]);
                 if (check_risk)
@@ -293,7 +299,8 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             }
         }
     }
-    wave_record_fault(key, suspect);
+    if (!NATIVE)
+        wave_record_fault(key, suspect);
 }
 
 // --------------------------------------------------------------- exact replay
@@ -459,6 +466,44 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                        (const unsigned long long *)sc.suspect, fault, prior, n_prior);
     if (ev)
         (void)hipEventRecord(ev[3], s);
+    return hipGetLastError();
+}
+
+template <bool TA, bool TB>
+static void native_f64_dispatch(hipStream_t s, dim3 grid, const double *A, const double *B,
+                                double *C, int M, int N, int K)
+{
+    const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    const int vc = (N % 4 == 0) && aligned16(C);
+    if (va && vb)
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+    else if (va)
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+    else if (vb)
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+    else
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+}
+
+hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
+                                uint64_t cols, bool ta, bool tb, const void *a, const void *b,
+                                void *c)
+{
+    if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
+        return hipErrorInvalidValue;
+    if (rows == 0 || cols == 0)
+        return hipSuccess;
+    const int M = (int)rows, N = (int)cols, K = (int)inner;
+    if (dtype == 0)
+        return launch_native_gemm_f32(s, M, N, K, ta, tb, (const float *)a, (const float *)b, (float *)c);
+    const dim3 grid((unsigned)(((rows + BM - 1) / BM) * ((cols + BN - 1) / BN)));
+    const double *A = (const double *)a, *B = (const double *)b;
+    double *C = (double *)c;
+    if (!ta && !tb) native_f64_dispatch<false, false>(s, grid, A, B, C, M, N, K);
+    else if (!ta && tb) native_f64_dispatch<false, true>(s, grid, A, B, C, M, N, K);
+    else if (ta && !tb) native_f64_dispatch<true, false>(s, grid, A, B, C, M, N, K);
+    else native_f64_dispatch<true, true>(s, grid, A, B, C, M, N, K);
     return hipGetLastError();
 }
 

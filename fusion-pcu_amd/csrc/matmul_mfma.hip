@@ -80,6 +80,60 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &
     tn = (L % per_group) / gsize;
 }
 
+// Global -> registers -> k-major LDS staging of one BK-deep slab of op(A) (BM x BK) and
+// op(B) (BK x BN). Out-of-range elements stage as +0.
+template <class Cfg, bool TA, bool TB, bool VA, bool VB> struct SlabStager {
+    static constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
+    float ra[EA], rb[EB];
+
+    __device__ __forceinline__ void fetch(const float *__restrict__ A, const float *__restrict__ B,
+                                          int M, int N, int K, int m0, int n0, int k0, int tid)
+    {
+        if (!TA) { // A is M x K: BK/EA threads per row
+            const int m = m0 + tid / (BK / EA), k = k0 + (tid % (BK / EA)) * EA;
+            load_run<EA, VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k, EA) : 0, ra);
+        } else {   // A is K x M: BM/EA threads per k-row
+            const int k = k0 + tid / (BM / EA), m = m0 + (tid % (BM / EA)) * EA;
+            load_run<EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
+        }
+        if (!TB) { // B is K x N: BN/EB threads per k-row
+            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
+            load_run<EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
+        } else {   // B is N x K: BK/EB threads per row
+            const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
+            load_run<EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
+        }
+    }
+
+    __device__ __forceinline__ void stash(float (*As)[Cfg::LDA], float (*Bs)[Cfg::LDB], int tid) const
+    {
+        if (!TA) {
+            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
+#pragma unroll
+            for (int i = 0; i < EA; i++)
+                As[k + i][m] = ra[i];
+        } else {
+            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
+#pragma unroll
+            for (int q = 0; q < EA / 4; q++)
+                *reinterpret_cast<float4 *>(&As[k][m + 4 * q]) =
+                    make_float4(ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
+        }
+        if (!TB) {
+            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
+#pragma unroll
+            for (int q = 0; q < EB / 4; q++)
+                *reinterpret_cast<float4 *>(&Bs[k][n + 4 * q]) =
+                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+        } else {
+            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
+                Bs[k + i][n] = rb[i];
+        }
+    }
+};
+
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
@@ -87,7 +141,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     int check_risk, unsigned long long *suspect)
 {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
-    constexpr int S = SM * SN, EA = Cfg::EA, EB = Cfg::EB;
+    constexpr int S = SM * SN;
     __shared__ __align__(16) float As[2][BK][Cfg::LDA];
     __shared__ __align__(16) float Bs[2][BK][Cfg::LDB];
 
@@ -105,51 +159,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         for (int r = 0; r < 16; r++)
             acc[t][r] = 0.0f;
 
-    float ra[EA], rb[EB];
-    // Global -> registers for the k-slab starting at k0.
-    auto fetch = [&](int k0) {
-        if (!TA) { // A is M x K: BK/EA threads per row
-            const int m = m0 + tid / (BK / EA), k = k0 + (tid % (BK / EA)) * EA;
-            load_run<EA, VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k, EA) : 0, ra);
-        } else {   // A is K x M: BM/EA threads per k-row
-            const int k = k0 + tid / (BM / EA), m = m0 + (tid % (BM / EA)) * EA;
-            load_run<EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
-        }
-        if (!TB) { // B is K x N: BN/EB threads per k-row
-            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
-            load_run<EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
-        } else {   // B is N x K: BK/EB threads per row
-            const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
-            load_run<EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
-        }
-    };
-    // Registers -> k-major LDS stage `buf`.
-    auto stash = [&](int buf) {
-        if (!TA) {
-            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
-#pragma unroll
-            for (int i = 0; i < EA; i++)
-                As[buf][k + i][m] = ra[i];
-        } else {
-            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
-#pragma unroll
-            for (int q = 0; q < EA / 4; q++)
-                *reinterpret_cast<float4 *>(&As[buf][k][m + 4 * q]) =
-                    make_float4(ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
-        }
-        if (!TB) {
-            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
-#pragma unroll
-            for (int q = 0; q < EB / 4; q++)
-                *reinterpret_cast<float4 *>(&Bs[buf][k][n + 4 * q]) =
-                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
-        } else {
-            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
-#pragma unroll
-            for (int i = 0; i < EB; i++)
-                Bs[buf][k + i][n] = rb[i];
-        }
-    };
+    SlabStager<Cfg, TA, TB, VA, VB> stage;
 
     v32f zero;
 #pragma unroll
@@ -170,15 +180,15 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 
     const int ktiles = (K + BK - 1) / BK;
     if (ktiles > 0) {
-        fetch(0);
-        stash(0);
+        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        stage.stash(As[0], Bs[0], tid);
     }
     __syncthreads();
     const int half = lane >> 5, col = lane & 31;
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < ktiles)
-            fetch((kt + 1) * BK);
+            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
         // Software pipeline: one MFMA is in flight while the vector unit folds the previous
         // one (the group barriers ask the scheduler for that alternation). Lanes 0-31 carry
         // k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
@@ -229,7 +239,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             }
         }
         if (kt + 1 < ktiles)
-            stash(cur ^ 1);
+            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
         __syncthreads();
     }
 
@@ -304,6 +314,110 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 unsigned long long *suspect)
 {
     mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect);
+    return hipGetLastError();
+}
+
+
+// ------------------------------------------------------------ native F32 MatMul
+// Explicitly permitted native compound arithmetic (Boundary + BackendDefined): the matrix
+// cores accumulate, v_mfma_f32_32x32x2_f32 folding k and k+1 of a 32x32 subtile per
+// instruction in their own order and rounding. No fault is classified.
+template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_gemm_mfma(
+    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
+    int N, int K)
+{
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
+    constexpr int S = SM * SN;
+    __shared__ __align__(16) float As[2][BK][Cfg::LDA];
+    __shared__ __align__(16) float Bs[2][BK][Cfg::LDB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    v16f acc[S];
+#pragma unroll
+    for (int t = 0; t < S; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            acc[t][r] = 0.0f;
+
+    SlabStager<Cfg, TA, TB, VA, VB> stage;
+    const int ktiles = (K + BK - 1) / BK;
+    if (ktiles > 0) {
+        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        stage.stash(As[0], Bs[0], tid);
+    }
+    __syncthreads();
+    const int half = lane >> 5, col = lane & 31;
+    for (int kt = 0; kt < ktiles; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles)
+            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[SM], b[SN];
+#pragma unroll
+            for (int i = 0; i < SM; i++)
+                a[i] = As[cur][kk + half][wm + 32 * i + col];
+#pragma unroll
+            for (int j = 0; j < SN; j++)
+                b[j] = Bs[cur][kk + half][wn + 32 * j + col];
+#pragma unroll
+            for (int t = 0; t < S; t++)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t / SN], b[t % SN], acc[t], 0, 0, 0);
+        }
+        if (kt + 1 < ktiles)
+            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = n0 + wn + 32 * (t % SN) + col;
+        if (c >= N)
+            continue;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + wm + 32 * (t / SN) + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (row < M)
+                C[(size_t)row * N + c] = acc[t][r];
+        }
+    }
+}
+
+template <class Cfg, bool TA, bool TB>
+static void native_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N, int K)
+{
+    const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
+    const dim3 block(Cfg::kThreads);
+    const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    if (va && vb)
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K);
+    else if (va)
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K);
+    else if (vb)
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K);
+    else
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K);
+}
+
+// 4 waves of 64 x 64 over a 128 x 128 tile: four independent accumulators per wave keep
+// the matrix core busy between dependent MFMAs.
+using NativeCfg = MfmaCfg<2, 2, 2, 2, 32, 2>;
+
+hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
+                                  const float *A, const float *B, float *C)
+{
+    if (!ta && !tb) native_dispatch<NativeCfg, false, false>(s, A, B, C, M, N, K);
+    else if (!ta && tb) native_dispatch<NativeCfg, false, true>(s, A, B, C, M, N, K);
+    else if (ta && !tb) native_dispatch<NativeCfg, true, false>(s, A, B, C, M, N, K);
+    else native_dispatch<NativeCfg, true, true>(s, A, B, C, M, N, K);
     return hipGetLastError();
 }
 

@@ -26,6 +26,17 @@ enum class Op : uint32_t {
 
 enum class Mode : int32_t { None = -1, Boundary = 0, Strict = 1 };
 
+// PcuNumericalOptions (core/numerical/numerical.rs:71-78): every node captures the graph's
+// options when it is appended.
+struct NumOptions {
+    uint32_t compound = 0;        // 0 Checked, 1 BackendDefined
+    uint32_t precision = 0;       // 0 Preserve, 1 BackendOptimized
+    uint32_t reproducibility = 0; // 0 Unspecified, 1 PortableV1
+};
+
+// How the prepared executor runs a compound node.
+enum class Route : int { Scalar, Strict, Native };
+
 struct Node {
     Op op = Op::Input;
     uint32_t a = UINT32_MAX, b = UINT32_MAX; // operands
@@ -36,11 +47,13 @@ struct Node {
     int dtype = 0;                           // 0 f32, 1 f64
     Mode mode = Mode::None;                  // numerical mode (MatMul/MSE/SGD/ReluBackward)
     int policy = -1;                         // float underflow policy; -1 when none
+    NumOptions options;                      // numerical options captured at append
 };
 
 struct Graph {
     std::vector<Node> nodes;
     Mode mode = Mode::Boundary; // default numerical mode for new compound nodes
+    NumOptions options;         // default numerical options for new nodes
     std::string error;
 
     uint32_t push(Node n);
@@ -73,6 +86,7 @@ struct Prepared {
     std::vector<int> is_output;     // per node
     std::vector<int> fused_into;    // Add fused into the ReLU at this id (or -1)
     std::vector<int> mse_side;      // MSE runs on the side stream
+    std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
     int bank = 0;                   // bank written by the next execution
     bool published = false;

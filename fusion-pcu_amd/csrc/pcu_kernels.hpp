@@ -61,6 +61,20 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 const unsigned long long *prior, unsigned n_prior,
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto);
 
+// Native compound arithmetic (Boundary + BackendDefined): no fault word.
+hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
+                                  const float *A, const float *B, float *C);
+hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
+                                uint64_t cols, bool ta, bool tb, const void *a, const void *b,
+                                void *c);
+hipError_t launch_native_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
+                             double rate, bool contracted, void *out);
+// `scratch` holds native_mse_scratch_bytes(dtype, n) bytes; `scale` is the rounded
+// reciprocal of the element count in the dtype.
+size_t native_mse_scratch_bytes(int dtype, uint64_t n);
+hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                             void *scratch, double scale, void *out);
+
 // Small device utilities (fill kernels rather than memsets, so a captured graph replays
 // them as kernels).
 hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value);

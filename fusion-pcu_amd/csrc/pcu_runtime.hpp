@@ -14,7 +14,8 @@ namespace pcu {
 extern thread_local std::string g_thread_error;
 
 // Ordered fault domain of one node (core/dialect/tensor/fault_domain/fault_domain.rs:30-34).
-enum class Prim { Elementwise, MatMul, Sgd, Mse };
+// Native: an explicitly permitted native compound, which records no arithmetic fault.
+enum class Prim { Elementwise, MatMul, Sgd, Mse, Native };
 
 struct NodeInfo {
     Prim prim;
@@ -98,6 +99,11 @@ struct Ctx {
                       int policy);
     pcu_status op_mse(int dtype, uint64_t n, const void *p, const void *t, void *out, int policy,
                       bool on_side);
+    pcu_status op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
+                                int tr, const void *a, const void *b, void *c);
+    pcu_status op_native_mse(int dtype, uint64_t n, const void *p, const void *t, void *out);
+    pcu_status op_native_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
+                             bool contracted, void *out);
 };
 
 } // namespace pcu

@@ -320,6 +320,8 @@ static bool decode_word(const NodeInfo &n, uint64_t word, pcu_fault *f)
         f->step = ordinal % 3 == 0 ? PCU_STEP_SUBTRACT
                                    : (ordinal % 3 == 1 ? PCU_STEP_MULTIPLY : PCU_STEP_ADD);
         return kind != PCU_FAULT_DIVIDE_BY_ZERO;
+    case Prim::Native:
+        return false; // native kernels never write their word
     }
     return false;
 }
@@ -662,6 +664,89 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     return hip(hipFreeAsync(sq, s), "hipFreeAsync");
 }
 
+// ------------------------------------------------------------ native compounds
+// Boundary + BackendDefined (core/numerical/numerical.rs:21-35): no arithmetic fault is
+// classified; argument, shape and device errors still are.
+
+pcu_status Ctx::op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
+                                 int tr, const void *a, const void *b, void *c)
+{
+    if (!valid_dtype(dtype) || !c || ((rows * inner) && !a) || ((inner * cols) && !b)) {
+        fail("native_matmul: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Native, rows * cols, inner}, &word);
+    if (st)
+        return st;
+    if (rows == 0 || cols == 0)
+        return PCU_OK;
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_native_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a, b, c),
+             "native_matmul launch");
+    timer_stop(PCU_KERNEL_NATIVE_GEMM, t, stream);
+    return st;
+}
+
+pcu_status Ctx::op_native_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
+                              bool contracted, void *out)
+{
+    if (!valid_dtype(dtype) || (n && (!w || !g || !out))) {
+        fail("native_sgd: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    uint32_t rb;
+    memcpy(&rb, &rate, 4);
+    if ((rb & 0x7f800000u) == 0x7f800000u) {
+        // native_sgd.rs:64-70 admits finite learning rates only.
+        fail("native_sgd: learning rate must be finite");
+        return PCU_ERR_ARGUMENT;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Native, n, 0}, &word);
+    if (st)
+        return st;
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_native_sgd(stream, dtype, n, w, g, (double)rate, contracted, out), "native_sgd launch");
+    timer_stop(PCU_KERNEL_NATIVE_SGD, t, stream);
+    return st;
+}
+
+pcu_status Ctx::op_native_mse(int dtype, uint64_t n, const void *p, const void *t, void *out)
+{
+    if (!valid_dtype(dtype) || !p || !t || !out) {
+        fail("native_mse: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (n == 0) {
+        fail("native_mse: empty input (TensorError::ShapeMismatch)");
+        return PCU_ERR_SHAPE;
+    }
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Native, n, 0}, &word);
+    if (st)
+        return st;
+    // Scale: the rounded reciprocal of the rounded count (tensor.rs:8701-8730); host IEEE
+    // division rounds to nearest even in each precision.
+    double scale;
+    if (dtype == PCU_F32) {
+        const float count = (float)count_as(dtype, n); // exact: count_as already rounded it
+        const volatile float one = 1.0f;
+        scale = (double)(one / count);
+    } else {
+        scale = 1.0 / count_as(dtype, n);
+    }
+    void *sc = nullptr;
+    if ((st = scratch(native_mse_scratch_bytes(dtype, n), stream, &sc)))
+        return st;
+    hipEvent_t t0 = timer_start(stream);
+    st = hip(launch_native_mse(stream, dtype, n, p, t, sc, scale, out), "native_mse launch");
+    timer_stop(PCU_KERNEL_NATIVE_MSE, t0, stream);
+    if (st)
+        return st;
+    return hip(hipFreeAsync(sc, stream), "hipFreeAsync");
+}
+
 } // namespace pcu
 
 // ======================================================================= C ABI
@@ -776,6 +861,31 @@ pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint6
     PCU_OP_PROLOGUE
     st = c->op_matmul(dtype, rows, inner, cols, transpose_left, transpose_right, left, right, out, policy);
     return c->finish_op(st, fault);
+}
+
+pcu_status pcu_native_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
+                             uint64_t cols, int transpose_left, int transpose_right,
+                             const void *left, const void *right, void *out)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_native_matmul(dtype, rows, inner, cols, transpose_left, transpose_right, left, right, out);
+    return c->finish_op(st, nullptr);
+}
+
+pcu_status pcu_native_mse(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *prediction,
+                          const void *target, void *out_scalar)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_native_mse(dtype, n, prediction, target, out_scalar);
+    return c->finish_op(st, nullptr);
+}
+
+pcu_status pcu_native_sgd(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *weights,
+                          const void *gradient, float learning_rate, int contracted, void *out)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_native_sgd(dtype, n, weights, gradient, learning_rate, contracted != 0, out);
+    return c->finish_op(st, nullptr);
 }
 
 pcu_status pcu_checked_binary(pcu_ctx *ctx, pcu_dtype dtype, pcu_binary_op op, uint64_t n,

@@ -65,6 +65,27 @@ class Graph:
     def set_numerical_mode(self, strict: bool) -> None:
         self._check(self._lib.pcu_graph_set_numerical_mode(self.handle, int(strict)))
 
+    @staticmethod
+    def _options(native_compound: bool, backend_precision: bool, deterministic: bool):
+        o = _abi.NumericalOptions()
+        o.compound_arithmetic = int(bool(native_compound))
+        o.precision = int(bool(backend_precision))
+        o.reproducibility = int(bool(deterministic))
+        return o
+
+    def set_numerical_options(self, native_compound: bool = False, backend_precision: bool = False,
+                              deterministic: bool = False) -> None:
+        """Graph::set_numerical_options: PcuNumericalOptions for nodes appended afterwards
+        (BackendDefined / BackendOptimized / PortableV1 when the flag is set)."""
+        o = self._options(native_compound, backend_precision, deterministic)
+        self._check(self._lib.pcu_graph_set_numerical_options(self.handle, ctypes.byref(o)))
+
+    def set_value_numerical_options(self, node: int, native_compound: bool = False,
+                                    backend_precision: bool = False,
+                                    deterministic: bool = False) -> None:
+        o = self._options(native_compound, backend_precision, deterministic)
+        self._check(self._lib.pcu_graph_set_value_numerical_options(self.handle, node, ctypes.byref(o)))
+
     def input(self, shape, dtype) -> int:
         r, s = self._shape(shape)
         return self._id(self._lib.pcu_graph_input, dtype_code(dtype), r, s)
@@ -122,6 +143,11 @@ class Graph:
             "learning_rate": float(d.learning_rate),
             "value_bits": int(d.value_bits),
             "shape": tuple(int(d.shape[k]) for k in range(d.rank)),
+            "numerical_options": {
+                "compound_arithmetic": ("Checked", "BackendDefined")[d.options.compound_arithmetic],
+                "precision": ("Preserve", "BackendOptimized")[d.options.precision],
+                "reproducibility": ("Unspecified", "PortableV1")[d.options.reproducibility],
+            },
         }
 
     def backward_mse(self, loss: int) -> List[Optional[int]]:
@@ -286,9 +312,11 @@ class CaptureValue:
 
 
 class _Capture:
-    def __init__(self, strict: bool, policy: int):
+    def __init__(self, strict: bool, policy: int, options: Optional[dict] = None):
         self.graph = Graph()
         self.graph.set_numerical_mode(strict)
+        if options:
+            self.graph.set_numerical_options(**options)
         self.policy = policy
         self.constants: List[np.ndarray] = []
         self.constant_nodes: List[int] = []
@@ -428,9 +456,16 @@ class _Entry:
         return outs[0] if self.single else outs
 
 
-def function(strict: bool = False, underflow: int = PcuFloatUnderflowPolicy.IeeeAfterRounding):
+def function(strict: bool = False, underflow: int = PcuFloatUnderflowPolicy.IeeeAfterRounding,
+             native_compound: bool = False, backend_precision: bool = False,
+             deterministic: bool = False):
     """The #[pcu] attribute: ``strict`` is flag(strict); ``underflow`` selects
-    flag(ieee_underflow | reject_subnormal_result | allow_gradual_underflow)."""
+    flag(ieee_underflow | reject_subnormal_result | allow_gradual_underflow); the numerical
+    option flags are flag(native_compound | checked_compound), flag(backend_precision |
+    preserve_precision) and flag(deterministic | non_deterministic)
+    (macros/fusion-pcu-macros/numerical/numerical.rs:22-31)."""
+    options = {"native_compound": native_compound, "backend_precision": backend_precision,
+               "deterministic": deterministic}
 
     def deco(fn):
         cache: Dict[tuple, _Entry] = {}
@@ -443,7 +478,7 @@ def function(strict: bool = False, underflow: int = PcuFloatUnderflowPolicy.Ieee
                                       str(a.dtype)) for a in args)
             entry = cache.get(key)
             if entry is None:
-                entry = _capture(fn, args, strict, int(underflow), ctx)
+                entry = _capture(fn, args, strict, int(underflow), ctx, options)
                 cache[key] = entry
             return entry.call(args)
 
@@ -453,10 +488,11 @@ def function(strict: bool = False, underflow: int = PcuFloatUnderflowPolicy.Ieee
     return deco
 
 
-def _capture(fn, args, strict: bool, policy: int, ctx: Context) -> _Entry:
+def _capture(fn, args, strict: bool, policy: int, ctx: Context,
+             options: Optional[dict] = None) -> _Entry:
     if getattr(_state, "capture", None) is not None:
         raise PcuExecutionError(_abi.PCU_ERR_STATE, "RecursiveTensorSource")
-    cap = _Capture(strict, policy)
+    cap = _Capture(strict, policy, options)
     _state.capture = cap
     try:
         vals = []
@@ -499,12 +535,14 @@ def c1_training_step(learning_rate: float = 0.01):
     return step
 
 
-def mlp_training_step(learning_rate: float = 1e-3):
+def mlp_training_step(learning_rate: float = 1e-3, native: bool = False):
     """Config C5: X@W1 -> relu -> @W2 -> relu -> @W3 -> MSE vs Y -> gradients for
-    (W1, W2, W3) -> strict SGD (benches/tensor_mlp_train/source/source.rs:46-75).
-    Returns (W1', W2', W3', loss)."""
+    (W1, W2, W3) -> SGD (benches/tensor_mlp_train/source/source.rs:46-75).
+    Returns (W1', W2', W3', loss). ``native`` captures the step in Boundary mode with
+    flag(native_compound): the MatMuls, MSE and SGD updates then run as native compounds,
+    while the elementwise nodes stay checked."""
 
-    @function(strict=True)
+    @function(strict=not native, native_compound=native)
     def step(x, w1, w2, w3, y):
         h1 = relu(matmul(x, w1))
         h2 = relu(matmul(h1, w2))

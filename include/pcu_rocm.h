@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define PCU_ROCM_ABI_VERSION 1
+#define PCU_ROCM_ABI_VERSION 2
 
 typedef struct pcu_ctx pcu_ctx;
 
@@ -176,6 +176,32 @@ pcu_status pcu_strict_mse(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void 
                           const void *target, void *out_scalar, pcu_underflow policy,
                           pcu_fault *fault);
 
+/* ------------------------------------------------------------ native ops
+ * Explicitly permitted native compound arithmetic (PcuCompoundArithmeticPolicy::
+ * BackendDefined in Boundary mode, core/numerical/numerical.rs:21-35). The reference
+ * routes these to rocBLAS SGEMM/DGEMM, a squared-difference kernel with rocBLAS ASUM, and
+ * a native SGD kernel (backends/rocm/tensor.rs:9016-9052, tensor/native_loss/native_loss.rs,
+ * tensor/native_sgd/native_sgd.rs). Reduction order, contraction and special-value
+ * behaviour are backend-defined; no arithmetic fault is classified (a non-finite result is
+ * an ordinary value). Shapes, pointers and device errors are still checked. Each call is a
+ * program node like the strict ops. */
+
+/* out = op(left) * op(right) in the declared precision. F32: matrix-core
+ * multiply-accumulate tiles; F64: vector-unit fused multiply-add. */
+pcu_status pcu_native_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
+                             uint64_t cols, int transpose_left, int transpose_right,
+                             const void *left, const void *right, void *out);
+/* *out = (sum of (p[i] - t[i])^2) * (1 / count): the difference and the square are rounded
+ * on their own, the sum is a fixed-shape tree in the declared precision, and the scale is the
+ * rounded reciprocal of the element count (backends/rocm/tensor.rs:8701-8730). */
+pcu_status pcu_native_mse(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *prediction,
+                          const void *target, void *out_scalar);
+/* out[i] = w[i] - rate * g[i]: the product rounded before the subtraction, or one fused
+ * multiply-add when `contracted` (PcuPrecisionPolicy::BackendOptimized,
+ * backends/rocm/tensor.rs:4941-4945). */
+pcu_status pcu_native_sgd(pcu_ctx *ctx, pcu_dtype dtype, uint64_t n, const void *weights,
+                          const void *gradient, float learning_rate, int contracted, void *out);
+
 /* ------------------------------------------------------------------ program
  * Between begin and end every op call is only enqueued and numbered as a node (0, 1, ...;
  * pcu_checked_add_relu takes two numbers). pcu_program_end synchronizes once and reports
@@ -205,7 +231,10 @@ typedef enum pcu_kernel_id {
     PCU_KERNEL_RELU_BACKWARD = 6,
     PCU_KERNEL_ADD_RELU = 7,
     PCU_KERNEL_MSE = 8,             /* squares + ordered sum + divide */
-    PCU_KERNEL_COUNT = 9
+    PCU_KERNEL_NATIVE_GEMM = 9,     /* native (BackendDefined) MatMul */
+    PCU_KERNEL_NATIVE_SGD = 10,
+    PCU_KERNEL_NATIVE_MSE = 11,
+    PCU_KERNEL_COUNT = 12
 } pcu_kernel_id;
 pcu_status pcu_profile_enable(pcu_ctx *ctx, int on);
 pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t *launches);
@@ -236,6 +265,20 @@ typedef enum pcu_graph_op {
     PCU_GRAPH_MEAN_SQUARED_ERROR = 10
 } pcu_graph_op;
 
+/* PcuNumericalOptions (core/numerical/numerical.rs:21-78): independent compound-arithmetic,
+ * precision and reproducibility requirements captured by every appended node. */
+typedef enum pcu_compound_arithmetic {
+    PCU_COMPOUND_CHECKED = 0,
+    PCU_COMPOUND_BACKEND_DEFINED = 1
+} pcu_compound_arithmetic;
+typedef enum pcu_precision { PCU_PRECISION_PRESERVE = 0, PCU_PRECISION_BACKEND_OPTIMIZED = 1 } pcu_precision;
+typedef enum pcu_reproducibility { PCU_REPRO_UNSPECIFIED = 0, PCU_REPRO_PORTABLE_V1 = 1 } pcu_reproducibility;
+typedef struct pcu_numerical_options {
+    uint32_t compound_arithmetic; /* pcu_compound_arithmetic */
+    uint32_t precision;           /* pcu_precision */
+    uint32_t reproducibility;     /* pcu_reproducibility */
+} pcu_numerical_options;
+
 /* NodeDescriptor (core/dialect/tensor.rs:3575-3586). numerical_mode: -1 none,
  * 0 Boundary, 1 Strict; underflow_policy: -1 none, else pcu_underflow. Operands are
  * UINT32_MAX when absent. */
@@ -250,6 +293,8 @@ typedef struct pcu_node_desc {
     uint32_t rank;
     uint64_t value_bits;
     uint64_t shape[8];
+    pcu_numerical_options options;
+    uint32_t reserved;
 } pcu_node_desc;
 
 pcu_status pcu_graph_create(pcu_graph **out);
@@ -273,6 +318,11 @@ pcu_status pcu_graph_mean_squared_error(pcu_graph *graph, uint32_t prediction, u
                                         uint32_t *id);
 pcu_status pcu_graph_sgd_update(pcu_graph *graph, uint32_t weights, uint32_t gradient,
                                 float learning_rate, uint32_t *id);
+/* Graph::set_numerical_options (defaults for nodes appended afterwards) and
+ * Graph::set_value_numerical_options (core/dialect/tensor.rs:3115-3136). */
+pcu_status pcu_graph_set_numerical_options(pcu_graph *graph, const pcu_numerical_options *options);
+pcu_status pcu_graph_set_value_numerical_options(pcu_graph *graph, uint32_t id,
+                                                 const pcu_numerical_options *options);
 /* Graph::set_value_float_underflow_policy / set_value_numerical_mode. */
 pcu_status pcu_graph_set_underflow_policy(pcu_graph *graph, uint32_t id, pcu_underflow policy);
 pcu_status pcu_graph_set_value_numerical_mode(pcu_graph *graph, uint32_t id, int strict);
@@ -290,7 +340,13 @@ pcu_status pcu_graph_describe(const pcu_graph *graph, uint32_t id, pcu_node_desc
 pcu_status pcu_graph_plan(const pcu_graph *graph, uint32_t n_outputs, const uint32_t *outputs,
                           uint32_t *order, uint32_t *order_len);
 
-/* Prepare once (plan, fusion of single-use Add->ReLU, device storage with two banks per
+/* Admission of compound nodes (MatMul, MeanSquaredError, SgdUpdate) at prepare:
+ *  Strict                                            -> the strict kernels;
+ *  Boundary + BackendDefined, Unspecified reproducibility, IEEE (or no) underflow policy
+ *                                                    -> the native kernels above;
+ *  anything else                                     -> PCU_ERR_UNSUPPORTED (the reference
+ *    rejects checked result-boundary MatMul: backends/rocm/tensor.rs:9053-9058).
+ * Prepare once (plan, fusion of single-use Add->ReLU, device storage with two banks per
  * output), execute many times. Inputs are device pointers in the order of the graph's Input
  * nodes that the plan uses (pcu_prepared_input_id). An execution that faults publishes
  * nothing and returns the first fault with `node` = its graph node id; the previous

@@ -35,6 +35,9 @@ class Node:
     mode: Optional[str] = None       # "Strict" / "Boundary" for compound ops
     policy: Optional[int] = None     # underflow policy when checked
     params: dict = field(default_factory=dict)
+    # PcuNumericalOptions captured at append (core/dialect/tensor.rs:3612-3618):
+    # (compound_arithmetic, precision, reproducibility)
+    options: tuple = ("Checked", "Preserve", "Unspecified")
 
 
 @dataclass
@@ -47,12 +50,14 @@ class Graph:
     def __init__(self):
         self.nodes: List[Node] = []
         self.mode = "Boundary"
+        self.options = ("Checked", "Preserve", "Unspecified")
 
     # -------------------------------------------------------------- builder
     def push(self, op, operands, shape, dtype, **params) -> int:
         mode = self.mode if op in COMPOUND else None
         policy = 0 if (op in ELEMENTWISE or mode is not None) else None
-        self.nodes.append(Node(op, tuple(operands), tuple(shape), np.dtype(dtype), mode, policy, params))
+        self.nodes.append(Node(op, tuple(operands), tuple(shape), np.dtype(dtype), mode, policy, params,
+                               self.options))
         return len(self.nodes) - 1
 
     def input(self, shape, dtype) -> int:
@@ -102,10 +107,13 @@ class Graph:
 
     # ------------------------------------------------------------- gradients
     def _scoped(self, source, fn):
-        """with_source_scope (gradients.rs:448-474)."""
+        """with_source_scope (gradients.rs:448-474): the source's mode (Boundary when it has
+        none), its numerical options and, where derived nodes carry one, its underflow
+        policy."""
         src = self.nodes[source]
-        prev = self.mode
+        prev, prev_options = self.mode, self.options
         self.mode = src.mode or "Boundary"
+        self.options = src.options
         first = len(self.nodes)
         try:
             return fn()
@@ -114,7 +122,7 @@ class Graph:
                 for n in self.nodes[first:]:
                     if n.policy is not None:
                         n.policy = src.policy
-            self.mode = prev
+            self.mode, self.options = prev, prev_options
 
     def _scale_value(self, p):
         count = self.elements(p)

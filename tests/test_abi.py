@@ -43,7 +43,29 @@ def test_binding_covers_header_and_loads_without_gpu(pcu_pkg):
     from fusion_pcu_amd import _abi
     assert set(_abi.SIGNATURES) >= _declared_functions() - _graph_only()
     lib = pcu_pkg.lib()
-    assert lib.pcu_abi_version() == 1
+    header = open(os.path.join(ROOT, "include", "pcu_rocm.h")).read()
+    version = int(re.search(r"#define PCU_ROCM_ABI_VERSION (\d+)", header).group(1))
+    assert lib.pcu_abi_version() == version
+
+
+def test_node_descriptor_layout_matches_the_header():
+    """The ctypes mirror of pcu_node_desc has the C layout (compiled with the host compiler
+    from the header itself)."""
+    import ctypes
+    import tempfile
+    from fusion_pcu_amd import _abi
+    src = ('#include <stdio.h>\n#include <stddef.h>\n#include "pcu_rocm.h"\n'
+           'int main(void){printf("%zu %zu %zu", sizeof(pcu_node_desc), '
+           'offsetof(pcu_node_desc, options), sizeof(pcu_numerical_options)); return 0;}\n')
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        size, off, osize = map(int, subprocess.run([exe], capture_output=True, text=True,
+                                                   check=True).stdout.split())
+    assert ctypes.sizeof(_abi.NodeDesc) == size
+    assert _abi.NodeDesc.options.offset == off
+    assert ctypes.sizeof(_abi.NumericalOptions) == osize
 
 
 def _graph_only():

@@ -18,10 +18,12 @@ def _seq_product(g):
     for i in range(g.node_count()):
         d = g.describe(i)
         ops = tuple(x for x in (d["left"], d["right"]) if x is not None)
+        o = d["numerical_options"]
         out.append((d["op"], ops, d["shape"], d["numerical_mode"], d["underflow_policy"],
                     d["transpose_left"] if d["op"] == "MatMul" else None,
                     d["transpose_right"] if d["op"] == "MatMul" else None,
-                    d["value_bits"] if d["op"] == "Uniform" else None))
+                    d["value_bits"] if d["op"] == "Uniform" else None,
+                    (o["compound_arithmetic"], o["precision"], o["reproducibility"])))
     return out
 
 
@@ -34,7 +36,7 @@ def _seq_oracle(g):
             bits = int(v.view(np.uint32 if v.dtype == np.float32 else np.uint64))
         out.append((n.op, n.operands, n.shape, n.mode,
                     n.policy, n.params.get("tl") if n.op == "MatMul" else None,
-                    n.params.get("tr") if n.op == "MatMul" else None, bits))
+                    n.params.get("tr") if n.op == "MatMul" else None, bits, n.options))
     return out
 
 
@@ -157,3 +159,51 @@ def test_plan_retains_unused_checked_nodes(G):
     x = g.input((1, 1), np.float32)
     discarded = g.matmul(x, x)
     assert discarded in g.plan([x])
+
+
+def test_numerical_options_capture_and_derivative_inheritance(G):
+    """PcuNumericalOptions are captured by every node when it is appended
+    (core/dialect/tensor.rs:3612-3618), Graph::set_value_numerical_options changes one node
+    (:3129-3136), and reverse mode appends derivative nodes under the source node's mode and
+    options (gradients.rs:448-474)."""
+    def build(p, o):
+        for g, key in ((p, "p"), (o, "o")):
+            x = g.input((8, 4), np.float32)
+            w = g.input((4, 3), np.float32)
+            y = g.input((8, 3), np.float32)
+            if key == "p":
+                g.set_numerical_options(native_compound=True)
+            else:
+                g.options = ("BackendDefined", "Preserve", "Unspecified")
+            pred = g.relu(g.matmul(x, w))
+            loss = g.mean_squared_error(pred, y)
+            if key == "p":
+                g.set_numerical_options(backend_precision=True, deterministic=True)
+            else:
+                g.options = ("Checked", "BackendOptimized", "PortableV1")
+            (gw,) = g.backward_mse_for_targets(loss, [w])
+            g.sgd_update(w, gw, 0.5)
+    p, o = _build_pair(G, build)
+    assert _seq_product(p) == _seq_oracle(o)
+    d = [p.describe(i) for i in range(p.node_count())]
+    assert d[0]["numerical_options"]["compound_arithmetic"] == "Checked"       # before the change
+    assert d[3]["numerical_mode"] == "Boundary" and d[3]["numerical_options"]["compound_arithmetic"] == "BackendDefined"
+    assert d[-1]["numerical_options"] == {"compound_arithmetic": "Checked", "precision": "BackendOptimized",
+                                          "reproducibility": "PortableV1"}
+    p.set_value_numerical_options(3, native_compound=False, backend_precision=True)
+    assert p.describe(3)["numerical_options"]["precision"] == "BackendOptimized"
+    assert p.describe(3)["numerical_options"]["compound_arithmetic"] == "Checked"
+
+
+def test_set_value_numerical_mode_rejects_scalar_nodes(G, pcu_pkg):
+    """Graph::set_value_numerical_mode returns UnsupportedNumericalMode for a node that
+    carries no numerical mode (core/dialect/tensor.rs:3154-3166)."""
+    g = G.Graph()
+    x = g.input((4,), np.float32)
+    r = g.relu(x)
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        g.set_value_numerical_mode(r, True)
+    y = g.input((4,), np.float32)
+    m = g.mean_squared_error(r, y)
+    g.set_value_numerical_mode(m, True)
+    assert g.describe(m)["numerical_mode"] == "Strict"
