@@ -118,8 +118,10 @@ template <typename T, int OP, bool UNIFORM, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
                                                        const T *__restrict__ b, T b_value,
                                                        T *__restrict__ out, uint64_t n,
-                                                       int policy, unsigned long long *fault)
+                                                       int policy, unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
     PCU_EW_LOOP(W)
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
             }
         }
     }
-    wave_record_fault(key, fault);
+    wave_record_fault(key, fault, gate);
 }
 
 // -------------------------------------------------------------------- relu
@@ -159,8 +161,10 @@ __global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T *__restrict__ out,
                                                      uint64_t n, int policy,
-                                                     unsigned long long *fault)
+                                                     unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
     PCU_EW_LOOP(W)
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T 
             }
         }
     }
-    wave_record_fault(key, fault);
+    wave_record_fault(key, fault, gate);
 }
 
 // ---------------------------------------------------------- relu backward
@@ -196,8 +200,10 @@ __global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restric
                                                               const T *__restrict__ up,
                                                               T *__restrict__ out, uint64_t n,
                                                               int policy,
-                                                              unsigned long long *fault)
+                                                              unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
     PCU_EW_LOOP(W)
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restric
             }
         }
     }
-    wave_record_fault(key, fault);
+    wave_record_fault(key, fault, gate);
 }
 
 // ------------------------------------------------------------ fused add->relu
@@ -238,8 +244,10 @@ __global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a
                                                          T *__restrict__ out, uint64_t n,
                                                          int policy,
                                                          unsigned long long *fault_add,
-                                                         unsigned long long *fault_relu)
+                                                         unsigned long long *fault_relu, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key_add = kNoFault, key_relu = kNoFault;
     PCU_EW_LOOP(W)
@@ -279,8 +287,8 @@ __global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a
             }
         }
     }
-    wave_record_fault(key_add, fault_add);
-    wave_record_fault(key_relu, fault_relu);
+    wave_record_fault(key_add, fault_add, gate);
+    wave_record_fault(key_relu, fault_relu, NodeGate{gate.word, gate.node + 1});
 }
 
 // -------------------------------------------------------------------- SGD
@@ -291,8 +299,10 @@ template <typename T, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void k_sgd(const T *__restrict__ w,
                                                     const T *__restrict__ g, T rate,
                                                     T *__restrict__ out, uint64_t n, int policy,
-                                                    unsigned long long *fault)
+                                                    unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
     PCU_EW_LOOP(W)
@@ -325,7 +335,7 @@ __global__ __launch_bounds__(kEwThreads) void k_sgd(const T *__restrict__ w,
             }
         }
     }
-    wave_record_fault(key, fault);
+    wave_record_fault(key, fault, gate);
 }
 
 // -------------------------------------------------------------------- MSE
@@ -340,8 +350,10 @@ __global__ __launch_bounds__(kEwThreads) void k_mse_squares(const T *__restrict_
                                                             const T *__restrict__ t,
                                                             T *__restrict__ sq, uint64_t n,
                                                             int policy,
-                                                            unsigned long long *fault)
+                                                            unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
     PCU_EW_LOOP(W)
@@ -375,7 +387,7 @@ __global__ __launch_bounds__(kEwThreads) void k_mse_squares(const T *__restrict_
             }
         }
     }
-    wave_record_fault(key, fault);
+    wave_record_fault(key, fault, gate);
 }
 
 // Ordered sum of the squares, exact and parallel. Every square is +0 or positive, so the
@@ -648,7 +660,7 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, bool
                             uint64_t base, uint64_t limit, int policy,
                             unsigned long long *fault, int &ue, uint64_t &m, uint64_t &mmax,
                             SumScan *wave_tot, uint64_t *wave_key,
-                            typename SumBits<T>::U *s_total, int *s_stop)
+                            typename SumBits<T>::U *s_total, int *s_stop, const NodeGate &gate)
 {
     using U = typename SumBits<T>::U;
     constexpr int P = SumBits<T>::kPer;
@@ -710,6 +722,7 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, bool
             const uint32_t kind = classify_add(acc, s_i, r, policy);
             if (kind != kOk) {
                 atomicMin(fault, (unsigned long long)pack_fault(3 * cross + 2, kind));
+                gate_record(gate);
                 *s_stop = 1;
             } else {
                 *s_stop = 0;
@@ -728,8 +741,10 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, bool
 template <typename T>
 __global__ __launch_bounds__(256) void k_mse_chunk_sums(const T *__restrict__ sq, uint64_t n,
                                                         const unsigned long long *fault,
-                                                        double *__restrict__ chunk_sum)
+                                                        double *__restrict__ chunk_sum, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     __shared__ double part[4];
     const uint64_t limit = sum_limit(fault, n);
     const uint64_t base = (uint64_t)blockIdx.x * sum_chunk_len<T>();
@@ -752,8 +767,10 @@ __global__ __launch_bounds__(256) void k_mse_chunk_sums(const T *__restrict__ sq
 template <typename T>
 __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     const T *__restrict__ sq, uint64_t n, const unsigned long long *fault,
-    const double *__restrict__ chunk_sum, ChunkSummary *__restrict__ summ)
+    const double *__restrict__ chunk_sum, ChunkSummary *__restrict__ summ, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     using U = typename SumBits<T>::U;
     constexpr int P = SumBits<T>::kPer;
     __shared__ SumScan wave_tot[kSumThreads / 64];
@@ -805,8 +822,10 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
 template <typename T>
 __global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
     const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
-    unsigned long long *fault, const ChunkSummary *__restrict__ summ)
+    unsigned long long *fault, const ChunkSummary *__restrict__ summ, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     using U = typename SumBits<T>::U;
     __shared__ SumScan wave_tot[kSumThreads / 64];
     __shared__ uint64_t wave_key[kSumThreads / 64];
@@ -846,7 +865,7 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
                 }
             }
             if (!exact_chunk<T>(src, vec_ok, c * L, limit, policy, fault, ue, m, mmax, wave_tot,
-                                wave_key, &s_total, &s_stop))
+                                wave_key, &s_total, &s_stop, gate))
                 return;
         }
     }
@@ -855,10 +874,12 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
     const T total = from_bits<T>(sum_bits<T>(ue, m));
     const T r = total / count;
     const uint32_t kind = classify_div(total, count, r, policy);
-    if (kind != kOk)
+    if (kind != kOk) {
         atomicMin(fault, (unsigned long long)pack_fault(3 * n, kind));
-    else
+        gate_record(gate);
+    } else {
         *out = r;
+    }
 }
 
 // ------------------------------------------------------------- native compounds
@@ -870,8 +891,10 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
 template <typename T, bool VEC, bool CONTRACT>
 __global__ __launch_bounds__(kEwThreads) void k_native_sgd(const T *__restrict__ w,
                                                            const T *__restrict__ g, T rate,
-                                                           T *__restrict__ out, uint64_t n)
+                                                           T *__restrict__ out, uint64_t n, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int W = Lanes<T, VEC>::W;
     PCU_EW_LOOP(W)
     {
@@ -915,8 +938,10 @@ template <typename T, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void k_native_mse_partial(const T *__restrict__ p,
                                                                    const T *__restrict__ t,
                                                                    T *__restrict__ partial,
-                                                                   uint64_t n)
+                                                                   uint64_t n, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     __shared__ T part[kEwThreads / 64];
     constexpr int W = Lanes<T, VEC>::W;
     T acc = (T)0;
@@ -942,8 +967,10 @@ __global__ __launch_bounds__(kEwThreads) void k_native_mse_partial(const T *__re
 template <typename T>
 __global__ __launch_bounds__(1024) void k_native_mse_final(const T *__restrict__ partial,
                                                            uint64_t blocks, T scale,
-                                                           T *__restrict__ out)
+                                                           T *__restrict__ out, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     __shared__ T part[16];
     T acc = (T)0;
     for (uint64_t i = threadIdx.x; i < blocks; i += 1024)
@@ -968,7 +995,7 @@ static inline unsigned grid_for(uint64_t work_items)
 
 template <typename T>
 static hipError_t binary_t(hipStream_t s, int op, uint64_t n, const void *a, const void *b,
-                           const void *b_value, void *out, int policy, unsigned long long *fault)
+                           const void *b_value, void *out, int policy, unsigned long long *fault, NodeGate gate)
 {
     const T *A = (const T *)a, *B = (const T *)b;
     T bv = b_value ? *(const T *)b_value : (T)0;
@@ -978,11 +1005,11 @@ static hipError_t binary_t(hipStream_t s, int op, uint64_t n, const void *a, con
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
 #define PCU_LAUNCH_BINARY(OPC)                                                                      \
     if (uniform) {                                                                                  \
-        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
-        else hipLaunchKernelGGL((k_binary<T, OPC, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault, gate); \
+        else hipLaunchKernelGGL((k_binary<T, OPC, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault, gate); \
     } else {                                                                                        \
-        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
-        else hipLaunchKernelGGL((k_binary<T, OPC, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault); \
+        if (vec) hipLaunchKernelGGL((k_binary<T, OPC, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault, gate); \
+        else hipLaunchKernelGGL((k_binary<T, OPC, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault, gate); \
     }
     switch (op) {
     case kOpAdd: PCU_LAUNCH_BINARY(kOpAdd) break;
@@ -996,65 +1023,65 @@ static hipError_t binary_t(hipStream_t s, int op, uint64_t n, const void *a, con
 
 hipError_t launch_binary(hipStream_t s, int dtype, int op, uint64_t n, const void *a,
                          const void *b, const void *b_value, void *out, int policy,
-                         unsigned long long *fault)
+                         unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? binary_t<float>(s, op, n, a, b, b_value, out, policy, fault)
-                      : binary_t<double>(s, op, n, a, b, b_value, out, policy, fault);
+    return dtype == 0 ? binary_t<float>(s, op, n, a, b, b_value, out, policy, fault, gate)
+                      : binary_t<double>(s, op, n, a, b, b_value, out, policy, fault, gate);
 }
 
 template <typename T>
 static hipError_t relu_t(hipStream_t s, uint64_t n, const void *x, void *out, int policy,
-                         unsigned long long *fault)
+                         unsigned long long *fault, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     bool vec = aligned16(x) && aligned16(out);
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_relu<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault, gate);
     else
-        hipLaunchKernelGGL((k_relu<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_relu(hipStream_t s, int dtype, uint64_t n, const void *x, void *out,
-                       int policy, unsigned long long *fault)
+                       int policy, unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? relu_t<float>(s, n, x, out, policy, fault)
-                      : relu_t<double>(s, n, x, out, policy, fault);
+    return dtype == 0 ? relu_t<float>(s, n, x, out, policy, fault, gate)
+                      : relu_t<double>(s, n, x, out, policy, fault, gate);
 }
 
 template <typename T>
 static hipError_t relu_backward_t(hipStream_t s, uint64_t n, const void *x, const void *up,
-                                  void *out, int policy, unsigned long long *fault)
+                                  void *out, int policy, unsigned long long *fault, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     bool vec = aligned16(x) && aligned16(up) && aligned16(out);
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_relu_backward<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu_backward<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault, gate);
     else
-        hipLaunchKernelGGL((k_relu_backward<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_relu_backward<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (const T *)up, (T *)out, n, policy, fault, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_relu_backward(hipStream_t s, int dtype, uint64_t n, const void *x,
                                 const void *up, void *out, int policy,
-                                unsigned long long *fault)
+                                unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? relu_backward_t<float>(s, n, x, up, out, policy, fault)
-                      : relu_backward_t<double>(s, n, x, up, out, policy, fault);
+    return dtype == 0 ? relu_backward_t<float>(s, n, x, up, out, policy, fault, gate)
+                      : relu_backward_t<double>(s, n, x, up, out, policy, fault, gate);
 }
 
 template <typename T>
 static hipError_t add_relu_t(hipStream_t s, uint64_t n, const void *a, const void *b,
                              const void *b_value, void *out, int policy,
-                             unsigned long long *fault_add, unsigned long long *fault_relu)
+                             unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate)
 {
     const T *A = (const T *)a, *B = (const T *)b;
     T bv = b_value ? *(const T *)b_value : (T)0;
@@ -1063,46 +1090,46 @@ static hipError_t add_relu_t(hipStream_t s, uint64_t n, const void *a, const voi
     bool vec = aligned16(a) && aligned16(out) && (uniform || aligned16(b));
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (uniform) {
-        if (vec) hipLaunchKernelGGL((k_add_relu<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
-        else hipLaunchKernelGGL((k_add_relu<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        if (vec) hipLaunchKernelGGL((k_add_relu<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu, gate);
+        else hipLaunchKernelGGL((k_add_relu<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu, gate);
     } else {
-        if (vec) hipLaunchKernelGGL((k_add_relu<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
-        else hipLaunchKernelGGL((k_add_relu<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu);
+        if (vec) hipLaunchKernelGGL((k_add_relu<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu, gate);
+        else hipLaunchKernelGGL((k_add_relu<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, A, B, bv, (T *)out, n, policy, fault_add, fault_relu, gate);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, const void *b,
                            const void *b_value, void *out, int policy,
-                           unsigned long long *fault_add, unsigned long long *fault_relu)
+                           unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? add_relu_t<float>(s, n, a, b, b_value, out, policy, fault_add, fault_relu)
-                      : add_relu_t<double>(s, n, a, b, b_value, out, policy, fault_add, fault_relu);
+    return dtype == 0 ? add_relu_t<float>(s, n, a, b, b_value, out, policy, fault_add, fault_relu, gate)
+                      : add_relu_t<double>(s, n, a, b, b_value, out, policy, fault_add, fault_relu, gate);
 }
 
 template <typename T>
 static hipError_t sgd_t(hipStream_t s, uint64_t n, const void *w, const void *g, T rate,
-                        void *out, int policy, unsigned long long *fault)
+                        void *out, int policy, unsigned long long *fault, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     bool vec = aligned16(w) && aligned16(g) && aligned16(out);
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate);
     else
-        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault);
+        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                      double rate, void *out, int policy, unsigned long long *fault)
+                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? sgd_t<float>(s, n, w, g, (float)rate, out, policy, fault)
-                      : sgd_t<double>(s, n, w, g, rate, out, policy, fault);
+    return dtype == 0 ? sgd_t<float>(s, n, w, g, (float)rate, out, policy, fault, gate)
+                      : sgd_t<double>(s, n, w, g, rate, out, policy, fault, gate);
 }
 
 // Scratch of one MSE call: the squares, then the chunk sums and the chunk summaries.
@@ -1125,7 +1152,7 @@ size_t mse_scratch_bytes(int dtype, uint64_t n)
 
 template <typename T>
 static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t, void *scratch,
-                        T count, void *out, int policy, unsigned long long *fault)
+                        T count, void *out, int policy, unsigned long long *fault, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     char *base = (char *)scratch;
@@ -1136,50 +1163,50 @@ static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
     const bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault);
+        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault, gate);
     else
-        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault);
-    hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)chunks), dim3(256), 0, s, (const T *)squares, n, (const unsigned long long *)fault, chunk_sum);
-    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_sum, summ);
-    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const ChunkSummary *)summ);
+        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault, gate);
+    hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)chunks), dim3(256), 0, s, (const T *)squares, n, (const unsigned long long *)fault, chunk_sum, gate);
+    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_sum, summ, gate);
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const ChunkSummary *)summ, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
                       void *scratch, double count, void *out, int policy,
-                      unsigned long long *fault)
+                      unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipErrorInvalidValue;
-    return dtype == 0 ? mse_t<float>(s, n, p, t, scratch, (float)count, out, policy, fault)
-                      : mse_t<double>(s, n, p, t, scratch, count, out, policy, fault);
+    return dtype == 0 ? mse_t<float>(s, n, p, t, scratch, (float)count, out, policy, fault, gate)
+                      : mse_t<double>(s, n, p, t, scratch, count, out, policy, fault, gate);
 }
 
 // ------------------------------------------------------------ native launchers
 
 template <typename T>
 static hipError_t native_sgd_t(hipStream_t s, uint64_t n, const void *w, const void *g, T rate,
-                               bool contracted, void *out)
+                               bool contracted, void *out, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     const bool vec = aligned16(w) && aligned16(g) && aligned16(out);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     const T *W = (const T *)w, *G = (const T *)g;
     T *O = (T *)out;
-    if (vec && contracted) hipLaunchKernelGGL((k_native_sgd<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
-    else if (vec) hipLaunchKernelGGL((k_native_sgd<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
-    else if (contracted) hipLaunchKernelGGL((k_native_sgd<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
-    else hipLaunchKernelGGL((k_native_sgd<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n);
+    if (vec && contracted) hipLaunchKernelGGL((k_native_sgd<T, true, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n, gate);
+    else if (vec) hipLaunchKernelGGL((k_native_sgd<T, true, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n, gate);
+    else if (contracted) hipLaunchKernelGGL((k_native_sgd<T, false, true>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n, gate);
+    else hipLaunchKernelGGL((k_native_sgd<T, false, false>), dim3(grid), dim3(kEwThreads), 0, s, W, G, rate, O, n, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_native_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                             double rate, bool contracted, void *out)
+                             double rate, bool contracted, void *out, NodeGate gate)
 {
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? native_sgd_t<float>(s, n, w, g, (float)rate, contracted, out)
-                      : native_sgd_t<double>(s, n, w, g, rate, contracted, out);
+    return dtype == 0 ? native_sgd_t<float>(s, n, w, g, (float)rate, contracted, out, gate)
+                      : native_sgd_t<double>(s, n, w, g, rate, contracted, out, gate);
 }
 
 static uint64_t native_mse_blocks(int dtype, uint64_t n)
@@ -1195,26 +1222,26 @@ size_t native_mse_scratch_bytes(int dtype, uint64_t n)
 
 template <typename T>
 static hipError_t native_mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
-                               void *scratch, T scale, void *out)
+                               void *scratch, T scale, void *out, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
     const bool vec = aligned16(p) && aligned16(t);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_native_mse_partial<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n);
+        hipLaunchKernelGGL((k_native_mse_partial<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n, gate);
     else
-        hipLaunchKernelGGL((k_native_mse_partial<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n);
-    hipLaunchKernelGGL((k_native_mse_final<T>), dim3(1), dim3(1024), 0, s, (const T *)scratch, (uint64_t)grid, scale, (T *)out);
+        hipLaunchKernelGGL((k_native_mse_partial<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, (T *)scratch, n, gate);
+    hipLaunchKernelGGL((k_native_mse_final<T>), dim3(1), dim3(1024), 0, s, (const T *)scratch, (uint64_t)grid, scale, (T *)out, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                             void *scratch, double scale, void *out)
+                             void *scratch, double scale, void *out, NodeGate gate)
 {
     if (n == 0)
         return hipErrorInvalidValue;
-    return dtype == 0 ? native_mse_t<float>(s, n, p, t, scratch, (float)scale, out)
-                      : native_mse_t<double>(s, n, p, t, scratch, scale, out);
+    return dtype == 0 ? native_mse_t<float>(s, n, p, t, scratch, (float)scale, out, gate)
+                      : native_mse_t<double>(s, n, p, t, scratch, scale, out, gate);
 }
 
 } // namespace pcu

@@ -63,8 +63,10 @@ __device__ __forceinline__ int wave_min_i32(int v)
 // out[r] = min over c of ilog2|X[r, c]| for a row-major R x C matrix; one wave per row.
 template <typename T>
 __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, uint64_t R,
-                                                      uint64_t C, int *__restrict__ out)
+                                                      uint64_t C, int *__restrict__ out, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     uint64_t r = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64;
     if (r >= R)
         return; // whole wave exits together
@@ -84,8 +86,10 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
 // its partial minimum in with atomicMin (out pre-filled with kExpNone).
 template <typename T>
 __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, uint64_t R,
-                                                      uint64_t C, int *__restrict__ out)
+                                                      uint64_t C, int *__restrict__ out, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= C)
         return;
@@ -100,6 +104,13 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
 }
 
 __global__ void k_fill_i32(int *p, uint64_t n, int v)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void k_fill_u32(unsigned int *p, uint64_t n, unsigned int v)
 {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x)
@@ -145,8 +156,10 @@ template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false>
 __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
-    int vec_c, unsigned long long *suspect)
+    int vec_c, unsigned long long *suspect, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     __shared__ __align__(16) T As[2][BK][BM + PAD];
     __shared__ __align__(16) T Bs[2][BK][BN + PAD];
 
@@ -310,15 +323,13 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
     const T *__restrict__ A, const T *__restrict__ B, const T *__restrict__ C, uint64_t M,
     uint64_t N, uint64_t K, int ta, int tb, const int *__restrict__ row_exp,
     const int *__restrict__ col_exp, int thr, int check_risk, int policy,
-    const unsigned long long *suspect, unsigned long long *fault,
-    const unsigned long long *prior, unsigned n_prior)
+    const unsigned long long *suspect, unsigned long long *fault, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return; // an earlier node faulted: that fault is the one reported
     const uint64_t first = *suspect;
     if (first == kNoFault)
         return;
-    for (unsigned i = 0; i < n_prior; i++)
-        if (prior[i] != kNoFault)
-            return; // an earlier op faulted: that fault is the one reported
     const uint64_t cells = M * N;
     const uint64_t threads = (uint64_t)gridDim.x * blockDim.x;
     const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -343,12 +354,14 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
             uint32_t kind = classify_mul(a, b, p, policy);
             if (kind != kOk) {
                 atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2, kind));
+                gate_record(gate);
                 break;
             }
             T nxt = total + p;
             kind = classify_add(total, p, nxt, policy);
             if (kind != kOk) {
                 atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2 + 1, kind));
+                gate_record(gate);
                 break;
             }
             total = nxt;
@@ -386,45 +399,54 @@ hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uin
     return hipGetLastError();
 }
 
+hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t value)
+{
+    if (n == 0)
+        return hipSuccess;
+    unsigned grid = (unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid), dim3(256), 0, s, p, n, (unsigned int)value);
+    return hipGetLastError();
+}
+
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Minimum exponent of each row of a stored R x C matrix (rows) or of each column (cols).
 template <typename T>
-static void exp_min(hipStream_t s, const T *X, uint64_t R, uint64_t C, bool along_rows, int *out)
+static void exp_min(hipStream_t s, const T *X, uint64_t R, uint64_t C, bool along_rows, int *out,
+                    NodeGate gate)
 {
     if (along_rows) {
-        hipLaunchKernelGGL(k_exp_min_rows<T>, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, X, R, C, out);
+        hipLaunchKernelGGL(k_exp_min_rows<T>, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, X, R, C, out, gate);
     } else {
         unsigned fg = (unsigned)((C + 255) / 256 < 1024 ? (C + 255) / 256 : 1024);
         hipLaunchKernelGGL(k_fill_i32, dim3(fg ? fg : 1), dim3(256), 0, s, out, C, kExpNone);
         hipLaunchKernelGGL(k_exp_min_cols<T>, dim3((unsigned)((C + 255) / 256), (unsigned)((R + 63) / 64)),
-                           dim3(256), 0, s, X, R, C, out);
+                           dim3(256), 0, s, X, R, C, out, gate);
     }
 }
 
 template <typename T, bool TA, bool TB>
 static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C, int M, int N,
                           int K, const int *re, const int *ce, int thr, int risk,
-                          unsigned long long *suspect)
+                          unsigned long long *suspect, NodeGate gate)
 {
     bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     int vc = (N % 4 == 0) && aligned16(C);
     if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
     else
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect);
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
 }
 
 template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
-                                  MatmulScratch sc, unsigned long long *fault,
-                                  const unsigned long long *prior, unsigned n_prior,
+                                  MatmulScratch sc, unsigned long long *fault, NodeGate gate,
                                   hipEvent_t *ev, int engine)
 {
     if (M == 0 || N == 0)
@@ -439,8 +461,8 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (ev)
         (void)hipEventRecord(ev[0], s);
     if (risk && K > 0) {
-        exp_min<T>(s, A, ta ? K : M, ta ? M : K, !ta, sc.row_exp);
-        exp_min<T>(s, B, tb ? N : K, tb ? K : N, tb, sc.col_exp);
+        exp_min<T>(s, A, ta ? K : M, ta ? M : K, !ta, sc.row_exp, gate);
+        exp_min<T>(s, B, tb ? N : K, tb ? K : N, tb, sc.col_exp, gate);
     } else if (risk) {
         risk = 0; // an empty reduction has no arithmetic events
     }
@@ -451,11 +473,11 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         (void)hipEventRecord(ev[1], s);
     if (f32 && engine != kEngineValu) {
         (void)launch_gemm_mfma_f32(s, m, n, k, ta, tb, (const float *)A, (const float *)B,
-                                   (float *)C, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
-    } else if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
-    else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
-    else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
-    else gemm_dispatch<T, true, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect);
+                                   (float *)C, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    } else if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    else gemm_dispatch<T, true, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
@@ -463,7 +485,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         (void)hipEventRecord(ev[2], s);
     hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(1024), dim3(256), 0, s, A, B, (const T *)C, M, N, K,
                        (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, risk, policy,
-                       (const unsigned long long *)sc.suspect, fault, prior, n_prior);
+                       (const unsigned long long *)sc.suspect, fault, gate);
     if (ev)
         (void)hipEventRecord(ev[3], s);
     return hipGetLastError();
@@ -471,24 +493,24 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
 
 template <bool TA, bool TB>
 static void native_f64_dispatch(hipStream_t s, dim3 grid, const double *A, const double *B,
-                                double *C, int M, int N, int K)
+                                double *C, int M, int N, int K, NodeGate gate)
 {
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     const int vc = (N % 4 == 0) && aligned16(C);
     if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
     else
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
 }
 
 hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool ta, bool tb, const void *a, const void *b,
-                                void *c)
+                                void *c, NodeGate gate)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
@@ -496,22 +518,21 @@ hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
         return hipSuccess;
     const int M = (int)rows, N = (int)cols, K = (int)inner;
     if (dtype == 0)
-        return launch_native_gemm_f32(s, M, N, K, ta, tb, (const float *)a, (const float *)b, (float *)c);
+        return launch_native_gemm_f32(s, M, N, K, ta, tb, (const float *)a, (const float *)b, (float *)c, gate);
     const dim3 grid((unsigned)(((rows + BM - 1) / BM) * ((cols + BN - 1) / BN)));
     const double *A = (const double *)a, *B = (const double *)b;
     double *C = (double *)c;
-    if (!ta && !tb) native_f64_dispatch<false, false>(s, grid, A, B, C, M, N, K);
-    else if (!ta && tb) native_f64_dispatch<false, true>(s, grid, A, B, C, M, N, K);
-    else if (ta && !tb) native_f64_dispatch<true, false>(s, grid, A, B, C, M, N, K);
-    else native_f64_dispatch<true, true>(s, grid, A, B, C, M, N, K);
+    if (!ta && !tb) native_f64_dispatch<false, false>(s, grid, A, B, C, M, N, K, gate);
+    else if (!ta && tb) native_f64_dispatch<false, true>(s, grid, A, B, C, M, N, K, gate);
+    else if (ta && !tb) native_f64_dispatch<true, false>(s, grid, A, B, C, M, N, K, gate);
+    else native_f64_dispatch<true, true>(s, grid, A, B, C, M, N, K, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
-                                MatmulScratch scratch, unsigned long long *fault,
-                                const unsigned long long *prior, unsigned n_prior,
+                                MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev, int engine)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
@@ -519,10 +540,10 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
     if (dtype == 0)
         return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                       (const float *)a, (const float *)b, (float *)c, policy,
-                                      scratch, fault, prior, n_prior, ev, engine);
+                                      scratch, fault, gate, ev, engine);
     return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                    (const double *)a, (const double *)b, (double *)c, policy,
-                                   scratch, fault, prior, n_prior, ev, kEngineValu);
+                                   scratch, fault, gate, ev, kEngineValu);
 }
 
 } // namespace pcu

@@ -138,8 +138,10 @@ template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr,
-    int check_risk, unsigned long long *suspect)
+    int check_risk, unsigned long long *suspect, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
     constexpr int S = SM * SN;
     __shared__ __align__(16) float As[2][BK][Cfg::LDA];
@@ -276,31 +278,31 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; 
 template <class Cfg, bool TA, bool TB>
 static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
                           int K, const int *re, const int *ce, int thr, int risk,
-                          unsigned long long *suspect)
+                          unsigned long long *suspect, NodeGate gate)
 {
     const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
 }
 
 template <class Cfg>
 static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, const float *A,
                         const float *B, float *C, const int *re, const int *ce, int thr,
-                        int risk, unsigned long long *suspect)
+                        int risk, unsigned long long *suspect, NodeGate gate)
 {
-    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
-    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
-    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
-    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect);
+    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
 }
 
 // 8 waves of 32 x 64 over a 128 x 128 tile, 127 VGPRs (4 waves per SIMD). On MI355X at
@@ -311,9 +313,9 @@ using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C, const int *row_exp,
                                 const int *col_exp, int thr, int risk,
-                                unsigned long long *suspect)
+                                unsigned long long *suspect, NodeGate gate)
 {
-    mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect);
+    mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
     return hipGetLastError();
 }
 
@@ -325,8 +327,10 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
-    int N, int K)
+    int N, int K, NodeGate gate)
 {
+    if (block_gate_closed(gate))
+        return;
     typedef float v16f __attribute__((ext_vector_type(16)));
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
     constexpr int S = SM * SN;
@@ -391,20 +395,21 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_ge
 }
 
 template <class Cfg, bool TA, bool TB>
-static void native_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N, int K)
+static void native_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
+                            int K, NodeGate gate)
 {
     const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     if (va && vb)
-        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K);
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, gate);
     else if (va)
-        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K);
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K);
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, gate);
     else
-        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K);
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, gate);
 }
 
 // 4 waves of 64 x 64 over a 128 x 128 tile: four independent accumulators per wave keep
@@ -412,12 +417,12 @@ static void native_dispatch(hipStream_t s, const float *A, const float *B, float
 using NativeCfg = MfmaCfg<2, 2, 2, 2, 32, 2>;
 
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
-                                  const float *A, const float *B, float *C)
+                                  const float *A, const float *B, float *C, NodeGate gate)
 {
-    if (!ta && !tb) native_dispatch<NativeCfg, false, false>(s, A, B, C, M, N, K);
-    else if (!ta && tb) native_dispatch<NativeCfg, false, true>(s, A, B, C, M, N, K);
-    else if (ta && !tb) native_dispatch<NativeCfg, true, false>(s, A, B, C, M, N, K);
-    else native_dispatch<NativeCfg, true, true>(s, A, B, C, M, N, K);
+    if (!ta && !tb) native_dispatch<NativeCfg, false, false>(s, A, B, C, M, N, K, gate);
+    else if (!ta && tb) native_dispatch<NativeCfg, false, true>(s, A, B, C, M, N, K, gate);
+    else if (ta && !tb) native_dispatch<NativeCfg, true, false>(s, A, B, C, M, N, K, gate);
+    else native_dispatch<NativeCfg, true, true>(s, A, B, C, M, N, K, gate);
     return hipGetLastError();
 }
 

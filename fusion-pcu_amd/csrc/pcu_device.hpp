@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "pcu_kernels.hpp"
+
 #pragma clang fp contract(off)
 
 namespace pcu {
@@ -367,15 +369,45 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v)
     return v;
 }
 
+// ------------------------------------------------------------- stage gate
+// The program's stage gate holds the lowest program node that has recorded an arithmetic
+// fault (0xffffffff while none). A node's kernels skip their work once an earlier node has
+// faulted: that node's fault is the one reported, so later work only costs time
+// (backends/rocm/owned_dispatch/guarded/guarded.rs gates each stage on the previous stage's
+// record). The gate only decreases, so a kernel that starts after it closed for its node
+// skips, and any partial result of a kernel that was running when it closed is read only
+// by later kernels of the same node, which skip too.
+__device__ __forceinline__ void gate_record(const NodeGate &g)
+{
+    if (g.word)
+        atomicMin(g.word, g.node);
+}
+
+// Block-uniform test (one read by thread 0, shared through LDS), so a block never splits
+// around a barrier or a wave-level reduction. Call it first thing in a kernel.
+__device__ __forceinline__ bool block_gate_closed(const NodeGate &g)
+{
+    __shared__ int closed;
+    if (threadIdx.x == 0)
+        closed = g.word != nullptr && __atomic_load_n(g.word, __ATOMIC_RELAXED) < g.node;
+    __syncthreads();
+    return closed != 0;
+}
+
 // Record the wave's earliest packed fault with one atomic. `key` is kNoFault on lanes
-// without a fault; the ballot keeps the fault-free path to one instruction.
-__device__ __forceinline__ void wave_record_fault(uint64_t key, unsigned long long *word)
+// without a fault; the ballot keeps the fault-free path to one instruction. A fault word
+// (as opposed to a scratch word such as the MatMul's first suspect cell) also closes the
+// stage gate for later nodes.
+__device__ __forceinline__ void wave_record_fault(uint64_t key, unsigned long long *word,
+                                                  const NodeGate &gate = NodeGate{nullptr, 0})
 {
     if (__ballot(key != kNoFault) == 0)
         return;
     uint64_t m = wave_min_u64(key);
-    if (__lane_id() == 0)
+    if (__lane_id() == 0) {
         atomicMin(word, (unsigned long long)m);
+        gate_record(gate);
+    }
 }
 
 } // namespace pcu

@@ -6,29 +6,37 @@
 
 namespace pcu {
 
+// Stage gate of a launch: the program's gate word (the lowest program node that recorded a
+// fault, 0xffffffff while none) and this launch's node number. A node's kernels skip their
+// work when an earlier node has faulted. NodeGate{nullptr, 0} is ungated.
+struct NodeGate {
+    unsigned int *word;
+    unsigned int node;
+};
+
 enum : int { kOpAdd = 0, kOpSub = 1, kOpMul = 2, kOpDiv = 3 };
 
 // Elementwise family. `b == nullptr` selects the uniform right operand `*b_value`
 // (host memory, dtype-sized). Each launcher enqueues on `s` and never synchronizes.
 hipError_t launch_binary(hipStream_t s, int dtype, int op, uint64_t n, const void *a,
                          const void *b, const void *b_value, void *out, int policy,
-                         unsigned long long *fault);
+                         unsigned long long *fault, NodeGate gate);
 hipError_t launch_relu(hipStream_t s, int dtype, uint64_t n, const void *x, void *out,
-                       int policy, unsigned long long *fault);
+                       int policy, unsigned long long *fault, NodeGate gate);
 hipError_t launch_relu_backward(hipStream_t s, int dtype, uint64_t n, const void *x,
                                 const void *up, void *out, int policy,
-                                unsigned long long *fault);
+                                unsigned long long *fault, NodeGate gate);
 hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, const void *b,
                            const void *b_value, void *out, int policy,
-                           unsigned long long *fault_add, unsigned long long *fault_relu);
+                           unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                      double rate, void *out, int policy, unsigned long long *fault);
+                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate);
 // `scratch` holds mse_scratch_bytes(dtype, n) bytes; `count` is the element count
 // rounded to the dtype.
 size_t mse_scratch_bytes(int dtype, uint64_t n);
 hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
                       void *scratch, double count, void *out, int policy,
-                      unsigned long long *fault);
+                      unsigned long long *fault, NodeGate gate);
 
 // Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.
 struct MatmulScratch {
@@ -47,36 +55,36 @@ enum : int { kEngineAuto = 0, kEngineValu = 1, kEngineMfmaProducts = 2 };
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C, const int *row_exp,
                                 const int *col_exp, int thr, int risk,
-                                unsigned long long *suspect);
+                                unsigned long long *suspect, NodeGate gate);
 
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
-// `prior`/`n_prior` are the fault words of the ops enqueued before this one: the exact
-// replay skips its work once one of them holds a fault (that earlier fault is reported).
+// Every kernel of the op skips its work once `gate` shows that an earlier program node
+// faulted (that earlier fault is reported).
 // `ev` (optional, 4 events) is recorded before the prefilter, before and after the main
 // kernel, and after the replay.
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
-                                MatmulScratch scratch, unsigned long long *fault,
-                                const unsigned long long *prior, unsigned n_prior,
+                                MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto);
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
-                                  const float *A, const float *B, float *C);
+                                  const float *A, const float *B, float *C, NodeGate gate);
 hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool ta, bool tb, const void *a, const void *b,
-                                void *c);
+                                void *c, NodeGate gate);
 hipError_t launch_native_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                             double rate, bool contracted, void *out);
+                             double rate, bool contracted, void *out, NodeGate gate);
 // `scratch` holds native_mse_scratch_bytes(dtype, n) bytes; `scale` is the rounded
 // reciprocal of the element count in the dtype.
 size_t native_mse_scratch_bytes(int dtype, uint64_t n);
 hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                             void *scratch, double scale, void *out);
+                             void *scratch, double scale, void *out, NodeGate gate);
 
 // Small device utilities (fill kernels rather than memsets, so a captured graph replays
 // them as kernels).
 hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value);
+hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t value);
 
 } // namespace pcu

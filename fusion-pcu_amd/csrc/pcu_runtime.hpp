@@ -83,6 +83,12 @@ struct Ctx {
     // Every faulted node in node order (empty when none).
     pcu_status end_program_all(std::vector<pcu_fault> *faults);
     pcu_status add_node(NodeInfo info, unsigned long long **word);
+    // The program's stage gate sits after the fault words; a node's gate carries its number.
+    unsigned int *gate_word() const { return reinterpret_cast<unsigned int *>(fault_words + kMaxNodes); }
+    NodeGate gate_for(const unsigned long long *word) const
+    {
+        return NodeGate{gate_word(), (unsigned int)(word - fault_words)};
+    }
     pcu_status start_op();
     pcu_status finish_op(pcu_status launched, pcu_fault *fault);
 

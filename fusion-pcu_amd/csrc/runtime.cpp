@@ -84,7 +84,8 @@ pcu_status Ctx::open(int dev)
     for (auto &e : staging_ev)
         if ((st = hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate")))
             return st;
-    if ((st = hip(hipMalloc(&fault_words, sizeof(unsigned long long) * kMaxNodes), "hipMalloc")))
+    // The fault words of a program's nodes, then its stage gate (one 32-bit word).
+    if ((st = hip(hipMalloc(&fault_words, sizeof(unsigned long long) * (kMaxNodes + 1)), "hipMalloc")))
         return st;
     if ((st = hip(hipHostMalloc((void **)&host_words, sizeof(unsigned long long) * kMaxNodes,
                                 hipHostMallocDefault), "hipHostMalloc")))
@@ -248,9 +249,11 @@ pcu_status Ctx::begin_program(bool implicit)
     in_program = true;
     implicit_program = implicit;
     nodes.clear();
-    // Only the words a program uses are read back; fill them all once (a kernel rather
-    // than a memset so the sequence stays capturable).
-    return hip(launch_fill_u64(stream, fault_words, kMaxNodes, kNoFaultWord), "fill fault words");
+    // Only the words a program uses are read back; fill them all once, and open the stage
+    // gate (kernels rather than memsets so the sequence stays capturable).
+    if ((st = hip(launch_fill_u64(stream, fault_words, kMaxNodes, kNoFaultWord), "fill fault words")))
+        return st;
+    return hip(launch_fill_u32(stream, gate_word(), 1, 0xffffffffu), "open stage gate");
 }
 
 pcu_status Ctx::add_node(NodeInfo info, unsigned long long **word)
@@ -486,13 +489,13 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     if ((st = scratch(matmul_scratch_bytes(rows, cols), stream, &sc)))
         return st;
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
-    unsigned prior = (unsigned)(word - fault_words);
+
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     if (profiling)
         for (auto &x : ev)
             x = take_event();
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
-                                        b, c, policy, s, word, fault_words, prior,
+                                        b, c, policy, s, word, gate_for(word),
                                         profiling ? ev : nullptr, matmul_engine);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
@@ -517,7 +520,7 @@ pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const vo
     if (st)
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word), "checked_binary launch");
+    st = hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word, gate_for(word)), "checked_binary launch");
     timer_stop(PCU_KERNEL_BINARY, t, stream);
     return st;
 }
@@ -533,7 +536,7 @@ pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int pol
     if (st)
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_relu(stream, dtype, n, x, out, policy, word), "checked_relu launch");
+    st = hip(launch_relu(stream, dtype, n, x, out, policy, word, gate_for(word)), "checked_relu launch");
     timer_stop(PCU_KERNEL_RELU, t, stream);
     return st;
 }
@@ -550,7 +553,7 @@ pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const voi
     if (st)
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word),
+    st = hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word, gate_for(word)),
              "checked_relu_backward launch");
     timer_stop(PCU_KERNEL_RELU_BACKWARD, t, stream);
     return st;
@@ -570,7 +573,7 @@ pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
     if ((st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &w_relu)))
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu),
+    st = hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu, gate_for(w_add)),
              "checked_add_relu launch");
     timer_stop(PCU_KERNEL_ADD_RELU, t, stream);
     return st;
@@ -596,7 +599,7 @@ pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, floa
     if (st)
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word), "strict_sgd launch");
+    st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word, gate_for(word)), "strict_sgd launch");
     timer_stop(PCU_KERNEL_SGD, t, stream);
     return st;
 }
@@ -657,7 +660,7 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     if ((st = scratch(mse_scratch_bytes(dtype, n), s, &sq)))
         return st;
     hipEvent_t t0 = timer_start(s);
-    if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word),
+    if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word, gate_for(word)),
                   "strict_mse launch")))
         return st;
     timer_stop(PCU_KERNEL_MSE, t0, s);
@@ -682,7 +685,7 @@ pcu_status Ctx::op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint6
     if (rows == 0 || cols == 0)
         return PCU_OK;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_native_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a, b, c),
+    st = hip(launch_native_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a, b, c, gate_for(word)),
              "native_matmul launch");
     timer_stop(PCU_KERNEL_NATIVE_GEMM, t, stream);
     return st;
@@ -707,7 +710,7 @@ pcu_status Ctx::op_native_sgd(int dtype, uint64_t n, const void *w, const void *
     if (st)
         return st;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_native_sgd(stream, dtype, n, w, g, (double)rate, contracted, out), "native_sgd launch");
+    st = hip(launch_native_sgd(stream, dtype, n, w, g, (double)rate, contracted, out, gate_for(word)), "native_sgd launch");
     timer_stop(PCU_KERNEL_NATIVE_SGD, t, stream);
     return st;
 }
@@ -740,7 +743,7 @@ pcu_status Ctx::op_native_mse(int dtype, uint64_t n, const void *p, const void *
     if ((st = scratch(native_mse_scratch_bytes(dtype, n), stream, &sc)))
         return st;
     hipEvent_t t0 = timer_start(stream);
-    st = hip(launch_native_mse(stream, dtype, n, p, t, sc, scale, out), "native_mse launch");
+    st = hip(launch_native_mse(stream, dtype, n, p, t, sc, scale, out, gate_for(word)), "native_mse launch");
     timer_stop(PCU_KERNEL_NATIVE_MSE, t0, stream);
     if (st)
         return st;

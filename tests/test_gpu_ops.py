@@ -479,3 +479,43 @@ def test_program_reports_first_node_and_recovers(ctx, pcu_pkg):
         y = ctx.checked_relu(x)
     ref2, _ = oracle.relu(ref)
     np.testing.assert_array_equal(_bits(y.numpy()), _bits(ref2))
+
+
+@pytest.mark.parametrize("engine_name", ["valu", "mfma_products"])
+def test_program_stage_gate_skips_nodes_after_a_fault(ctx, pcu_pkg, engine_name):
+    """Stage gating (backends/rocm/owned_dispatch/guarded/guarded.rs): once a node has
+    faulted, the kernels of later nodes skip their work; earlier nodes always run, and the
+    reported fault is the earliest one."""
+    ctx.set_matmul_engine(engine_name)
+    try:
+        rng = np.random.default_rng(4)
+        a = rng.uniform(-1, 1, (256, 128)).astype(np.float32)
+        b = rng.uniform(-1, 1, (128, 192)).astype(np.float32)
+        da, db = ctx.upload(a), ctx.upload(b)
+        sentinel = np.full((256, 192), 7.0, np.float32)
+        out = ctx.upload(sentinel)
+        dnan = ctx.upload(np.array([1.0, np.nan, 2.0], np.float32))
+        relu_out = ctx.empty((3,), np.float32)
+        # node 0 faults, node 1 (a MatMul) is skipped
+        with pytest.raises(pcu_pkg.PcuExecutionError) as e:
+            with ctx.program():
+                ctx.checked_relu(dnan, out=relu_out)
+                ctx.strict_matmul(da, db, out=out)
+        f = e.value.tensor_fault
+        assert (f.node, f.element_index, int(f.kind)) == (0, 1, 5)
+        assert np.array_equal(out.numpy().view(np.uint32), sentinel.view(np.uint32))
+        # an earlier node always runs: node 0 (the MatMul) completes, node 1 faults
+        with pytest.raises(pcu_pkg.PcuExecutionError) as e:
+            with ctx.program():
+                ctx.strict_matmul(da, db, out=out)
+                ctx.checked_relu(dnan, out=relu_out)
+        assert e.value.tensor_fault.node == 1
+        ref, _ = oracle.matmul(a, b)
+        np.testing.assert_array_equal(_bits(out.numpy()), _bits(ref))
+        # the next program starts with an open gate
+        out2 = ctx.upload(sentinel)
+        with ctx.program():
+            ctx.strict_matmul(da, db, out=out2)
+        np.testing.assert_array_equal(_bits(out2.numpy()), _bits(ref))
+    finally:
+        ctx.set_matmul_engine("auto")
