@@ -101,12 +101,30 @@ def bench_sgd(pkg, ctx, n, steps, warmup):
     t1 = time.perf_counter()
     k_ms, k_n = ctx.kernel_time("sgd")
     ctx.profile(False)
-    for x in (dw, dg, out):
+    for x in (dw, dg):
         x.free()
     avg = k_ms / max(k_n, 1)
-    return {"elements": n, "ms_per_step": (t1 - t0) * 1e3 / steps, "kernel_avg_ms": avg,
-            "kernel_GBps": 12.0 * n / (avg * 1e-3) / 1e9,
-            "kernel_hbm_frac": 12.0 * n / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    res = {"elements": n, "ms_per_step": (t1 - t0) * 1e3 / steps, "kernel_avg_ms": avg,
+           "kernel_GBps": 12.0 * n / (avg * 1e-3) / 1e9,
+           "kernel_hbm_frac": 12.0 * n / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    # C4's checked add then ReLU over the same size, fused (one kernel, 12 B/element).
+    dw, dg = ctx.upload(syn.normal(41, (n,), 1.0, np.float32)), ctx.upload(syn.normal(42, (n,), 1e-3, np.float32))
+    for _ in range(2):
+        ctx.checked_add_relu(dw, dg, out=out)
+    ctx.synchronize()
+    ctx.profile(True)
+    for _ in range(steps):
+        ctx.checked_add_relu(dw, dg, out=out)
+    ctx.synchronize()
+    a_ms, a_n = ctx.kernel_time("add_relu")
+    ctx.profile(False)
+    for x in (dw, dg, out):
+        x.free()
+    a_avg = a_ms / max(a_n, 1)
+    res["add_relu_kernel_avg_ms"] = a_avg
+    res["add_relu_kernel_GBps"] = 12.0 * n / (a_avg * 1e-3) / 1e9
+    res["add_relu_hbm_frac"] = res["add_relu_kernel_GBps"] / HBM_PEAK_GBS
+    return res
 
 
 def bench_native_matmul(pkg, ctx, m, k, n, dtype, steps, warmup):

@@ -19,6 +19,7 @@
 //                 found lies before the cells still to visit. Returns at once when no cell
 //                 is suspect, which is the fault-free path.
 #include "pcu_device.hpp"
+#include "pcu_gemm_stage.hpp"
 #include "pcu_kernels.hpp"
 
 #include <limits.h>
@@ -60,47 +61,102 @@ __device__ __forceinline__ int wave_min_i32(int v)
     return v;
 }
 
+// Minimum exponents for the underflow screen. Both kernels read their operand once with
+// 16-byte loads (VEC: rows or columns of whole runs, 16-byte aligned).
+
 // out[r] = min over c of ilog2|X[r, c]| for a row-major R x C matrix; one wave per row.
-template <typename T>
+// The first prefilter launch of a MatMul also opens the other kernel's atomicMin targets
+// (init[0, n_init) = kExpNone) and clears the first-suspect word, saving two fill launches.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, uint64_t R,
-                                                      uint64_t C, int *__restrict__ out, NodeGate gate)
+                                                      uint64_t C, int *__restrict__ out,
+                                                      int *__restrict__ init, uint64_t n_init,
+                                                      unsigned long long *suspect, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
-    uint64_t r = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    const uint64_t gtid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint64_t i = gtid; i < n_init; i += (uint64_t)gridDim.x * blockDim.x)
+        init[i] = kExpNone;
+    if (suspect && gtid == 0)
+        *suspect = kNoFault;
+    const uint64_t r = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64;
     if (r >= R)
         return; // whole wave exits together
-    int lane = threadIdx.x % 64;
+    const int lane = threadIdx.x % 64;
     int m = kExpNone;
     const T *row = X + r * C;
-    for (uint64_t c = lane; c < C; c += 64) {
-        int e = ilog2_abs(row[c]);
-        m = e < m ? e : m;
+    if (VEC) {
+        constexpr int P = 16 / sizeof(T);
+        for (uint64_t c = (uint64_t)lane * P; c < C; c += 64 * P) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(row + c);
+            const T *v = reinterpret_cast<const T *>(&q);
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                const int e = ilog2_abs(v[j]);
+                m = e < m ? e : m;
+            }
+        }
+    } else {
+        for (uint64_t c = lane; c < C; c += 64) {
+            const int e = ilog2_abs(row[c]);
+            m = e < m ? e : m;
+        }
     }
     m = wave_min_i32(m);
     if (lane == 0)
         out[r] = m;
 }
 
-// out[c] = min over r of ilog2|X[r, c]|; a block covers 256 columns x 64 rows and folds
-// its partial minimum in with atomicMin (out pre-filled with kExpNone).
-template <typename T>
+// out[c] = min over r of ilog2|X[r, c]|. A block is 64 column-runs (16 bytes each) by 4 row
+// groups over 64 rows; the row groups meet in LDS and the block folds its minimum into out
+// with one atomicMin per column (out opened to kExpNone beforehand).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, uint64_t R,
                                                       uint64_t C, int *__restrict__ out, NodeGate gate)
 {
+    constexpr int P = VEC ? 16 / sizeof(T) : 1;
+    __shared__ int part[4][64 * P];
     if (block_gate_closed(gate))
         return;
-    uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (c >= C)
-        return;
-    uint64_t r0 = (uint64_t)blockIdx.y * 64;
-    uint64_t r1 = r0 + 64 < R ? r0 + 64 : R;
-    int m = kExpNone;
-    for (uint64_t r = r0; r < r1; r++) {
-        int e = ilog2_abs(X[r * C + c]);
-        m = e < m ? e : m;
+    const int cx = threadIdx.x % 64, ry = threadIdx.x / 64;
+    const uint64_t c0 = ((uint64_t)blockIdx.x * 64 + cx) * P;
+    const uint64_t r0 = (uint64_t)blockIdx.y * 64;
+    const uint64_t r1 = r0 + 64 < R ? r0 + 64 : R;
+    int m[P];
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        m[j] = kExpNone;
+    if (c0 < C) {
+        for (uint64_t r = r0 + ry; r < r1; r += 4) {
+            const T *p = X + r * C + c0;
+            if (VEC) {
+                const uint4 q = *reinterpret_cast<const uint4 *>(p);
+                const T *v = reinterpret_cast<const T *>(&q);
+#pragma unroll
+                for (int j = 0; j < P; j++) {
+                    const int e = ilog2_abs(v[j]);
+                    m[j] = e < m[j] ? e : m[j];
+                }
+            } else {
+                const int e = ilog2_abs(p[0]);
+                m[0] = e < m[0] ? e : m[0];
+            }
+        }
     }
-    atomicMin(&out[c], m);
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        part[ry][cx * P + j] = m[j];
+    __syncthreads();
+    if (ry == 0 && c0 < C) {
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            int v = part[0][cx * P + j];
+            for (int g = 1; g < 4; g++)
+                v = part[g][cx * P + j] < v ? part[g][cx * P + j] : v;
+            atomicMin(&out[c0 + j], v);
+        }
+    }
 }
 
 __global__ void k_fill_i32(int *p, uint64_t n, int v)
@@ -126,29 +182,16 @@ __global__ void k_fill_u64(unsigned long long *p, uint64_t n, unsigned long long
 
 // ------------------------------------------------------------------- main tile
 
-constexpr int BM = 128, BN = 128, BK = 8, PAD = 4;
+constexpr int BM = 128, BN = 128; // output tile of every MatMul kernel here
 
-// Four consecutive elements of a row-major operand starting at p[0]; `valid` of them are
-// in bounds (the rest read as +0, which leaves every accumulator unchanged: +0 * +0 = +0
-// and acc + (+0) == acc since an accumulator started at +0 is never -0).
-template <typename T, bool VEC>
-__device__ __forceinline__ void load4(const T *__restrict__ p, int valid, T (&v)[4])
-{
-    if (VEC && valid >= 4) {
-        if (sizeof(T) == 4) {
-            float4 q = *reinterpret_cast<const float4 *>(p);
-            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-        } else {
-            double2 q0 = *reinterpret_cast<const double2 *>(p);
-            double2 q1 = *reinterpret_cast<const double2 *>(p + 2);
-            v[0] = q0.x; v[1] = q0.y; v[2] = q1.x; v[3] = q1.y;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            v[i] = i < valid ? p[i] : (T)0;
-    }
-}
+// Tile shape of the vector-unit kernel: 128 x 128 outputs per 256-thread workgroup (8 x 8
+// per thread); binary64 stages twice as deep a k-slab, halving its barriers.
+template <typename T> struct ValuCfg {
+    static constexpr int BM = 128, BN = 128, BK = sizeof(T) == 4 ? 8 : 16;
+    static constexpr int kThreads = 256;
+    static constexpr int LDA = BM + 4, LDB = BN + 4; // row pitch of the k-major LDS stages
+    static constexpr int EA = BM * BK / kThreads, EB = BN * BK / kThreads;
+};
 
 // NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per
 // (cell, k) and no fault screen.
@@ -160,22 +203,17 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 {
     if (block_gate_closed(gate))
         return;
-    __shared__ __align__(16) T As[2][BK][BM + PAD];
-    __shared__ __align__(16) T Bs[2][BK][BN + PAD];
+    using Cfg = ValuCfg<T>;
+    constexpr int BK = Cfg::BK;
+    __shared__ __align__(16) T As[2][BK][Cfg::LDA];
+    __shared__ __align__(16) T Bs[2][BK][Cfg::LDB];
 
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
 
-    // Grouped tile order: 8 tile-rows share their B panels while they are L2-resident.
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const int group = 8;
-    int bid = blockIdx.x;
-    int per_group = group * tiles_n;
-    int gid = bid / per_group;
-    int first_m = gid * group;
-    int gsize = tiles_m - first_m < group ? tiles_m - first_m : group;
-    int tile_m = first_m + (bid % per_group) % gsize;
-    int tile_n = (bid % per_group) / gsize;
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
 
     T acc[8][8];
@@ -185,65 +223,18 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
         for (int j = 0; j < 8; j++)
             acc[i][j] = (T)0;
 
-    T ra[4], rb[4];
-
-    // Global -> registers for the tile starting at k0.
-    auto fetch = [&](int k0) {
-        if (!TA) { // A is M x K: row m0 + tid/2, columns k0 + (tid&1)*4 .. +3
-            int m = m0 + tid / 2, k = k0 + (tid & 1) * 4;
-            int valid = (m < M) ? (K - k < 4 ? (K - k > 0 ? K - k : 0) : 4) : 0;
-            load4<T, VA>(A + (size_t)m * K + k, valid, ra);
-        } else {   // A is K x M: row k0 + tid/32, columns m0 + (tid%32)*4 .. +3
-            int k = k0 + tid / 32, m = m0 + (tid % 32) * 4;
-            int valid = (k < K) ? (M - m < 4 ? (M - m > 0 ? M - m : 0) : 4) : 0;
-            load4<T, VA>(A + (size_t)k * M + m, valid, ra);
-        }
-        if (!TB) { // B is K x N: row k0 + tid/32, columns n0 + (tid%32)*4 .. +3
-            int k = k0 + tid / 32, n = n0 + (tid % 32) * 4;
-            int valid = (k < K) ? (N - n < 4 ? (N - n > 0 ? N - n : 0) : 4) : 0;
-            load4<T, VB>(B + (size_t)k * N + n, valid, rb);
-        } else {   // B is N x K: row n0 + tid/2, columns k0 + (tid&1)*4 .. +3
-            int n = n0 + tid / 2, k = k0 + (tid & 1) * 4;
-            int valid = (n < N) ? (K - k < 4 ? (K - k > 0 ? K - k : 0) : 4) : 0;
-            load4<T, VB>(B + (size_t)n * K + k, valid, rb);
-        }
-    };
-    // Registers -> LDS buffer `buf` in k-major layout.
-    auto stash = [&](int buf) {
-        if (!TA) {
-            int m = tid / 2, k = (tid & 1) * 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                As[buf][k + i][m] = ra[i];
-        } else {
-            int k = tid / 32, m = (tid % 32) * 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                As[buf][k][m + i] = ra[i];
-        }
-        if (!TB) {
-            int k = tid / 32, n = (tid % 32) * 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                Bs[buf][k][n + i] = rb[i];
-        } else {
-            int n = tid / 2, k = (tid & 1) * 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                Bs[buf][k + i][n] = rb[i];
-        }
-    };
+    SlabStager<T, Cfg, TA, TB, VA, VB> stage;
 
     const int ktiles = (K + BK - 1) / BK;
     if (ktiles > 0) {
-        fetch(0);
-        stash(0);
+        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        stage.stash(As[0], Bs[0], tid);
     }
     __syncthreads();
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < ktiles)
-            fetch((kt + 1) * BK);
+            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
 #pragma unroll(sizeof(T) == 4 ? BK : 2)
         for (int k = 0; k < BK; k++) {
             T a[8], b[8];
@@ -267,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                 }
         }
         if (kt + 1 < ktiles)
-            stash(cur ^ 1);
+            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
         __syncthreads();
     }
 
@@ -410,19 +401,67 @@ hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t 
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Minimum exponent of each row of a stored R x C matrix (rows) or of each column (cols).
+// One exponent job: per-row minima of a stored R x C matrix (rows) or per-column (cols).
+template <typename T> struct ExpJob {
+    const T *X;
+    uint64_t R, C;
+    bool rows;
+    int *out;
+};
+
 template <typename T>
-static void exp_min(hipStream_t s, const T *X, uint64_t R, uint64_t C, bool along_rows, int *out,
-                    NodeGate gate)
+static void exp_rows(hipStream_t s, const ExpJob<T> &j, int *init, uint64_t n_init,
+                     unsigned long long *suspect, NodeGate gate)
 {
-    if (along_rows) {
-        hipLaunchKernelGGL(k_exp_min_rows<T>, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, X, R, C, out, gate);
-    } else {
-        unsigned fg = (unsigned)((C + 255) / 256 < 1024 ? (C + 255) / 256 : 1024);
-        hipLaunchKernelGGL(k_fill_i32, dim3(fg ? fg : 1), dim3(256), 0, s, out, C, kExpNone);
-        hipLaunchKernelGGL(k_exp_min_cols<T>, dim3((unsigned)((C + 255) / 256), (unsigned)((R + 63) / 64)),
-                           dim3(256), 0, s, X, R, C, out, gate);
+    const bool vec = j.C % (16 / sizeof(T)) == 0 && aligned16(j.X);
+    const dim3 grid((unsigned)((j.R + 3) / 4));
+    if (vec)
+        hipLaunchKernelGGL((k_exp_min_rows<T, true>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, init, n_init, suspect, gate);
+    else
+        hipLaunchKernelGGL((k_exp_min_rows<T, false>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, init, n_init, suspect, gate);
+}
+
+template <typename T>
+static void exp_cols(hipStream_t s, const ExpJob<T> &j, NodeGate gate)
+{
+    constexpr uint64_t P = 16 / sizeof(T);
+    const bool vec = j.C % P == 0 && aligned16(j.X);
+    const uint64_t cols_per_block = 64 * (vec ? P : 1);
+    const dim3 grid((unsigned)((j.C + cols_per_block - 1) / cols_per_block), (unsigned)((j.R + 63) / 64));
+    if (vec)
+        hipLaunchKernelGGL((k_exp_min_cols<T, true>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, gate);
+    else
+        hipLaunchKernelGGL((k_exp_min_cols<T, false>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, gate);
+}
+
+// Prefilter of op(A) rows and op(B) columns, plus the first-suspect word: the rows jobs run
+// first and open the columns jobs' targets.
+template <typename T>
+static void prefilter(hipStream_t s, const ExpJob<T> &ja, const ExpJob<T> &jb,
+                      unsigned long long *suspect, NodeGate gate)
+{
+    const ExpJob<T> *rows[2], *cols[2];
+    int nr = 0, nc = 0;
+    for (const ExpJob<T> *j : {&ja, &jb}) {
+        if (j->rows)
+            rows[nr++] = j;
+        else
+            cols[nc++] = j;
     }
+    if (nr == 0) {
+        // Both jobs fold with atomics: open their targets and the suspect word first.
+        for (int k = 0; k < nc; k++) {
+            const unsigned fg = (unsigned)((cols[k]->C + 255) / 256 < 1024 ? (cols[k]->C + 255) / 256 : 1024);
+            hipLaunchKernelGGL(k_fill_i32, dim3(fg ? fg : 1), dim3(256), 0, s, cols[k]->out, cols[k]->C, kExpNone);
+        }
+        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, suspect, (uint64_t)1, (unsigned long long)kNoFault);
+    } else {
+        exp_rows<T>(s, *rows[0], nc ? cols[0]->out : nullptr, nc ? cols[0]->C : 0, suspect, gate);
+        if (nr == 2)
+            exp_rows<T>(s, *rows[1], nullptr, 0, nullptr, gate);
+    }
+    for (int k = 0; k < nc; k++)
+        exp_cols<T>(s, *cols[k], gate);
 }
 
 template <typename T, bool TA, bool TB>
@@ -461,12 +500,15 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (ev)
         (void)hipEventRecord(ev[0], s);
     if (risk && K > 0) {
-        exp_min<T>(s, A, ta ? K : M, ta ? M : K, !ta, sc.row_exp, gate);
-        exp_min<T>(s, B, tb ? N : K, tb ? K : N, tb, sc.col_exp, gate);
-    } else if (risk) {
-        risk = 0; // an empty reduction has no arithmetic events
+        // op(A) row r is stored row r (A is M x K) or stored column r (A is K x M); op(B)
+        // column c is stored column c (B is K x N) or stored row c (B is N x K).
+        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, sc.row_exp};
+        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, sc.col_exp};
+        prefilter<T>(s, ja, jb, sc.suspect, gate);
+    } else {
+        risk = 0; // AllowGradual, or an empty reduction: no underflow screen
+        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);
     }
-    hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);
     dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)));
     const int m = (int)M, n = (int)N, k = (int)K;
     if (ev)

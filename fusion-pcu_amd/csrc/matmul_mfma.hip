@@ -22,6 +22,7 @@
 // Fault screening (non-finite result, exponent prefilter) and the exact replay of suspect
 // cells are shared with the VALU kernel.
 #include "pcu_device.hpp"
+#include "pcu_gemm_stage.hpp"
 #include "pcu_kernels.hpp"
 
 #pragma clang fp contract(off)
@@ -41,97 +42,6 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
     static constexpr int EA = BM * BK / kThreads;    // A elements one thread stages per slab
     static constexpr int EB = BN * BK / kThreads;
     static_assert(EA % 4 == 0 && EB % 4 == 0, "staging moves whole float4s");
-};
-
-// E consecutive elements of a row-major operand at p; `valid` of them in bounds (the rest
-// read as +0: a zero product leaves every accumulator unchanged).
-template <int E, bool VEC>
-__device__ __forceinline__ void load_run(const float *__restrict__ p, int valid, float (&v)[E])
-{
-    if (VEC && valid >= E) {
-#pragma unroll
-        for (int q = 0; q < E / 4; q++) {
-            const float4 x = reinterpret_cast<const float4 *>(p)[q];
-            v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < E; i++)
-            v[i] = i < valid ? p[i] : 0.0f;
-    }
-}
-
-__device__ __forceinline__ int clamp_valid(int rem, int e) { return rem < 0 ? 0 : (rem > e ? e : rem); }
-
-// Output tile of workgroup `bid`: blocks are dealt round-robin to the 8 XCDs, so each XCD
-// is given one contiguous run of the tile order (its L2 then holds that run's panels),
-// and inside the order 8 tile-rows share each B panel.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn)
-{
-    const int T = tiles_m * tiles_n;
-    const int xcd = bid % 8, slot = bid / 8;
-    const int L = xcd * (T / 8) + (xcd < T % 8 ? xcd : T % 8) + slot;
-    const int group = 8;
-    const int per_group = group * tiles_n;
-    const int gid = L / per_group;
-    const int first_m = gid * group;
-    const int gsize = tiles_m - first_m < group ? tiles_m - first_m : group;
-    tm = first_m + (L % per_group) % gsize;
-    tn = (L % per_group) / gsize;
-}
-
-// Global -> registers -> k-major LDS staging of one BK-deep slab of op(A) (BM x BK) and
-// op(B) (BK x BN). Out-of-range elements stage as +0.
-template <class Cfg, bool TA, bool TB, bool VA, bool VB> struct SlabStager {
-    static constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
-    float ra[EA], rb[EB];
-
-    __device__ __forceinline__ void fetch(const float *__restrict__ A, const float *__restrict__ B,
-                                          int M, int N, int K, int m0, int n0, int k0, int tid)
-    {
-        if (!TA) { // A is M x K: BK/EA threads per row
-            const int m = m0 + tid / (BK / EA), k = k0 + (tid % (BK / EA)) * EA;
-            load_run<EA, VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k, EA) : 0, ra);
-        } else {   // A is K x M: BM/EA threads per k-row
-            const int k = k0 + tid / (BM / EA), m = m0 + (tid % (BM / EA)) * EA;
-            load_run<EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
-        }
-        if (!TB) { // B is K x N: BN/EB threads per k-row
-            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
-            load_run<EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
-        } else {   // B is N x K: BK/EB threads per row
-            const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
-            load_run<EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
-        }
-    }
-
-    __device__ __forceinline__ void stash(float (*As)[Cfg::LDA], float (*Bs)[Cfg::LDB], int tid) const
-    {
-        if (!TA) {
-            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
-#pragma unroll
-            for (int i = 0; i < EA; i++)
-                As[k + i][m] = ra[i];
-        } else {
-            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
-#pragma unroll
-            for (int q = 0; q < EA / 4; q++)
-                *reinterpret_cast<float4 *>(&As[k][m + 4 * q]) =
-                    make_float4(ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
-        }
-        if (!TB) {
-            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
-#pragma unroll
-            for (int q = 0; q < EB / 4; q++)
-                *reinterpret_cast<float4 *>(&Bs[k][n + 4 * q]) =
-                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
-        } else {
-            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
-#pragma unroll
-            for (int i = 0; i < EB; i++)
-                Bs[k + i][n] = rb[i];
-        }
-    }
 };
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
@@ -161,7 +71,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         for (int r = 0; r < 16; r++)
             acc[t][r] = 0.0f;
 
-    SlabStager<Cfg, TA, TB, VA, VB> stage;
+    SlabStager<float, Cfg, TA, TB, VA, VB> stage;
 
     v32f zero;
 #pragma unroll
@@ -351,7 +261,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_ge
         for (int r = 0; r < 16; r++)
             acc[t][r] = 0.0f;
 
-    SlabStager<Cfg, TA, TB, VA, VB> stage;
+    SlabStager<float, Cfg, TA, TB, VA, VB> stage;
     const int ktiles = (K + BK - 1) / BK;
     if (ktiles > 0) {
         stage.fetch(A, B, M, N, K, m0, n0, 0, tid);

@@ -1,0 +1,120 @@
+// Global -> LDS staging shared by the strict and native MatMul tile kernels (gfx950).
+//
+// A workgroup computes a BM x BN output tile and walks k in slabs of BK. Each slab of op(A)
+// (BM x BK) and op(B) (BK x BN) goes global -> registers -> a k-major LDS stage, so both
+// operands are read from LDS along a row of the stage. Each thread moves EA elements of A and
+// EB of B per slab as 16-byte runs; elements outside the matrices stage as +0 (a zero product
+// leaves every accumulator unchanged).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pcu {
+
+// E consecutive elements of a row-major operand at p; `valid` of them in bounds.
+template <typename T, int E, bool VEC>
+__device__ __forceinline__ void load_run(const T *__restrict__ p, int valid, T (&v)[E])
+{
+    constexpr int P = 16 / (int)sizeof(T); // elements per 16-byte load
+    if (VEC && valid >= E) {
+#pragma unroll
+        for (int q = 0; q < E / P; q++) {
+            const uint4 x = reinterpret_cast<const uint4 *>(p)[q];
+            const T *xs = reinterpret_cast<const T *>(&x);
+#pragma unroll
+            for (int j = 0; j < P; j++)
+                v[P * q + j] = xs[j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < E; i++)
+            v[i] = i < valid ? p[i] : (T)0;
+    }
+}
+
+__device__ __forceinline__ int clamp_valid(int rem, int e) { return rem < 0 ? 0 : (rem > e ? e : rem); }
+
+// E elements to LDS at p as 16-byte stores (p 16-byte aligned).
+template <typename T, int E>
+__device__ __forceinline__ void store_run(T *p, const T (&v)[E])
+{
+    constexpr int P = 16 / (int)sizeof(T);
+#pragma unroll
+    for (int q = 0; q < E / P; q++) {
+        uint4 x;
+        T *xs = reinterpret_cast<T *>(&x);
+#pragma unroll
+        for (int j = 0; j < P; j++)
+            xs[j] = v[P * q + j];
+        reinterpret_cast<uint4 *>(p)[q] = x;
+    }
+}
+
+// Output tile of workgroup `bid`: blocks are dealt round-robin to the 8 XCDs, so each XCD
+// is given one contiguous run of the tile order (its L2 then holds that run's panels),
+// and inside the order 8 tile-rows share each B panel.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn)
+{
+    const int T = tiles_m * tiles_n;
+    const int xcd = bid % 8, slot = bid / 8;
+    const int L = xcd * (T / 8) + (xcd < T % 8 ? xcd : T % 8) + slot;
+    const int group = 8;
+    const int per_group = group * tiles_n;
+    const int gid = L / per_group;
+    const int first_m = gid * group;
+    const int gsize = tiles_m - first_m < group ? tiles_m - first_m : group;
+    tm = first_m + (L % per_group) % gsize;
+    tn = (L % per_group) / gsize;
+}
+
+// Cfg provides T-independent BM, BN, BK, kThreads, EA, EB, LDA, LDB.
+template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct SlabStager {
+    static constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
+    static_assert(EA % (16 / sizeof(T)) == 0 && EB % (16 / sizeof(T)) == 0,
+                  "staging moves whole 16-byte runs");
+    T ra[EA], rb[EB];
+
+    __device__ __forceinline__ void fetch(const T *__restrict__ A, const T *__restrict__ B, int M,
+                                          int N, int K, int m0, int n0, int k0, int tid)
+    {
+        if (!TA) { // A is M x K: BK/EA threads per row
+            const int m = m0 + tid / (BK / EA), k = k0 + (tid % (BK / EA)) * EA;
+            load_run<T, EA, VA>(A + (size_t)m * K + k, m < M ? clamp_valid(K - k, EA) : 0, ra);
+        } else {   // A is K x M: BM/EA threads per k-row
+            const int k = k0 + tid / (BM / EA), m = m0 + (tid % (BM / EA)) * EA;
+            load_run<T, EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
+        }
+        if (!TB) { // B is K x N: BN/EB threads per k-row
+            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
+            load_run<T, EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
+        } else {   // B is N x K: BK/EB threads per row
+            const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
+            load_run<T, EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
+        }
+    }
+
+    __device__ __forceinline__ void stash(T (*As)[Cfg::LDA], T (*Bs)[Cfg::LDB], int tid) const
+    {
+        if (!TA) {
+            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
+#pragma unroll
+            for (int i = 0; i < EA; i++)
+                As[k + i][m] = ra[i];
+        } else {
+            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
+            store_run<T, EA>(&As[k][m], ra);
+        }
+        if (!TB) {
+            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
+            store_run<T, EB>(&Bs[k][n], rb);
+        } else {
+            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
+                Bs[k + i][n] = rb[i];
+        }
+    }
+};
+
+} // namespace pcu
