@@ -541,19 +541,20 @@ template <>
 __device__ __forceinline__ double from_bits<double>(uint64_t b) { return __longlong_as_double((long long)b); }
 
 // ----------------------------------------------------- ordered sum: pipeline
-// The squares are cut into chunks of 512*P elements (P = 16 for binary32, 8 for binary64;
-// thread t of a workgroup holds elements [base + P*t, base + P*t + P)).
-//  A  k_mse_chunk_sums       per-chunk sum in binary64: the prefix of these estimates
-//                            where the running total stands at each chunk start;
-//  B  k_mse_chunk_summaries  per chunk, in parallel, the summary (count added for an even
+// The squares are cut into chunks of 512*P elements (P = 16 for binary32, 8 for binary64).
+//  A  k_mse_chunk_sums       per-chunk sum in binary64 (an estimate: order does not matter);
+//  B  k_mse_chunk_prefix     the exclusive prefix of those sums: about where the running
+//                            total stands at each chunk start;
+//  C  k_mse_chunk_summaries  per chunk, in parallel, the summary (count added for an even
 //                            and an odd start) of the whole chunk inside one binade, for
 //                            the one or two binades the estimate allows;
-//  C  k_mse_ordered_walk     one workgroup walks the chunks in order: where a summary
-//                            exists for the running binade and does not reach its end,
-//                            the chunk folds in O(1); any other chunk (a binade crossing,
-//                            or an estimate that missed) is run exactly, element by
-//                            element in parallel, with the crossing steps as real Adds.
-// The estimate only decides how fast a chunk goes, never its value.
+//  D  k_mse_ordered_walk     one workgroup walks the chunks in order, 512 at a time: a scan
+//                            of the summaries made for the running binade folds every chunk
+//                            before the first one that has no such summary or reaches the
+//                            binade's end. That chunk runs exactly, in windows sized from its
+//                            estimate: each window is a parallel scan whose first step to
+//                            reach the binade's end runs as a real, checked Add.
+// The estimate only decides how fast the walk goes, never its value.
 
 struct ChunkSummary {
     uint64_t r0, r1;   // count added starting from an even / odd count
@@ -561,7 +562,7 @@ struct ChunkSummary {
     uint32_t pad;
 };
 constexpr int32_t kNoPhase = INT32_MIN;
-constexpr int kWalkBatch = kSumThreads / 2; // chunks whose summaries are staged per pass
+constexpr uint32_t kNoStep = 0xffffffffu;
 
 template <typename T> __device__ __forceinline__ uint64_t sum_chunk_len() { return (uint64_t)kSumThreads * SumBits<T>::kPer; }
 
@@ -652,89 +653,157 @@ __device__ __forceinline__ void block_scan(SumScan mine, int lane, int wave, Sum
     excl = scan_compose(before, lane_excl);
 }
 
-// Exact fold of one chunk from the phase (ue, m, mmax): the scan finds the first step that
-// would reach the binade's end, that step runs as a real checked Add, and the rest of the
-// chunk is scanned again in the new binade. Returns false when an Add faulted (recorded).
+// A chunk staged in LDS for its exact run: element i sits at slot i + i / kPadEvery (one
+// spare slot per 128 bytes), so that runs of 2..16 consecutive elements per thread spread
+// over distinct banks.
+template <typename T> struct ChunkLds {
+    using U = typename SumBits<T>::U;
+    static constexpr uint32_t kPadEvery = 128 / sizeof(U);
+    static constexpr uint32_t kLen = kSumThreads * SumBits<T>::kPer;
+    static constexpr uint32_t kSlots = kLen + kLen / kPadEvery;
+    __device__ static __forceinline__ uint32_t slot(uint32_t i) { return i + i / kPadEvery; }
+};
+
+// Shared state of the ordered walk. The step slots are double-buffered by iteration: one
+// is written during an iteration while the other is cleared for the next.
+template <typename T> struct WalkShared {
+    typename SumBits<T>::U vals[ChunkLds<T>::kSlots];
+    SumScan wave_tot[kSumThreads / 64];
+    uint64_t m_first[2];             // count standing before the stopping chunk
+    uint32_t first[2];               // stopping chunk of a batch (offset), kNoStep: none
+    uint32_t at[2];                  // crossing element of a window (offset), kNoStep: none
+    typename SumBits<T>::U total;    // total after the crossing Add
+    int stop;                        // the crossing Add faulted
+    uint64_t limit;
+};
+
+// Summary of elements [i0, min(i0 + PER, i1)) of the staged chunk on the quantum 2^ue.
+template <typename T, int PER>
+__device__ __forceinline__ SumScan run_scan(const typename SumBits<T>::U *vals, uint32_t i0,
+                                            uint32_t i1, int ue)
+{
+    SumScan s = scan_identity();
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        if (i0 + j < i1) {
+            uint64_t nn;
+            uint32_t cls;
+            sum_elem<T>(vals[ChunkLds<T>::slot(i0 + j)], ue, nn, cls);
+            s = scan_compose(s, scan_elem(nn, cls));
+        }
+    }
+    return s;
+}
+
 template <typename T>
-__device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, bool vec_ok,
-                            uint64_t base, uint64_t limit, int policy,
-                            unsigned long long *fault, int &ue, uint64_t &m, uint64_t &mmax,
-                            SumScan *wave_tot, uint64_t *wave_key,
-                            typename SumBits<T>::U *s_total, int *s_stop, const NodeGate &gate)
+__device__ __forceinline__ SumScan run_scan_per(const typename SumBits<T>::U *vals, uint32_t per,
+                                                uint32_t i0, uint32_t i1, int ue)
+{
+    constexpr int P = SumBits<T>::kPer;
+    if (per == 1)
+        return run_scan<T, 1>(vals, i0, i1, ue);
+    if (per == 2)
+        return run_scan<T, 2>(vals, i0, i1, ue);
+    if (per == 4)
+        return run_scan<T, 4>(vals, i0, i1, ue);
+    if (P > 8 && per == 8)
+        return run_scan<T, 8>(vals, i0, i1, ue);
+    return run_scan<T, P>(vals, i0, i1, ue);
+}
+
+// Elements per thread of the next window: a power of two covering about twice the expected
+// distance to the binade's end (room quanta of 2^ue at the chunk's mean square), from one
+// element per thread up to the whole chunk.
+template <typename T>
+__device__ __forceinline__ uint32_t window_per(uint64_t room, int ue, double mean)
+{
+    constexpr uint32_t P = SumBits<T>::kPer;
+    const double span = mean > 0.0 ? 2.0 * ldexp((double)room, ue) / (mean * kSumThreads) : (double)P;
+    uint32_t per = 1;
+    while (per < P && (double)per < span)
+        per <<= 1;
+    return per;
+}
+
+// Exact fold of the chunk at base (len elements) from the phase (ue, m, mmax), window by
+// window: the one thread whose run holds the window's first step to reach the binade's end
+// executes that step as the contract's Add, and the next window starts after it in the new
+// binade. Returns false when an Add faulted (recorded).
+template <typename T>
+__device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint64_t base,
+                            uint32_t len, double mean, int policy, unsigned long long *fault,
+                            int &ue, uint64_t &m, uint64_t &mmax, WalkShared<T> &sh,
+                            const NodeGate &gate)
 {
     using U = typename SumBits<T>::U;
-    constexpr int P = SumBits<T>::kPer;
-    constexpr int kWaves = kSumThreads / 64;
+    constexpr uint32_t P = SumBits<T>::kPer;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    U cur[P];
-    load_chunk<T>(src, vec_ok, base, limit, tid, cur);
-    const uint64_t first = base + (uint64_t)tid * P;
-    uint64_t start = base; // first element of the chunk not yet folded into m
-    for (;;) {
-        SumScan mine = scan_identity();
-#pragma unroll
-        for (int j = 0; j < P; j++) {
-            uint64_t nn;
-            uint32_t cls;
-            sum_elem<T>(cur[j], ue, nn, cls);
-            if (first + j >= start && first + j < limit)
-                mine = scan_compose(mine, scan_elem(nn, cls));
-        }
+    for (uint32_t i = tid; i < len; i += kSumThreads)
+        sh.vals[ChunkLds<T>::slot(i)] = src[base + i];
+    if (tid == 0)
+        sh.at[0] = sh.at[1] = kNoStep;
+    __syncthreads();
+    uint32_t off = 0, per = window_per<T>(mmax - m, ue, mean);
+    for (int it = 0; off < len; it++) {
+        const int slot = it & 1;
+        const uint32_t wend = off + per * kSumThreads < len ? off + per * kSumThreads : len;
+        const uint32_t i0 = off + (uint32_t)tid * per;
+        const uint32_t i1 = i0 + per < wend ? i0 + per : wend;
+        const SumScan mine = run_scan_per<T>(sh.vals, per, i0, i1, ue);
         SumScan before, total;
-        block_scan(mine, lane, wave, wave_tot, before, total);
-        // Walk this thread's elements from its exact starting state.
+        block_scan(mine, lane, wave, sh.wave_tot, before, total);
         const uint32_t p0 = (uint32_t)(m & 1u);
-        uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
-        uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
-        uint64_t key = kNoFault, key_m = 0;
-        U key_bits = 0;
-#pragma unroll
-        for (int j = 0; j < P; j++) {
-            uint64_t nn;
-            uint32_t cls;
-            sum_elem<T>(cur[j], ue, nn, cls);
-            if (first + j >= start && first + j < limit && key == kNoFault) {
-                const uint64_t r = sum_step(nn, cls, pt);
-                if (cls == kRForce || mt + r >= mmax) {
-                    key = first + j;
-                    key_bits = cur[j];
-                    key_m = mt;
-                } else {
-                    mt += r;
-                    pt = (pt + (uint32_t)r) & 1u;
+        const uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+        const uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
+        // Counts only grow along the window, so exactly one run can start below the
+        // binade's end and reach it.
+        if (mt < mmax && sat_add(mt, pt ? mine.r1 : mine.r0) >= mmax) {
+            uint64_t mm = mt;
+            uint32_t pp = pt;
+            for (uint32_t i = i0; i < i1; i++) {
+                const U b = sh.vals[ChunkLds<T>::slot(i)];
+                uint64_t nn;
+                uint32_t cls;
+                sum_elem<T>(b, ue, nn, cls);
+                const uint64_t r = sum_step(nn, cls, pp);
+                if (cls == kRForce || mm + r >= mmax) {
+                    // The crossing step, executed and checked as the contract's Add.
+                    const T acc = from_bits<T>(sum_bits<T>(ue, mm));
+                    const T s_i = from_bits<T>(b);
+                    const T res = acc + s_i;
+                    const uint32_t kind = classify_add(acc, s_i, res, policy);
+                    if (kind != kOk) {
+                        atomicMin(fault, (unsigned long long)pack_fault(3 * (base + i) + 2, kind));
+                        gate_record(gate);
+                        sh.stop = 1;
+                    } else {
+                        sh.stop = 0;
+                        sh.total = (U)bits_of(res);
+                    }
+                    sh.at[slot] = i;
+                    break;
                 }
+                mm += r;
+                pp = (pp + (uint32_t)r) & 1u;
             }
         }
-        const uint64_t wk = wave_min_u64(key);
-        if (lane == 0)
-            wave_key[wave] = wk;
         __syncthreads();
-        const uint64_t cross = wave_min_u64(lane < kWaves ? wave_key[lane] : kNoFault);
-        if (cross == kNoFault) {
+        const uint32_t at = sh.at[slot];
+        if (tid == 0)
+            sh.at[slot ^ 1] = kNoStep;
+        if (at == kNoStep) {
             m = sat_add(m, p0 ? total.r1 : total.r0);
-            return true;
+            off = wend;
+            per = per * 2 < P ? per * 2 : P;
+            continue;
         }
-        if (key == cross) {
-            // The crossing step, executed and checked as the contract's Add.
-            const T acc = from_bits<T>(sum_bits<T>(ue, key_m));
-            const T s_i = from_bits<T>(key_bits);
-            const T r = acc + s_i;
-            const uint32_t kind = classify_add(acc, s_i, r, policy);
-            if (kind != kOk) {
-                atomicMin(fault, (unsigned long long)pack_fault(3 * cross + 2, kind));
-                gate_record(gate);
-                *s_stop = 1;
-            } else {
-                *s_stop = 0;
-                *s_total = (U)bits_of(r);
-            }
-        }
-        __syncthreads();
-        if (*s_stop)
+        if (sh.stop)
             return false;
-        sum_phase<T>(*s_total, ue, m, mmax);
-        start = cross + 1;
+        sum_phase<T>(sh.total, ue, m, mmax);
+        off = at + 1;
+        per = window_per<T>(mmax - m, ue, mean);
     }
+    return true;
 }
 
 // A: chunk sums in binary64 (order inside a chunk does not matter: only an estimate).
@@ -762,34 +831,58 @@ __global__ __launch_bounds__(256) void k_mse_chunk_sums(const T *__restrict__ sq
         chunk_sum[blockIdx.x] = (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-// B: summary of chunk blockIdx.x for candidate blockIdx.y (0: the binade of the estimate
+// B: exclusive prefix of the chunk sums (one workgroup; each thread a contiguous run).
+constexpr int kPrefixThreads = 1024;
+__global__ __launch_bounds__(kPrefixThreads) void k_mse_chunk_prefix(const double *__restrict__ chunk_sum,
+                                                                     uint64_t chunks,
+                                                                     double *__restrict__ pre,
+                                                                     NodeGate gate)
+{
+    if (block_gate_closed(gate))
+        return;
+    __shared__ double wave_sum[kPrefixThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t per = (chunks + kPrefixThreads - 1) / kPrefixThreads;
+    const uint64_t i0 = (uint64_t)tid * per;
+    const uint64_t i1 = i0 + per < chunks ? i0 + per : chunks;
+    double own = 0.0;
+    for (uint64_t i = i0; i < i1; i++)
+        own += chunk_sum[i];
+    double inc = own;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = __shfl_up(inc, d, 64);
+        if (lane >= d)
+            inc += o;
+    }
+    if (lane == 63)
+        wave_sum[wave] = inc;
+    __syncthreads();
+    double run = inc - own;
+    for (int w = 0; w < wave; w++)
+        run += wave_sum[w];
+    for (uint64_t i = i0; i < i1; i++) {
+        pre[i] = run;
+        run += chunk_sum[i];
+    }
+}
+
+// C: summary of chunk blockIdx.x for candidate blockIdx.y (0: the binade of the estimate
 // less 1/512 of it, 1: plus 1/512; the second is skipped when both agree).
 template <typename T>
 __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     const T *__restrict__ sq, uint64_t n, const unsigned long long *fault,
-    const double *__restrict__ chunk_sum, ChunkSummary *__restrict__ summ, NodeGate gate)
+    const double *__restrict__ chunk_pre, ChunkSummary *__restrict__ summ, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
     using U = typename SumBits<T>::U;
     constexpr int P = SumBits<T>::kPer;
     __shared__ SumScan wave_tot[kSumThreads / 64];
-    __shared__ double part[kSumThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t c = blockIdx.x;
     const uint64_t limit = sum_limit(fault, n);
-    double pre = 0.0;
-    for (uint64_t j = tid; j < c; j += kSumThreads)
-        pre += chunk_sum[j];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        pre += __shfl_xor(pre, off, 64);
-    if (lane == 0)
-        part[wave] = pre;
-    __syncthreads();
-    pre = 0.0;
-    for (int w = 0; w < kSumThreads / 64; w++)
-        pre += part[w];
+    const double pre = chunk_pre[c];
     const int32_t lo = phase_ue_of<T>(pre * (1.0 - 1.0 / 512)), hi = phase_ue_of<T>(pre * (1.0 + 1.0 / 512));
     ChunkSummary *out = summ + 2 * c + blockIdx.y;
     if (blockIdx.y == 1 && hi == lo) {
@@ -818,56 +911,73 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
         *out = ChunkSummary{total.r0, total.r1, ue, 0};
 }
 
-// C: the ordered walk (one workgroup), then total (/) count.
+// D: the ordered walk (one workgroup), then total (/) count.
 template <typename T>
-__global__ __launch_bounds__(kSumThreads) void k_mse_ordered_walk(
+__global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_mse_ordered_walk(
     const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
-    unsigned long long *fault, const ChunkSummary *__restrict__ summ, NodeGate gate)
+    unsigned long long *fault, const double *__restrict__ chunk_sum,
+    const ChunkSummary *__restrict__ summ, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
     using U = typename SumBits<T>::U;
-    __shared__ SumScan wave_tot[kSumThreads / 64];
-    __shared__ uint64_t wave_key[kSumThreads / 64];
-    __shared__ ChunkSummary staged[2 * kWalkBatch];
-    __shared__ uint64_t s_limit;
-    __shared__ U s_total;
-    __shared__ int s_stop;
-    const int tid = threadIdx.x;
-    if (tid == 0)
-        s_limit = sum_limit(fault, n);
+    __shared__ WalkShared<T> sh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        sh.limit = sum_limit(fault, n);
+        sh.first[0] = sh.first[1] = kNoStep;
+    }
     __syncthreads();
-    const uint64_t limit = s_limit;
+    const uint64_t limit = sh.limit;
     const U *src = reinterpret_cast<const U *>(sq);
-    const bool vec_ok = ((uintptr_t)sq & 15u) == 0;
     const uint64_t L = sum_chunk_len<T>();
     const uint64_t chunks = (limit + L - 1) / L;
 
     int ue;
     uint64_t m, mmax;
     sum_phase<T>((U)0, ue, m, mmax); // the total starts at +0
-    for (uint64_t c0 = 0; c0 < chunks; c0 += kWalkBatch) {
-        const uint64_t c1 = c0 + kWalkBatch < chunks ? c0 + kWalkBatch : chunks;
-        __syncthreads(); // everyone is done with the previous batch
-        if (c0 * 2 + tid < c1 * 2)
-            staged[tid] = summ[c0 * 2 + tid];
-        __syncthreads();
-        for (uint64_t c = c0; c < c1; c++) {
-            // Uniform across the workgroup: every thread reads the same staged entries.
-            const ChunkSummary a = staged[2 * (c - c0)], b = staged[2 * (c - c0) + 1];
-            const uint32_t p0 = (uint32_t)(m & 1u);
-            const bool ha = a.ue == ue, hb = b.ue == ue;
-            if (ha || hb) {
-                const uint64_t r = ha ? (p0 ? a.r1 : a.r0) : (p0 ? b.r1 : b.r0);
-                if (m + r < mmax) {
-                    m += r;
-                    continue;
-                }
+    uint64_t c0 = 0;
+    for (int it = 0; c0 < chunks; it++) {
+        const int slot = it & 1;
+        const uint64_t c = c0 + tid;
+        SumScan mine = scan_identity();
+        if (c < chunks) {
+            const ChunkSummary a = summ[2 * c], b = summ[2 * c + 1];
+            if (a.ue == ue || b.ue == ue) {
+                const uint64_t r0 = a.ue == ue ? a.r0 : b.r0, r1 = a.ue == ue ? a.r1 : b.r1;
+                mine = SumScan{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
+            } else {
+                mine = SumScan{kSumBig, kSumBig, 2u}; // no summary for this binade: stop here
             }
-            if (!exact_chunk<T>(src, vec_ok, c * L, limit, policy, fault, ue, m, mmax, wave_tot,
-                                wave_key, &s_total, &s_stop, gate))
-                return;
         }
+        SumScan before, total;
+        block_scan(mine, lane, wave, sh.wave_tot, before, total);
+        const uint32_t p0 = (uint32_t)(m & 1u);
+        const uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+        const uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
+        if (c < chunks && mt < mmax && sat_add(mt, pt ? mine.r1 : mine.r0) >= mmax) {
+            sh.first[slot] = (uint32_t)tid;
+            sh.m_first[slot] = mt;
+        }
+        __syncthreads();
+        const uint32_t first = sh.first[slot];
+        const uint64_t m_first = sh.m_first[slot];
+        if (tid == 0)
+            sh.first[slot ^ 1] = kNoStep;
+        if (first == kNoStep) {
+            m = sat_add(m, p0 ? total.r1 : total.r0);
+            c0 += kSumThreads;
+            continue;
+        }
+        // Chunks before the stopping one fold; it runs exactly from the count before it.
+        m = m_first;
+        const uint64_t cc = c0 + first;
+        const uint64_t base = cc * L;
+        const uint32_t len = (uint32_t)(base + L <= limit ? L : limit - base);
+        if (!exact_chunk<T>(src, base, len, chunk_sum[cc] / (double)len, policy, fault, ue, m,
+                            mmax, sh, gate))
+            return;
+        c0 = cc + 1;
     }
     if (limit < n || tid != 0)
         return;
@@ -1146,7 +1256,7 @@ size_t mse_scratch_bytes(int dtype, uint64_t n)
 {
     const size_t es = dtype == 0 ? 4 : 8;
     const size_t chunks = dtype == 0 ? mse_chunks<float>(n) : mse_chunks<double>(n);
-    return round256(n * es) + round256(chunks * sizeof(double)) +
+    return round256(n * es) + 2 * round256(chunks * sizeof(double)) +
            round256(2 * chunks * sizeof(ChunkSummary));
 }
 
@@ -1159,7 +1269,8 @@ static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
     T *squares = (T *)base;
     const size_t chunks = mse_chunks<T>(n);
     double *chunk_sum = (double *)(base + round256(n * sizeof(T)));
-    ChunkSummary *summ = (ChunkSummary *)((char *)chunk_sum + round256(chunks * sizeof(double)));
+    double *chunk_pre = (double *)((char *)chunk_sum + round256(chunks * sizeof(double)));
+    ChunkSummary *summ = (ChunkSummary *)((char *)chunk_pre + round256(chunks * sizeof(double)));
     const bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
@@ -1167,8 +1278,9 @@ static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t,
     else
         hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault, gate);
     hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)chunks), dim3(256), 0, s, (const T *)squares, n, (const unsigned long long *)fault, chunk_sum, gate);
-    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_sum, summ, gate);
-    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const ChunkSummary *)summ, gate);
+    hipLaunchKernelGGL(k_mse_chunk_prefix, dim3(1), dim3(kPrefixThreads), 0, s, (const double *)chunk_sum, (uint64_t)chunks, chunk_pre, gate);
+    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_pre, summ, gate);
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const double *)chunk_sum, (const ChunkSummary *)summ, gate);
     return hipGetLastError();
 }
 

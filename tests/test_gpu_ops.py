@@ -322,6 +322,38 @@ def test_mse_ordered_sum_estimate_misses(ctx, pcu_pkg):
     assert ref * np.float32(n) == np.float32(5792.0 ** 2)  # the total never moved
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_mse_ordered_sum_uneven_chunks(ctx, pcu_pkg, dtype):
+    """Chunks whose squares are far from their mean: the walk folds a chunk exactly in
+    windows sized from the chunk's mean square, so windows that are too short (no crossing:
+    fold and widen) and too long (several crossings) both occur. Also zero prefixes, a
+    steady exponential climb with a crossing every few thousand squares, sparse spikes, and
+    binade crossings in the last chunk of a 512-chunk batch and past it. Bit-exact against
+    the oracle's dependent chain."""
+    rng = np.random.default_rng(99)
+    L = 8192 if dtype == np.float32 else 4096   # elements per chunk of the ordered sum
+    n = 6 * L + 77
+    half = np.where((np.arange(n) % L) < L // 2, dtype(1e-3), dtype(1.0))
+    zeros_then = np.concatenate([np.zeros(L + L // 2, dtype), rng.uniform(-1, 1, n - L - L // 2).astype(dtype)])
+    climb = np.exp2(np.arange(n) / 4000.0).astype(dtype)
+    spikes = np.full(n, 1e-4, dtype)
+    spikes[::997] = dtype(300.0)
+    tail_heavy = rng.uniform(-1e-3, 1e-3, n).astype(dtype)
+    tail_heavy[n - L // 3:] = rng.uniform(100, 200, L // 3).astype(dtype)
+    cases = [half, zeros_then, climb, spikes, tail_heavy]
+    # Every total a whole count: the k-th binade starts at square 2^k, in chunks 2^(k-13)-1
+    # (binary32) or 2^(k-12)-1 (binary64), among them the last of the first 512-chunk batch.
+    ones_n = 1024 * L + 5
+    cases.append(np.ones(ones_n, dtype))
+    for i, p in enumerate(cases):
+        t = np.zeros(p.size, dtype)
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_mse(ctx.upload(p), ctx.upload(t)).numpy())
+        ref, rf = oracle.mse(p, t)
+        assert gf == _ofault(rf), (i, gf, rf)
+        if rf is None:
+            assert _bits(got).item() == _bits(ref).item(), (i, got, ref)
+
+
 # ------------------------------------------------------------------- MatMul
 
 
