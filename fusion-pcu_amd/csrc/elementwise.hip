@@ -404,45 +404,53 @@ __global__ __launch_bounds__(kEwThreads) void k_mse_squares(const T *__restrict_
 template <typename T> struct SumBits;
 template <> struct SumBits<float> {
     using U = uint32_t;
+    using C = uint32_t;                  // step counts: a binade holds 2^24 quanta at most
     static constexpr int kFrac = 23;     // stored fraction bits
     static constexpr int kQmin = -149;   // exponent of the smallest subnormal
     static constexpr uint32_t kExpAll = 0xff;
-    static constexpr int kPer = 16;      // elements per thread of the ordered sum
+    static constexpr int kPer = 16;      // elements per thread of a full-chunk scan
+    static constexpr C kBig = 1u << 25;  // r of a step that surely leaves the binade
+    static constexpr C kCap = 1u << 30;  // saturation of prefix counts (past any crossing)
 };
 template <> struct SumBits<double> {
     using U = uint64_t;
+    using C = uint64_t;
     static constexpr int kFrac = 52;
     static constexpr int kQmin = -1074;
     static constexpr uint32_t kExpAll = 0x7ff;
     static constexpr int kPer = 8;
+    static constexpr C kBig = 1ull << 54;
+    static constexpr C kCap = 1ull << 62;
 };
 
 constexpr int kSumThreads = 512;
-constexpr uint64_t kSumCap = 1ull << 62;   // saturation of prefix sums (past any crossing)
-constexpr uint64_t kSumBig = 1ull << 54;   // r of a step that surely leaves the binade
 
 enum : uint32_t { kRBelow = 0, kRAbove = 1, kRTie = 2, kRForce = 3 };
 
-__device__ __forceinline__ uint64_t sat_add(uint64_t a, uint64_t b)
+template <typename T>
+__device__ __forceinline__ typename SumBits<T>::C sat_add(typename SumBits<T>::C a,
+                                                          typename SumBits<T>::C b)
 {
-    uint64_t c = a + b; // a, b <= 2^62: no wrap
-    return c < kSumCap ? c : kSumCap;
+    const typename SumBits<T>::C c = a + b; // a, b <= kCap: no wrap
+    return c < SumBits<T>::kCap ? c : SumBits<T>::kCap;
 }
 
 // Step r of one square s (bits) on the quantum 2^ue, before the tie decision.
 template <typename T>
-__device__ __forceinline__ void sum_elem(typename SumBits<T>::U b, int ue, uint64_t &n,
-                                         uint32_t &cls)
+__device__ __forceinline__ void sum_elem(typename SumBits<T>::U b, int ue,
+                                         typename SumBits<T>::C &n, uint32_t &cls)
 {
     using B = SumBits<T>;
+    using U = typename B::U;
+    using C = typename B::C;
     const uint32_t e = (uint32_t)(b >> B::kFrac) & B::kExpAll;
-    const uint64_t f = (uint64_t)b & ((1ull << B::kFrac) - 1);
-    if ((b >> (sizeof(T) * 8 - 1)) || e == B::kExpAll) { // negative or non-finite
-        n = kSumBig;
+    const C f = (C)(b & (((U)1 << B::kFrac) - 1));
+    if ((b >> (sizeof(U) * 8 - 1)) || e == B::kExpAll) { // negative or non-finite
+        n = B::kBig;
         cls = kRForce;
         return;
     }
-    const uint64_t sig = e ? (f | (1ull << B::kFrac)) : f;
+    const C sig = e ? (f | ((C)1 << B::kFrac)) : f;
     const int q = e ? (int)e + B::kQmin - 1 : B::kQmin;
     cls = kRBelow;
     if (sig == 0) {
@@ -451,86 +459,144 @@ __device__ __forceinline__ void sum_elem(typename SumBits<T>::U b, int ue, uint6
     }
     const int sh = q - ue;
     if (sh >= 0) {
-        n = sh >= 11 ? kSumBig : (sig << sh);
-        n = n < kSumBig ? n : kSumBig;
+        // sh > 0 only for normal squares (sig >= 2^kFrac): from sh = 2 on, r >= kBig.
+        n = sh >= 2 ? B::kBig : (sig << sh);
         return;
     }
     const int k = -sh;
-    if (k > 63) {
+    if (k > B::kFrac + 1) { // sig < 2^(kFrac+1) <= half a quantum: rounds to 0
         n = 0;
         return;
     }
     n = sig >> k;
-    const uint64_t rem = sig & ((1ull << k) - 1), half = 1ull << (k - 1);
+    const C rem = sig & (((C)1 << k) - 1), half = (C)1 << (k - 1);
     cls = rem < half ? kRBelow : (rem > half ? kRAbove : kRTie);
 }
 
-__device__ __forceinline__ uint64_t sum_step(uint64_t n, uint32_t cls, uint32_t parity)
+template <typename C>
+__device__ __forceinline__ C sum_step(C n, uint32_t cls, uint32_t parity)
 {
-    return n + (cls == kRAbove) + (cls == kRTie && ((parity ^ (uint32_t)n) & 1u));
+    return n + (C)(cls == kRAbove) + (C)(cls == kRTie && ((parity ^ (uint32_t)n) & 1u));
 }
 
 // Effect of a run of steps as a function of the parity of m before it: the added count
 // and the parity after it, for each starting parity (bit 0: start even, bit 1: start odd).
-struct SumScan {
-    uint64_t r0, r1;
+template <typename C> struct SumScanT {
+    C r0, r1;
     uint32_t p;
 };
+template <typename T> using SumScan = SumScanT<typename SumBits<T>::C>;
 
-__device__ __forceinline__ SumScan scan_identity() { return SumScan{0, 0, 2u}; }
+template <typename T> __device__ __forceinline__ SumScan<T> scan_identity() { return SumScan<T>{0, 0, 2u}; }
 
-__device__ __forceinline__ SumScan scan_compose(SumScan a, SumScan b)
+template <typename T>
+__device__ __forceinline__ SumScan<T> scan_compose(const SumScan<T> &a, const SumScan<T> &b)
 {
     const uint32_t a0 = a.p & 1u, a1 = (a.p >> 1) & 1u;
     const uint32_t b0 = b.p & 1u, b1 = (b.p >> 1) & 1u;
-    SumScan c;
-    c.r0 = sat_add(a.r0, a0 ? b.r1 : b.r0);
-    c.r1 = sat_add(a.r1, a1 ? b.r1 : b.r0);
+    SumScan<T> c;
+    c.r0 = sat_add<T>(a.r0, a0 ? b.r1 : b.r0);
+    c.r1 = sat_add<T>(a.r1, a1 ? b.r1 : b.r0);
     c.p = (a0 ? b1 : b0) | ((a1 ? b1 : b0) << 1);
     return c;
 }
 
-__device__ __forceinline__ SumScan scan_elem(uint64_t n, uint32_t cls)
+template <typename T>
+__device__ __forceinline__ SumScan<T> scan_elem(typename SumBits<T>::C n, uint32_t cls)
 {
-    const uint64_t r0 = sum_step(n, cls, 0), r1 = sum_step(n, cls, 1);
-    return SumScan{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
+    using C = typename SumBits<T>::C;
+    const C r0 = sum_step<C>(n, cls, 0), r1 = sum_step<C>(n, cls, 1);
+    return SumScan<T>{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
 }
 
-__device__ __forceinline__ SumScan scan_shfl_up(SumScan v, int d)
+// Cross-lane moves of a summary. DPP (a register read across lanes, no LDS): a lane
+// whose source lies outside the pattern, or whose row the row mask leaves out, keeps old.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_c(uint32_t old, uint32_t v)
 {
-    SumScan o;
-    o.r0 = __shfl_up(v.r0, d, 64);
-    o.r1 = __shfl_up(v.r1, d, 64);
-    o.p = __shfl_up(v.p, d, 64);
-    return o;
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_c(uint64_t old, uint64_t v)
+{
+    const uint32_t lo = dpp_c<CTRL, ROW_MASK>((uint32_t)old, (uint32_t)v);
+    const uint32_t hi = dpp_c<CTRL, ROW_MASK>((uint32_t)(old >> 32), (uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <typename T, int CTRL, int ROW_MASK>
+__device__ __forceinline__ SumScan<T> scan_dpp(const SumScan<T> &v)
+{
+    const SumScan<T> id = scan_identity<T>();
+    return SumScan<T>{dpp_c<CTRL, ROW_MASK>(id.r0, v.r0), dpp_c<CTRL, ROW_MASK>(id.r1, v.r1),
+                      dpp_c<CTRL, ROW_MASK>(id.p, v.p)};
+}
+
+__device__ __forceinline__ uint32_t readlane_c(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+__device__ __forceinline__ uint64_t readlane_c(uint64_t v, int l)
+{
+    return ((uint64_t)readlane_c((uint32_t)(v >> 32), l) << 32) | readlane_c((uint32_t)v, l);
+}
+
+template <typename T>
+__device__ __forceinline__ SumScan<T> scan_readlane(const SumScan<T> &v, int l)
+{
+    return SumScan<T>{readlane_c(v.r0, l), readlane_c(v.r1, l), readlane_c(v.p, l)};
+}
+
+template <typename T>
+__device__ __forceinline__ SumScan<T> scan_shfl_up(const SumScan<T> &v, int d)
+{
+    return SumScan<T>{__shfl_up(v.r0, d, 64), __shfl_up(v.r1, d, 64), __shfl_up(v.p, d, 64)};
+}
+
+// DPP patterns of the wave scan: row_shr:1,2,4,8 inside each row of 16 lanes, then
+// row_bcast:15 (lane 15 of rows 0 and 2 into rows 1 and 3) and row_bcast:31 (lane 31 into
+// rows 2 and 3).
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+// Inclusive ordered composition over the 64 lanes of a wave.
+template <typename T>
+__device__ __forceinline__ SumScan<T> wave_scan_incl(SumScan<T> v)
+{
+    v = scan_compose<T>(scan_dpp<T, kDppRowShr1, 0xf>(v), v);
+    v = scan_compose<T>(scan_dpp<T, kDppRowShr2, 0xf>(v), v);
+    v = scan_compose<T>(scan_dpp<T, kDppRowShr4, 0xf>(v), v);
+    v = scan_compose<T>(scan_dpp<T, kDppRowShr8, 0xf>(v), v);
+    v = scan_compose<T>(scan_dpp<T, kDppRowBcast15, 0xa>(v), v);
+    v = scan_compose<T>(scan_dpp<T, kDppRowBcast31, 0xc>(v), v);
+    return v;
 }
 
 // Phase of a total given by its bits: quantum exponent, count m and the count at which
 // the next binade starts.
 template <typename T>
-__device__ __forceinline__ void sum_phase(typename SumBits<T>::U bits, int &ue, uint64_t &m,
-                                          uint64_t &mmax)
+__device__ __forceinline__ void sum_phase(typename SumBits<T>::U bits, int &ue,
+                                          typename SumBits<T>::C &m, typename SumBits<T>::C &mmax)
 {
     using B = SumBits<T>;
+    using C = typename B::C;
     const uint32_t e = (uint32_t)(bits >> B::kFrac) & B::kExpAll;
     if (e == 0) {
         ue = B::kQmin;
-        m = (uint64_t)bits;
-        mmax = 1ull << B::kFrac;
+        m = (C)bits;
+        mmax = (C)1 << B::kFrac;
     } else {
         ue = (int)e + B::kQmin - 1;
-        m = ((uint64_t)bits & ((1ull << B::kFrac) - 1)) | (1ull << B::kFrac);
-        mmax = 1ull << (B::kFrac + 1);
+        m = ((C)bits & (((C)1 << B::kFrac) - 1)) | ((C)1 << B::kFrac);
+        mmax = (C)1 << (B::kFrac + 1);
     }
 }
 
 template <typename T>
-__device__ __forceinline__ typename SumBits<T>::U sum_bits(int ue, uint64_t m)
+__device__ __forceinline__ typename SumBits<T>::U sum_bits(int ue, typename SumBits<T>::C m)
 {
     using B = SumBits<T>;
-    if (ue == B::kQmin && m < (1ull << B::kFrac))
-        return (typename SumBits<T>::U)m;
-    return (typename SumBits<T>::U)(((uint64_t)(ue - B::kQmin) << B::kFrac) + m);
+    using U = typename B::U;
+    if (ue == B::kQmin && m < ((typename B::C)1 << B::kFrac))
+        return (U)m;
+    return (U)(((U)(ue - B::kQmin) << B::kFrac) + (U)m);
 }
 
 template <typename T>
@@ -551,9 +617,11 @@ __device__ __forceinline__ double from_bits<double>(uint64_t b) { return __longl
 //  D  k_mse_ordered_walk     one workgroup walks the chunks in order, 512 at a time: a scan
 //                            of the summaries made for the running binade folds every chunk
 //                            before the first one that has no such summary or reaches the
-//                            binade's end. That chunk runs exactly, in windows sized from its
-//                            estimate: each window is a parallel scan whose first step to
-//                            reach the binade's end runs as a real, checked Add.
+//                            binade's end. That chunk runs exactly: where crossings are
+//                            dense, one wave scans 64 squares at a time; elsewhere the
+//                            workgroup scans windows sized from the chunk's estimate. In
+//                            both, the first step to reach the binade's end runs as a real,
+//                            checked Add.
 // The estimate only decides how fast the walk goes, never its value.
 
 struct ChunkSummary {
@@ -615,42 +683,30 @@ __device__ __forceinline__ void load_chunk(const typename SumBits<T>::U *__restr
 
 // Ordered composition over the workgroup: every thread gets the summary of all threads
 // before it (excl) and of the whole workgroup (total).
-__device__ __forceinline__ void block_scan(SumScan mine, int lane, int wave, SumScan *wave_tot,
-                                           SumScan &excl, SumScan &total)
+template <typename T>
+__device__ __forceinline__ void block_scan(const SumScan<T> &mine, int lane, int wave,
+                                           SumScan<T> *wave_tot, SumScan<T> &excl,
+                                           SumScan<T> &total)
 {
     constexpr int kWaves = kSumThreads / 64;
-    SumScan inc = mine;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const SumScan o = scan_shfl_up(inc, d);
-        if (lane >= d)
-            inc = scan_compose(o, inc);
-    }
-    SumScan lane_excl = scan_shfl_up(inc, 1);
+    static_assert(kWaves <= 8, "the wave totals are scanned inside one DPP row");
+    const SumScan<T> inc = wave_scan_incl<T>(mine);
+    SumScan<T> lane_excl = scan_shfl_up<T>(inc, 1);
     if (lane == 0)
-        lane_excl = scan_identity();
+        lane_excl = scan_identity<T>();
     if (lane == 63)
         wave_tot[wave] = inc;
     __syncthreads();
-    // Every wave scans the per-wave totals on its first lanes (one LDS read each).
-    SumScan wt = lane < kWaves ? wave_tot[lane] : scan_identity();
-#pragma unroll
-    for (int d = 1; d < kWaves; d <<= 1) {
-        const SumScan o = scan_shfl_up(wt, d);
-        if (lane >= d)
-            wt = scan_compose(o, wt);
-    }
-    total.r0 = __shfl(wt.r0, kWaves - 1, 64);
-    total.r1 = __shfl(wt.r1, kWaves - 1, 64);
-    total.p = __shfl(wt.p, kWaves - 1, 64);
-    const int pw = wave > 0 ? wave - 1 : 0;
-    SumScan before;
-    before.r0 = __shfl(wt.r0, pw, 64);
-    before.r1 = __shfl(wt.r1, pw, 64);
-    before.p = __shfl(wt.p, pw, 64);
+    // Every wave scans the per-wave totals on the first lanes of its first row.
+    SumScan<T> wt = lane < kWaves ? wave_tot[lane] : scan_identity<T>();
+    wt = scan_compose<T>(scan_dpp<T, kDppRowShr1, 0xf>(wt), wt);
+    wt = scan_compose<T>(scan_dpp<T, kDppRowShr2, 0xf>(wt), wt);
+    wt = scan_compose<T>(scan_dpp<T, kDppRowShr4, 0xf>(wt), wt);
+    total = scan_readlane<T>(wt, kWaves - 1);
+    SumScan<T> before = scan_readlane<T>(wt, wave > 0 ? wave - 1 : 0);
     if (wave == 0)
-        before = scan_identity();
-    excl = scan_compose(before, lane_excl);
+        before = scan_identity<T>();
+    excl = scan_compose<T>(before, lane_excl);
 }
 
 // A chunk staged in LDS for its exact run: element i sits at slot i + i / kPadEvery (one
@@ -668,36 +724,37 @@ template <typename T> struct ChunkLds {
 // is written during an iteration while the other is cleared for the next.
 template <typename T> struct WalkShared {
     typename SumBits<T>::U vals[ChunkLds<T>::kSlots];
-    SumScan wave_tot[kSumThreads / 64];
+    SumScan<T> wave_tot[kSumThreads / 64];
     uint64_t m_first[2];             // count standing before the stopping chunk
     uint32_t first[2];               // stopping chunk of a batch (offset), kNoStep: none
-    uint32_t at[2];                  // crossing element of a window (offset), kNoStep: none
-    typename SumBits<T>::U total;    // total after the crossing Add
-    int stop;                        // the crossing Add faulted
+    uint32_t at[2];                  // crossing element of a window, or the element after a
+                                     // wave walk (offset); kNoStep: no crossing
+    typename SumBits<T>::U total[2]; // total after the crossing Add or the wave walk
+    int stop[2];                     // an Add faulted
     uint64_t limit;
 };
 
 // Summary of elements [i0, min(i0 + PER, i1)) of the staged chunk on the quantum 2^ue.
 template <typename T, int PER>
-__device__ __forceinline__ SumScan run_scan(const typename SumBits<T>::U *vals, uint32_t i0,
-                                            uint32_t i1, int ue)
+__device__ __forceinline__ SumScan<T> run_scan(const typename SumBits<T>::U *vals, uint32_t i0,
+                                               uint32_t i1, int ue)
 {
-    SumScan s = scan_identity();
+    SumScan<T> s = scan_identity<T>();
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         if (i0 + j < i1) {
-            uint64_t nn;
+            typename SumBits<T>::C nn;
             uint32_t cls;
             sum_elem<T>(vals[ChunkLds<T>::slot(i0 + j)], ue, nn, cls);
-            s = scan_compose(s, scan_elem(nn, cls));
+            s = scan_compose<T>(s, scan_elem<T>(nn, cls));
         }
     }
     return s;
 }
 
 template <typename T>
-__device__ __forceinline__ SumScan run_scan_per(const typename SumBits<T>::U *vals, uint32_t per,
-                                                uint32_t i0, uint32_t i1, int ue)
+__device__ __forceinline__ SumScan<T> run_scan_per(const typename SumBits<T>::U *vals,
+                                                   uint32_t per, uint32_t i0, uint32_t i1, int ue)
 {
     constexpr int P = SumBits<T>::kPer;
     if (per == 1)
@@ -711,31 +768,111 @@ __device__ __forceinline__ SumScan run_scan_per(const typename SumBits<T>::U *va
     return run_scan<T, P>(vals, i0, i1, ue);
 }
 
+// Expected number of squares (at the chunk's mean square) until the running total leaves
+// its binade: room quanta of 2^ue left.
+__device__ __forceinline__ double expected_gap(double room, int ue, double mean)
+{
+    return mean > 0.0 ? ldexp(room, ue) / mean : INFINITY;
+}
+
 // Elements per thread of the next window: a power of two covering about twice the expected
-// distance to the binade's end (room quanta of 2^ue at the chunk's mean square), from one
-// element per thread up to the whole chunk.
+// gap, from one element per thread up to the whole chunk.
 template <typename T>
-__device__ __forceinline__ uint32_t window_per(uint64_t room, int ue, double mean)
+__device__ __forceinline__ uint32_t window_per(double gap)
 {
     constexpr uint32_t P = SumBits<T>::kPer;
-    const double span = mean > 0.0 ? 2.0 * ldexp((double)room, ue) / (mean * kSumThreads) : (double)P;
+    const double span = 2.0 * gap / kSumThreads;
     uint32_t per = 1;
     while (per < P && (double)per < span)
         per <<= 1;
     return per;
 }
 
-// Exact fold of the chunk at base (len elements) from the phase (ue, m, mmax), window by
-// window: the one thread whose run holds the window's first step to reach the binade's end
-// executes that step as the contract's Add, and the next window starts after it in the new
-// binade. Returns false when an Add faulted (recorded).
+// Below this expected gap (in squares) one wave walks, 64 squares per scan: a crossing
+// then costs one wave scan instead of a workgroup scan of a window. A wave walk stops at
+// the first binade whose expected gap reaches kWaveGap, or after kWaveMax squares (then a
+// window runs next, whatever the estimate says).
+constexpr double kWaveGap = 1024.0;
+constexpr uint32_t kWaveMax = 4096;
+
+// The wave walk (wave 0 alone; every value it keeps is uniform over the wave): lane l
+// holds square off + l, a wave scan gives each lane the count before it, and the first
+// lane whose step reaches the binade's end executes that step as the contract's Add.
+// Returns false when that Add faulted (recorded).
+template <typename T>
+__device__ bool wave_walk(const typename SumBits<T>::U *vals, uint64_t base, uint32_t len,
+                          double mean, int policy, unsigned long long *fault,
+                          const NodeGate &gate, int lane, uint32_t &off, int &ue,
+                          typename SumBits<T>::C &m, typename SumBits<T>::C &mmax)
+{
+    using U = typename SumBits<T>::U;
+    using C = typename SumBits<T>::C;
+    const uint32_t end = off + kWaveMax < len ? off + kWaveMax : len;
+    while (off < end) {
+        const uint32_t i = off + (uint32_t)lane;
+        const bool in = i < end;
+        U b = 0;
+        C nn = 0;
+        uint32_t cls = kRBelow;
+        if (in) {
+            b = vals[ChunkLds<T>::slot(i)];
+            sum_elem<T>(b, ue, nn, cls);
+        }
+        const SumScan<T> inc = wave_scan_incl<T>(in ? scan_elem<T>(nn, cls) : scan_identity<T>());
+        SumScan<T> ex = scan_shfl_up<T>(inc, 1);
+        if (lane == 0)
+            ex = scan_identity<T>();
+        const uint32_t p0 = (uint32_t)(m & 1u);
+        const C mt = sat_add<T>(m, p0 ? ex.r1 : ex.r0);
+        const uint32_t pt = p0 ? (ex.p >> 1) & 1u : ex.p & 1u;
+        const C r = sum_step<C>(nn, cls, pt);
+        // Counts only grow along the lanes: at most one lane starts below the binade's end
+        // and reaches it.
+        const bool cross = in && mt < mmax && (cls == kRForce || mt + r >= mmax);
+        const uint64_t mask = __ballot(cross);
+        if (mask == 0) {
+            const SumScan<T> tot = scan_readlane<T>(inc, 63);
+            m = sat_add<T>(m, p0 ? tot.r1 : tot.r0);
+            off = off + 64 < end ? off + 64 : end;
+            continue;
+        }
+        const int c = __builtin_ctzll(mask);
+        U res_bits = 0;
+        uint32_t kind = kOk;
+        if (lane == c) {
+            const T acc = from_bits<T>(sum_bits<T>(ue, mt));
+            const T s_i = from_bits<T>(b);
+            const T res = acc + s_i;
+            kind = classify_add(acc, s_i, res, policy);
+            res_bits = (U)bits_of(res);
+            if (kind != kOk) {
+                atomicMin(fault, (unsigned long long)pack_fault(3 * (base + i) + 2, kind));
+                gate_record(gate);
+            }
+        }
+        if (readlane_c(kind, c) != kOk)
+            return false;
+        sum_phase<T>(readlane_c(res_bits, c), ue, m, mmax);
+        off += (uint32_t)c + 1;
+        if (expected_gap((double)(mmax - m), ue, mean) >= kWaveGap)
+            break;
+    }
+    return true;
+}
+
+// Exact fold of the chunk at base (len elements) from the phase (ue, m, mmax): by the wave
+// walk where crossings are dense, elsewhere window by window, where the one thread whose
+// run holds the window's first step to reach the binade's end executes that step as the
+// contract's Add and the next window starts after it in the new binade. Returns false when
+// an Add faulted (recorded).
 template <typename T>
 __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint64_t base,
                             uint32_t len, double mean, int policy, unsigned long long *fault,
-                            int &ue, uint64_t &m, uint64_t &mmax, WalkShared<T> &sh,
-                            const NodeGate &gate)
+                            int &ue, typename SumBits<T>::C &m, typename SumBits<T>::C &mmax,
+                            WalkShared<T> &sh, const NodeGate &gate)
 {
     using U = typename SumBits<T>::U;
+    using C = typename SumBits<T>::C;
     constexpr uint32_t P = SumBits<T>::kPer;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (uint32_t i = tid; i < len; i += kSumThreads)
@@ -743,29 +880,61 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint
     if (tid == 0)
         sh.at[0] = sh.at[1] = kNoStep;
     __syncthreads();
-    uint32_t off = 0, per = window_per<T>(mmax - m, ue, mean);
+    uint32_t off = 0, per = 0; // per = 0: no window has run yet
+    bool wave_ok = true;
     for (int it = 0; off < len; it++) {
         const int slot = it & 1;
+        const double gap = expected_gap((double)(mmax - m), ue, mean);
+        if (wave_ok && gap < kWaveGap) {
+            if (wave == 0) {
+                uint32_t o = off;
+                int u = ue;
+                C mm = m, mx = mmax;
+                const bool ok = wave_walk<T>(sh.vals, base, len, mean, policy, fault, gate, lane,
+                                             o, u, mm, mx);
+                if (lane == 0) {
+                    sh.stop[slot] = !ok;
+                    sh.total[slot] = sum_bits<T>(u, mm);
+                    sh.at[slot] = o;
+                }
+            }
+            __syncthreads();
+            const uint32_t next = sh.at[slot];
+            const int stop = sh.stop[slot];
+            const U tot = sh.total[slot];
+            if (tid == 0)
+                sh.at[slot ^ 1] = kNoStep;
+            if (stop)
+                return false;
+            sum_phase<T>(tot, ue, m, mmax);
+            wave_ok = next - off < kWaveMax;
+            off = next;
+            per = 0;
+            continue;
+        }
+        // After a window without a crossing the next one is at least twice as long.
+        const uint32_t want = window_per<T>(gap);
+        per = per && 2 * per > want ? (2 * per < P ? 2 * per : P) : want;
         const uint32_t wend = off + per * kSumThreads < len ? off + per * kSumThreads : len;
         const uint32_t i0 = off + (uint32_t)tid * per;
         const uint32_t i1 = i0 + per < wend ? i0 + per : wend;
-        const SumScan mine = run_scan_per<T>(sh.vals, per, i0, i1, ue);
-        SumScan before, total;
-        block_scan(mine, lane, wave, sh.wave_tot, before, total);
+        const SumScan<T> mine = run_scan_per<T>(sh.vals, per, i0, i1, ue);
+        SumScan<T> before, total;
+        block_scan<T>(mine, lane, wave, sh.wave_tot, before, total);
         const uint32_t p0 = (uint32_t)(m & 1u);
-        const uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+        const C mt = sat_add<T>(m, p0 ? before.r1 : before.r0);
         const uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
         // Counts only grow along the window, so exactly one run can start below the
         // binade's end and reach it.
-        if (mt < mmax && sat_add(mt, pt ? mine.r1 : mine.r0) >= mmax) {
-            uint64_t mm = mt;
+        if (mt < mmax && sat_add<T>(mt, pt ? mine.r1 : mine.r0) >= mmax) {
+            C mm = mt;
             uint32_t pp = pt;
             for (uint32_t i = i0; i < i1; i++) {
                 const U b = sh.vals[ChunkLds<T>::slot(i)];
-                uint64_t nn;
+                C nn;
                 uint32_t cls;
                 sum_elem<T>(b, ue, nn, cls);
-                const uint64_t r = sum_step(nn, cls, pp);
+                const C r = sum_step<C>(nn, cls, pp);
                 if (cls == kRForce || mm + r >= mmax) {
                     // The crossing step, executed and checked as the contract's Add.
                     const T acc = from_bits<T>(sum_bits<T>(ue, mm));
@@ -775,10 +944,10 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint
                     if (kind != kOk) {
                         atomicMin(fault, (unsigned long long)pack_fault(3 * (base + i) + 2, kind));
                         gate_record(gate);
-                        sh.stop = 1;
+                        sh.stop[slot] = 1;
                     } else {
-                        sh.stop = 0;
-                        sh.total = (U)bits_of(res);
+                        sh.stop[slot] = 0;
+                        sh.total[slot] = (U)bits_of(res);
                     }
                     sh.at[slot] = i;
                     break;
@@ -789,19 +958,21 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint
         }
         __syncthreads();
         const uint32_t at = sh.at[slot];
+        const int stop = sh.stop[slot];
+        const U tot = sh.total[slot];
         if (tid == 0)
             sh.at[slot ^ 1] = kNoStep;
         if (at == kNoStep) {
-            m = sat_add(m, p0 ? total.r1 : total.r0);
+            m = sat_add<T>(m, p0 ? total.r1 : total.r0);
             off = wend;
-            per = per * 2 < P ? per * 2 : P;
             continue;
         }
-        if (sh.stop)
+        if (stop)
             return false;
-        sum_phase<T>(sh.total, ue, m, mmax);
+        sum_phase<T>(tot, ue, m, mmax);
         off = at + 1;
-        per = window_per<T>(mmax - m, ue, mean);
+        per = 0;
+        wave_ok = true;
     }
     return true;
 }
@@ -878,7 +1049,7 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
         return;
     using U = typename SumBits<T>::U;
     constexpr int P = SumBits<T>::kPer;
-    __shared__ SumScan wave_tot[kSumThreads / 64];
+    __shared__ SumScan<T> wave_tot[kSumThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t c = blockIdx.x;
     const uint64_t limit = sum_limit(fault, n);
@@ -896,19 +1067,19 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     const uint64_t base = c * sum_chunk_len<T>();
     load_chunk<T>(src, ((uintptr_t)sq & 15u) == 0, base, limit, tid, cur);
     const uint64_t first = base + (uint64_t)tid * P;
-    SumScan mine = scan_identity();
+    SumScan<T> mine = scan_identity<T>();
 #pragma unroll
     for (int j = 0; j < P; j++) {
-        uint64_t nn;
+        typename SumBits<T>::C nn;
         uint32_t cls;
         sum_elem<T>(cur[j], ue, nn, cls);
         if (first + j < limit)
-            mine = scan_compose(mine, scan_elem(nn, cls));
+            mine = scan_compose<T>(mine, scan_elem<T>(nn, cls));
     }
-    SumScan excl, total;
-    block_scan(mine, lane, wave, wave_tot, excl, total);
+    SumScan<T> excl, total;
+    block_scan<T>(mine, lane, wave, wave_tot, excl, total);
     if (tid == 0)
-        *out = ChunkSummary{total.r0, total.r1, ue, 0};
+        *out = ChunkSummary{(uint64_t)total.r0, (uint64_t)total.r1, ue, 0};
 }
 
 // D: the ordered walk (one workgroup), then total (/) count.
@@ -921,6 +1092,8 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
     if (block_gate_closed(gate))
         return;
     using U = typename SumBits<T>::U;
+    using C = typename SumBits<T>::C;
+    constexpr C kBig = SumBits<T>::kBig;
     __shared__ WalkShared<T> sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) {
@@ -934,38 +1107,39 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
     const uint64_t chunks = (limit + L - 1) / L;
 
     int ue;
-    uint64_t m, mmax;
+    C m, mmax;
     sum_phase<T>((U)0, ue, m, mmax); // the total starts at +0
     uint64_t c0 = 0;
     for (int it = 0; c0 < chunks; it++) {
         const int slot = it & 1;
         const uint64_t c = c0 + tid;
-        SumScan mine = scan_identity();
+        SumScan<T> mine = scan_identity<T>();
         if (c < chunks) {
             const ChunkSummary a = summ[2 * c], b = summ[2 * c + 1];
             if (a.ue == ue || b.ue == ue) {
-                const uint64_t r0 = a.ue == ue ? a.r0 : b.r0, r1 = a.ue == ue ? a.r1 : b.r1;
-                mine = SumScan{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
+                // Summary counts saturate at kCap, past any crossing: they fit C.
+                const C r0 = (C)(a.ue == ue ? a.r0 : b.r0), r1 = (C)(a.ue == ue ? a.r1 : b.r1);
+                mine = SumScan<T>{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
             } else {
-                mine = SumScan{kSumBig, kSumBig, 2u}; // no summary for this binade: stop here
+                mine = SumScan<T>{kBig, kBig, 2u}; // no summary for this binade: stop here
             }
         }
-        SumScan before, total;
-        block_scan(mine, lane, wave, sh.wave_tot, before, total);
+        SumScan<T> before, total;
+        block_scan<T>(mine, lane, wave, sh.wave_tot, before, total);
         const uint32_t p0 = (uint32_t)(m & 1u);
-        const uint64_t mt = sat_add(m, p0 ? before.r1 : before.r0);
+        const C mt = sat_add<T>(m, p0 ? before.r1 : before.r0);
         const uint32_t pt = p0 ? (before.p >> 1) & 1u : before.p & 1u;
-        if (c < chunks && mt < mmax && sat_add(mt, pt ? mine.r1 : mine.r0) >= mmax) {
+        if (c < chunks && mt < mmax && sat_add<T>(mt, pt ? mine.r1 : mine.r0) >= mmax) {
             sh.first[slot] = (uint32_t)tid;
-            sh.m_first[slot] = mt;
+            sh.m_first[slot] = (uint64_t)mt;
         }
         __syncthreads();
         const uint32_t first = sh.first[slot];
-        const uint64_t m_first = sh.m_first[slot];
+        const C m_first = (C)sh.m_first[slot];
         if (tid == 0)
             sh.first[slot ^ 1] = kNoStep;
         if (first == kNoStep) {
-            m = sat_add(m, p0 ? total.r1 : total.r0);
+            m = sat_add<T>(m, p0 ? total.r1 : total.r0);
             c0 += kSumThreads;
             continue;
         }
@@ -1260,38 +1434,69 @@ size_t mse_scratch_bytes(int dtype, uint64_t n)
            round256(2 * chunks * sizeof(ChunkSummary));
 }
 
+template <typename T> struct MseScratch {
+    T *squares;
+    double *chunk_sum, *chunk_pre;
+    ChunkSummary *summ;
+    size_t chunks;
+    MseScratch(void *scratch, uint64_t n)
+    {
+        char *base = (char *)scratch;
+        chunks = mse_chunks<T>(n);
+        squares = (T *)base;
+        chunk_sum = (double *)(base + round256(n * sizeof(T)));
+        chunk_pre = (double *)((char *)chunk_sum + round256(chunks * sizeof(double)));
+        summ = (ChunkSummary *)((char *)chunk_pre + round256(chunks * sizeof(double)));
+    }
+};
+
 template <typename T>
-static hipError_t mse_t(hipStream_t s, uint64_t n, const void *p, const void *t, void *scratch,
-                        T count, void *out, int policy, unsigned long long *fault, NodeGate gate)
+static hipError_t mse_prepare_t(hipStream_t s, uint64_t n, const void *p, const void *t,
+                                void *scratch, int policy, unsigned long long *fault, NodeGate gate)
 {
     constexpr int Wd = Vec<T>::width;
-    char *base = (char *)scratch;
-    T *squares = (T *)base;
-    const size_t chunks = mse_chunks<T>(n);
-    double *chunk_sum = (double *)(base + round256(n * sizeof(T)));
-    double *chunk_pre = (double *)((char *)chunk_sum + round256(chunks * sizeof(double)));
-    ChunkSummary *summ = (ChunkSummary *)((char *)chunk_pre + round256(chunks * sizeof(double)));
-    const bool vec = aligned16(p) && aligned16(t) && aligned16(squares);
+    const MseScratch<T> m(scratch, n);
+    const bool vec = aligned16(p) && aligned16(t) && aligned16(m.squares);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
     if (vec)
-        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault, gate);
+        hipLaunchKernelGGL((k_mse_squares<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, m.squares, n, policy, fault, gate);
     else
-        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, squares, n, policy, fault, gate);
-    hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)chunks), dim3(256), 0, s, (const T *)squares, n, (const unsigned long long *)fault, chunk_sum, gate);
-    hipLaunchKernelGGL(k_mse_chunk_prefix, dim3(1), dim3(kPrefixThreads), 0, s, (const double *)chunk_sum, (uint64_t)chunks, chunk_pre, gate);
-    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)chunks, 2), dim3(kSumThreads), 0, s, (const T *)squares, n, (const unsigned long long *)fault, (const double *)chunk_pre, summ, gate);
-    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)squares, n, count, policy, (T *)out, fault, (const double *)chunk_sum, (const ChunkSummary *)summ, gate);
+        hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, m.squares, n, policy, fault, gate);
+    hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)m.chunks), dim3(256), 0, s, (const T *)m.squares, n, (const unsigned long long *)fault, m.chunk_sum, gate);
+    hipLaunchKernelGGL(k_mse_chunk_prefix, dim3(1), dim3(kPrefixThreads), 0, s, (const double *)m.chunk_sum, (uint64_t)m.chunks, m.chunk_pre, gate);
+    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)m.chunks, 2), dim3(kSumThreads), 0, s, (const T *)m.squares, n, (const unsigned long long *)fault, (const double *)m.chunk_pre, m.summ, gate);
     return hipGetLastError();
 }
 
-hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                      void *scratch, double count, void *out, int policy,
-                      unsigned long long *fault, NodeGate gate)
+template <typename T>
+static hipError_t mse_walk_t(hipStream_t s, uint64_t n, void *scratch, T count, void *out,
+                             int policy, unsigned long long *fault, NodeGate gate)
+{
+    const MseScratch<T> m(scratch, n);
+    // The walk asks for most of its CU's LDS although it uses about 36 KB: no workgroup of
+    // a MatMul running beside it then shares that CU's SIMDs (and waits on the serial walk);
+    // the MatMul spreads over the other CUs instead.
+    constexpr size_t kReserveLds = 96 * 1024;
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), kReserveLds, s, (const T *)m.squares, n, count, policy, (T *)out, fault, (const double *)m.chunk_sum, (const ChunkSummary *)m.summ, gate);
+    return hipGetLastError();
+}
+
+hipError_t launch_mse_prepare(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                              void *scratch, int policy, unsigned long long *fault, NodeGate gate)
 {
     if (n == 0)
         return hipErrorInvalidValue;
-    return dtype == 0 ? mse_t<float>(s, n, p, t, scratch, (float)count, out, policy, fault, gate)
-                      : mse_t<double>(s, n, p, t, scratch, count, out, policy, fault, gate);
+    return dtype == 0 ? mse_prepare_t<float>(s, n, p, t, scratch, policy, fault, gate)
+                      : mse_prepare_t<double>(s, n, p, t, scratch, policy, fault, gate);
+}
+
+hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, double count,
+                           void *out, int policy, unsigned long long *fault, NodeGate gate)
+{
+    if (n == 0)
+        return hipErrorInvalidValue;
+    return dtype == 0 ? mse_walk_t<float>(s, n, scratch, (float)count, out, policy, fault, gate)
+                      : mse_walk_t<double>(s, n, scratch, count, out, policy, fault, gate);
 }
 
 // ------------------------------------------------------------ native launchers

@@ -31,12 +31,15 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                            unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
                       double rate, void *out, int policy, unsigned long long *fault, NodeGate gate);
-// `scratch` holds mse_scratch_bytes(dtype, n) bytes; `count` is the element count
-// rounded to the dtype.
+// Strict MSE in two launches on one scratch of mse_scratch_bytes(dtype, n) bytes: the
+// parallel part (squares, chunk estimates and summaries), then the one-workgroup ordered
+// walk and the division, which may run on another stream once the first is done. `count`
+// is the element count rounded to the dtype.
 size_t mse_scratch_bytes(int dtype, uint64_t n);
-hipError_t launch_mse(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
-                      void *scratch, double count, void *out, int policy,
-                      unsigned long long *fault, NodeGate gate);
+hipError_t launch_mse_prepare(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                              void *scratch, int policy, unsigned long long *fault, NodeGate gate);
+hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, double count,
+                           void *out, int policy, unsigned long long *fault, NodeGate gate);
 
 // Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.
 struct MatmulScratch {

@@ -645,10 +645,18 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     pcu_status st = add_node(NodeInfo{Prim::Mse, n, 0}, &word);
     if (st)
         return st;
+    void *sq = nullptr;
+    if ((st = scratch(mse_scratch_bytes(dtype, n), stream, &sq)))
+        return st;
+    hipEvent_t t0 = timer_start(stream);
+    if ((st = hip(launch_mse_prepare(stream, dtype, n, p, t, sq, policy, word, gate_for(word)),
+                  "strict_mse launch")))
+        return st;
+    timer_stop(PCU_KERNEL_MSE, t0, stream);
     hipStream_t s = stream;
     if (on_side) {
-        // The serial sum overlaps the following ordered work; the side stream starts after
-        // everything enqueued so far (the prediction's producers).
+        // The one-workgroup ordered walk overlaps the following ordered work on the side
+        // stream, which starts once everything enqueued so far is done.
         if ((st = hip(hipEventRecord(main_ready, stream), "hipEventRecord")))
             return st;
         if ((st = hip(hipStreamWaitEvent(side, main_ready, 0), "hipStreamWaitEvent")))
@@ -656,14 +664,11 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
         s = side;
         side_pending = true;
     }
-    void *sq = nullptr;
-    if ((st = scratch(mse_scratch_bytes(dtype, n), s, &sq)))
-        return st;
-    hipEvent_t t0 = timer_start(s);
-    if ((st = hip(launch_mse(s, dtype, n, p, t, sq, count_as(dtype, n), out, policy, word, gate_for(word)),
+    hipEvent_t t1 = timer_start(s);
+    if ((st = hip(launch_mse_walk(s, dtype, n, sq, count_as(dtype, n), out, policy, word, gate_for(word)),
                   "strict_mse launch")))
         return st;
-    timer_stop(PCU_KERNEL_MSE, t0, s);
+    timer_stop(PCU_KERNEL_MSE, t1, s);
     return hip(hipFreeAsync(sq, s), "hipFreeAsync");
 }
 
