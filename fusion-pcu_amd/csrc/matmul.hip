@@ -30,25 +30,20 @@ namespace pcu {
 
 constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
 
+// Branch-free: the prefilter applies it to every element of both operands.
 __device__ __forceinline__ int ilog2_abs(float v)
 {
-    uint32_t b = bits_of(v);
-    uint32_t e = (b >> 23) & 0xff, f = b & 0x7fffff;
-    if (e == 0xff || (e == 0 && f == 0))
-        return kExpNone;
-    if (e == 0)
-        return (31 - __clz(f)) - 149;
-    return (int)e - 127;
+    const uint32_t b = bits_of(v) & 0x7fffffffu, e = b >> 23;
+    const int sub = (31 - __clz(b | 1u)) - 149; // e == 0: b is the fraction
+    const int r = e ? (int)e - 127 : sub;
+    return (e == 0xff || b == 0) ? kExpNone : r;
 }
 __device__ __forceinline__ int ilog2_abs(double v)
 {
-    uint64_t b = bits_of(v);
-    uint64_t e = (b >> 52) & 0x7ff, f = b & 0x000fffffffffffffull;
-    if (e == 0x7ff || (e == 0 && f == 0))
-        return kExpNone;
-    if (e == 0)
-        return (63 - __clzll(f)) - 1074;
-    return (int)e - 1023;
+    const uint64_t b = bits_of(v) & 0x7fffffffffffffffull, e = b >> 52;
+    const int sub = (63 - __clzll(b | 1ull)) - 1074;
+    const int r = e ? (int)e - 1023 : sub;
+    return (e == 0x7ff || b == 0) ? kExpNone : r;
 }
 
 __device__ __forceinline__ int wave_min_i32(int v)
@@ -88,7 +83,25 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
     const T *row = X + r * C;
     if (VEC) {
         constexpr int P = 16 / sizeof(T);
-        for (uint64_t c = (uint64_t)lane * P; c < C; c += 64 * P) {
+        constexpr uint64_t S = 64 * P; // elements one pass of the wave covers
+        constexpr int U = 4;           // 16-byte loads per lane in flight
+        uint64_t c = (uint64_t)lane * P;
+        for (; c + (U - 1) * S < C; c += U * S) {
+            uint4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                q[u] = *reinterpret_cast<const uint4 *>(row + c + u * S);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const T *v = reinterpret_cast<const T *>(&q[u]);
+#pragma unroll
+                for (int j = 0; j < P; j++) {
+                    const int e = ilog2_abs(v[j]);
+                    m = e < m ? e : m;
+                }
+            }
+        }
+        for (; c < C; c += S) {
             const uint4 q = *reinterpret_cast<const uint4 *>(row + c);
             const T *v = reinterpret_cast<const T *>(&q);
 #pragma unroll
@@ -110,7 +123,8 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
 
 // out[c] = min over r of ilog2|X[r, c]|. A block is 64 column-runs (16 bytes each) by 4 row
 // groups over 64 rows; the row groups meet in LDS and the block folds its minimum into out
-// with one atomicMin per column (out opened to kExpNone beforehand).
+// with one atomicMin per column (out opened to kExpNone beforehand). Fewer rows per block
+// measured slower: the atomics on one column then contend.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, uint64_t R,
                                                       uint64_t C, int *__restrict__ out, NodeGate gate)
@@ -128,7 +142,26 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
     for (int j = 0; j < P; j++)
         m[j] = kExpNone;
     if (c0 < C) {
-        for (uint64_t r = r0 + ry; r < r1; r += 4) {
+        uint64_t r = r0 + ry;
+        if (VEC) {
+            // Four rows per step: four 16-byte loads per thread in flight.
+            for (; r + 12 < r1; r += 16) {
+                uint4 q[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    q[u] = *reinterpret_cast<const uint4 *>(X + (r + 4 * u) * C + c0);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const T *v = reinterpret_cast<const T *>(&q[u]);
+#pragma unroll
+                    for (int j = 0; j < P; j++) {
+                        const int e = ilog2_abs(v[j]);
+                        m[j] = e < m[j] ? e : m[j];
+                    }
+                }
+            }
+        }
+        for (; r < r1; r += 4) {
             const T *p = X + r * C + c0;
             if (VEC) {
                 const uint4 q = *reinterpret_cast<const uint4 *>(p);
