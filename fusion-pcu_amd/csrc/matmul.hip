@@ -423,6 +423,25 @@ hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uin
     return hipGetLastError();
 }
 
+__global__ void k_program_open(unsigned long long *words, uint64_t n, unsigned long long value,
+                               unsigned int *gate)
+{
+    const uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint64_t i = i0; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        words[i] = value;
+    if (i0 == 0)
+        *gate = 0xffffffffu;
+}
+
+hipError_t launch_program_open(hipStream_t s, unsigned long long *words, uint64_t n, uint64_t value,
+                               unsigned int *gate)
+{
+    unsigned grid = (unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+    grid = grid ? grid : 1;
+    hipLaunchKernelGGL(k_program_open, dim3(grid), dim3(256), 0, s, words, n, (unsigned long long)value, gate);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t value)
 {
     if (n == 0)

@@ -89,5 +89,8 @@ hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p
 // them as kernels).
 hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value);
 hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t value);
+// Program start: words[0, n) = value and *gate = 0xffffffff (open), in one launch.
+hipError_t launch_program_open(hipStream_t s, unsigned long long *words, uint64_t n, uint64_t value,
+                               unsigned int *gate);
 
 } // namespace pcu

@@ -43,6 +43,7 @@ struct Ctx {
     unsigned long long *host_words = nullptr;  // pinned mirror
     bool in_program = false;
     bool implicit_program = false;
+    bool words_pending = false; // the open program's fault words and gate await their reset
     std::vector<NodeInfo> nodes;
     std::string error;
 
@@ -78,6 +79,7 @@ struct Ctx {
     pcu_status join_side();
     pcu_status scratch(size_t bytes, hipStream_t s, void **out);
 
+    pcu_status open_words();
     pcu_status begin_program(bool implicit);
     pcu_status end_program(pcu_fault *first);
     // Every faulted node in node order (empty when none).

@@ -249,11 +249,20 @@ pcu_status Ctx::begin_program(bool implicit)
     in_program = true;
     implicit_program = implicit;
     nodes.clear();
-    // Only the words a program uses are read back; fill them all once, and open the stage
-    // gate (kernels rather than memsets so the sequence stays capturable).
-    if ((st = hip(launch_fill_u64(stream, fault_words, kMaxNodes, kNoFaultWord), "fill fault words")))
-        return st;
-    return hip(launch_fill_u32(stream, gate_word(), 1, 0xffffffffu), "open stage gate");
+    words_pending = true;
+    return PCU_OK;
+}
+
+// The fault words and the stage gate are reset by one kernel (not memsets, so the sequence
+// stays capturable), launched right before the program's first kernel: the host work of
+// the first op (scratch, events) then runs before it rather than between it and the op.
+pcu_status Ctx::open_words()
+{
+    if (!words_pending)
+        return PCU_OK;
+    words_pending = false;
+    return hip(launch_program_open(stream, fault_words, kMaxNodes, kNoFaultWord, gate_word()),
+               "open fault words and stage gate");
 }
 
 pcu_status Ctx::add_node(NodeInfo info, unsigned long long **word)
@@ -342,6 +351,9 @@ pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
         return st;
     size_t used = nodes.size();
     if (used) {
+        // Nodes that launched nothing (empty shapes) still have their words read.
+        if ((st = open_words()))
+            return st;
         if ((st = hip(hipMemcpyAsync(host_words, fault_words, used * sizeof(unsigned long long),
                                      hipMemcpyDeviceToHost, stream), "hipMemcpyAsync")))
             return st;
@@ -494,6 +506,8 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     if (profiling)
         for (auto &x : ev)
             x = take_event();
+    if ((st = open_words()))
+        return st;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
                                         profiling ? ev : nullptr, matmul_engine);
@@ -519,6 +533,8 @@ pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const vo
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
         return st;
+    if ((st = open_words()))
+        return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_binary(stream, dtype, op, n, a, b, b_value, out, policy, word, gate_for(word)), "checked_binary launch");
     timer_stop(PCU_KERNEL_BINARY, t, stream);
@@ -534,6 +550,8 @@ pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int pol
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_relu(stream, dtype, n, x, out, policy, word, gate_for(word)), "checked_relu launch");
@@ -551,6 +569,8 @@ pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const voi
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_relu_backward(stream, dtype, n, x, up, out, policy, word, gate_for(word)),
@@ -571,6 +591,8 @@ pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
     if (st)
         return st;
     if ((st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &w_relu)))
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_add_relu(stream, dtype, n, a, b, b_value, out, policy, w_add, w_relu, gate_for(w_add)),
@@ -597,6 +619,8 @@ pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, floa
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Sgd, n, 0}, &word);
     if (st)
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word, gate_for(word)), "strict_sgd launch");
@@ -648,6 +672,8 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     void *sq = nullptr;
     if ((st = scratch(mse_scratch_bytes(dtype, n), stream, &sq)))
         return st;
+    if ((st = open_words()))
+        return st;
     hipEvent_t t0 = timer_start(stream);
     if ((st = hip(launch_mse_prepare(stream, dtype, n, p, t, sq, policy, word, gate_for(word)),
                   "strict_mse launch")))
@@ -689,6 +715,8 @@ pcu_status Ctx::op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint6
         return st;
     if (rows == 0 || cols == 0)
         return PCU_OK;
+    if ((st = open_words()))
+        return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_native_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a, b, c, gate_for(word)),
              "native_matmul launch");
@@ -713,6 +741,8 @@ pcu_status Ctx::op_native_sgd(int dtype, uint64_t n, const void *w, const void *
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Native, n, 0}, &word);
     if (st)
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t = timer_start(stream);
     st = hip(launch_native_sgd(stream, dtype, n, w, g, (double)rate, contracted, out, gate_for(word)), "native_sgd launch");
@@ -746,6 +776,8 @@ pcu_status Ctx::op_native_mse(int dtype, uint64_t n, const void *p, const void *
     }
     void *sc = nullptr;
     if ((st = scratch(native_mse_scratch_bytes(dtype, n), stream, &sc)))
+        return st;
+    if ((st = open_words()))
         return st;
     hipEvent_t t0 = timer_start(stream);
     st = hip(launch_native_mse(stream, dtype, n, p, t, sc, scale, out, gate_for(word)), "native_mse launch");
