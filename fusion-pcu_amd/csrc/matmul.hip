@@ -243,6 +243,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
+    // The lane's 8 columns come in RUN adjacent columns per run: binary32 lanes own 2 runs
+    // of 4 (64 columns apart), binary64 lanes 4 runs of 2 (32 apart), so that each 16-byte
+    // LDS read of B covers 256 contiguous bytes over the 16 lanes of a row (no bank
+    // conflicts) and each 16-byte store is coalesced the same way.
+    constexpr int RUN = 16 / sizeof(T), RUNS = 8 / RUN, RUN_STRIDE = BN / RUNS;
+    auto col_of = [&](int j) { return (j / RUN) * RUN_STRIDE + tx * RUN + (j % RUN); };
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tile_m, tile_n;
@@ -275,9 +281,10 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             for (int i = 0; i < 4; i++) {
                 a[i] = As[cur][k][ty * 4 + i];
                 a[4 + i] = As[cur][k][64 + ty * 4 + i];
-                b[i] = Bs[cur][k][tx * 4 + i];
-                b[4 + i] = Bs[cur][k][64 + tx * 4 + i];
             }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                b[j] = Bs[cur][k][col_of(j)];
 #pragma unroll
             for (int i = 0; i < 8; i++)
 #pragma unroll
@@ -304,29 +311,27 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             continue;
         int rexp = check_risk ? row_exp[r] : 0;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int c0 = n0 + h * 64 + tx * 4;
+        for (int h = 0; h < RUNS; h++) {
+            int c0 = n0 + col_of(h * RUN);
             T *dst = C + (size_t)r * N + c0;
-            if (vec_c && c0 + 4 <= N) {
-                if (sizeof(T) == 4) {
+            if (vec_c && c0 + RUN <= N) {
+                if (sizeof(T) == 4)
                     *reinterpret_cast<float4 *>(dst) =
                         make_float4(acc[i][h * 4], acc[i][h * 4 + 1], acc[i][h * 4 + 2], acc[i][h * 4 + 3]);
-                } else {
-                    reinterpret_cast<double2 *>(dst)[0] = make_double2(acc[i][h * 4], acc[i][h * 4 + 1]);
-                    reinterpret_cast<double2 *>(dst)[1] = make_double2(acc[i][h * 4 + 2], acc[i][h * 4 + 3]);
-                }
+                else
+                    *reinterpret_cast<double2 *>(dst) = make_double2(acc[i][h * 2], acc[i][h * 2 + 1]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < RUN; j++)
                     if (c0 + j < N)
-                        dst[j] = acc[i][h * 4 + j];
+                        dst[j] = acc[i][h * RUN + j];
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < RUN; j++) {
                 int c = c0 + j;
                 if (NATIVE || c >= N)
                     continue;
-                bool bad = !finite_bits(acc[i][h * 4 + j]);
+                bool bad = !finite_bits(acc[i][h * RUN + j]);
                 if (check_risk)
                     bad |= rexp + col_exp[c] < thr;
                 if (bad) {
