@@ -77,8 +77,17 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 #pragma unroll
     for (int r = 0; r < 32; r++)
         zero[r] = 0.0f;
+    // Raising the wave's priority around each MFMA issue measured about 0.8% faster at
+    // 4096^3 when op(A) and op(B) are staged alike (both transposed or neither) and about
+    // 0.4% slower otherwise, so it is used only there.
+    constexpr bool kIssuePrio = TA == TB;
     auto mma = [&](float a, float b) {
-        return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, zero, 0, 0, 0);
+        if (kIssuePrio)
+            __builtin_amdgcn_s_setprio(1);
+        const v32f r = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, zero, 0, 0, 0);
+        if (kIssuePrio)
+            __builtin_amdgcn_s_setprio(0);
+        return r;
     };
     // Fold one MFMA's products into a subtile: each cell adds its k product, then its
     // k+1 product (registers r and 16 + r of the same cell).
