@@ -228,7 +228,8 @@ template <typename T> struct ValuCfg {
 
 // NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per
 // (cell, k) and no fault screen.
-template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false>
+// WHOLE: every slab of every tile is whole (see the MFMA kernel).
+template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false, bool WHOLE = false>
 __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
@@ -265,15 +266,24 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     SlabStager<T, Cfg, TA, TB, VA, VB> stage;
 
     const int ktiles = (K + BK - 1) / BK;
+    if (WHOLE)
+        stage.begin_whole(A, B, M, N, K, m0, n0, tid);
     if (ktiles > 0) {
-        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        if (WHOLE)
+            stage.fetch_whole();
+        else
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
         stage.stash(As[0], Bs[0], tid);
     }
     __syncthreads();
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < ktiles)
-            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        if (kt + 1 < ktiles) {
+            if (WHOLE)
+                stage.fetch_whole();
+            else
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        }
 #pragma unroll(sizeof(T) == 4 ? BK : 2)
         for (int k = 0; k < BK; k++) {
             T a[8], b[8];
@@ -529,7 +539,10 @@ static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C
     bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     int vc = (N % 4 == 0) && aligned16(C);
-    if (va && vb)
+    using Cfg = ValuCfg<T>;
+    if (va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0)
+        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+    else if (va && vb)
         hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
     else if (va)
         hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
@@ -597,7 +610,10 @@ static void native_f64_dispatch(hipStream_t s, dim3 grid, const double *A, const
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     const int vc = (N % 4 == 0) && aligned16(C);
-    if (va && vb)
+    using Cfg = ValuCfg<double>;
+    if (va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0)
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+    else if (va && vb)
         hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
     else if (va)
         hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);

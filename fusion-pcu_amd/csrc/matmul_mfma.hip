@@ -44,7 +44,9 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
     static_assert(EA % 4 == 0 && EB % 4 == 0, "staging moves whole float4s");
 };
 
-template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+// WHOLE: every slab of every tile is whole (M, N, K multiples of the tile and slab, 16-byte
+// loads allowed), so staging runs on advancing pointers with no bound checks.
+template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr,
@@ -100,16 +102,25 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     };
 
     const int ktiles = (K + BK - 1) / BK;
+    if (WHOLE)
+        stage.begin_whole(A, B, M, N, K, m0, n0, tid);
     if (ktiles > 0) {
-        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        if (WHOLE)
+            stage.fetch_whole();
+        else
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
         stage.stash(As[0], Bs[0], tid);
     }
     __syncthreads();
     const int half = lane >> 5, col = lane & 31;
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < ktiles)
-            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        if (kt + 1 < ktiles) {
+            if (WHOLE)
+                stage.fetch_whole();
+            else
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        }
         // Software pipeline: one MFMA is in flight while the vector unit folds the previous
         // one (the group barriers ask the scheduler for that alternation). Lanes 0-31 carry
         // k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
@@ -203,7 +214,10 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    if (va && vb)
+    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0;
+    if (whole)
+        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    else if (va && vb)
         hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else if (va)
         hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
@@ -243,7 +257,7 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
 // Explicitly permitted native compound arithmetic (Boundary + BackendDefined): the matrix
 // cores accumulate, v_mfma_f32_32x32x2_f32 folding k and k+1 of a 32x32 subtile per
 // instruction in their own order and rounding. No fault is classified.
-template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, NodeGate gate)
@@ -272,16 +286,25 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_ge
 
     SlabStager<float, Cfg, TA, TB, VA, VB> stage;
     const int ktiles = (K + BK - 1) / BK;
+    if (WHOLE)
+        stage.begin_whole(A, B, M, N, K, m0, n0, tid);
     if (ktiles > 0) {
-        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        if (WHOLE)
+            stage.fetch_whole();
+        else
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
         stage.stash(As[0], Bs[0], tid);
     }
     __syncthreads();
     const int half = lane >> 5, col = lane & 31;
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < ktiles)
-            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        if (kt + 1 < ktiles) {
+            if (WHOLE)
+                stage.fetch_whole();
+            else
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             float a[SM], b[SN];
@@ -321,7 +344,10 @@ static void native_dispatch(hipStream_t s, const float *A, const float *B, float
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    if (va && vb)
+    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0;
+    if (whole)
+        hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, gate);
+    else if (va && vb)
         hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, gate);
     else if (va)
         hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, gate);

@@ -74,6 +74,35 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
     static_assert(EA % (16 / sizeof(T)) == 0 && EB % (16 / sizeof(T)) == 0,
                   "staging moves whole 16-byte runs");
     T ra[EA], rb[EB];
+    // Whole slabs (the tile inside M and N, K a multiple of BK, 16-byte loads allowed): the
+    // thread's run pointers advance one slab per fetch, with no bound checks.
+    const T *pa = nullptr, *pb = nullptr;
+    size_t sa = 0, sb = 0;
+    __device__ __forceinline__ void begin_whole(const T *__restrict__ A, const T *__restrict__ B,
+                                                int M, int N, int K, int m0, int n0, int tid)
+    {
+        if (!TA) {
+            pa = A + (size_t)(m0 + tid / (BK / EA)) * K + (tid % (BK / EA)) * EA;
+            sa = BK;
+        } else {
+            pa = A + (size_t)(tid / (BM / EA)) * M + m0 + (tid % (BM / EA)) * EA;
+            sa = (size_t)BK * M;
+        }
+        if (!TB) {
+            pb = B + (size_t)(tid / (BN / EB)) * N + n0 + (tid % (BN / EB)) * EB;
+            sb = (size_t)BK * N;
+        } else {
+            pb = B + (size_t)(n0 + tid / (BK / EB)) * K + (tid % (BK / EB)) * EB;
+            sb = BK;
+        }
+    }
+    __device__ __forceinline__ void fetch_whole()
+    {
+        load_run<T, EA, true>(pa, EA, ra);
+        load_run<T, EB, true>(pb, EB, rb);
+        pa += sa;
+        pb += sb;
+    }
 
     __device__ __forceinline__ void fetch(const T *__restrict__ A, const T *__restrict__ B, int M,
                                           int N, int K, int m0, int n0, int k0, int tid)
