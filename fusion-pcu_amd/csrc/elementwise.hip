@@ -1473,11 +1473,7 @@ static hipError_t mse_walk_t(hipStream_t s, uint64_t n, void *scratch, T count, 
                              int policy, unsigned long long *fault, NodeGate gate)
 {
     const MseScratch<T> m(scratch, n);
-    // The walk asks for most of its CU's LDS although it uses about 36 KB: no workgroup of
-    // a MatMul running beside it then shares that CU's SIMDs (and waits on the serial walk);
-    // the MatMul spreads over the other CUs instead.
-    constexpr size_t kReserveLds = 96 * 1024;
-    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), kReserveLds, s, (const T *)m.squares, n, count, policy, (T *)out, fault, (const double *)m.chunk_sum, (const ChunkSummary *)m.summ, gate);
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)m.squares, n, count, policy, (T *)out, fault, (const double *)m.chunk_sum, (const ChunkSummary *)m.summ, gate);
     return hipGetLastError();
 }
 
