@@ -214,6 +214,35 @@ def cpu_baseline(m, k, n, rows):
     }
 
 
+def cpu_fast_oracle(m, k, n, seconds=5.0):
+    """The same MatMul on the oracle's fast path (host IEEE arithmetic with a conservative
+    screen re-run through the integer law, OpenMP on all the host cores we may use), on a
+    leading block of output rows sized to about `seconds`."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    from fusion_pcu_amd import synthetic as syn
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    a = syn.uniform(11, (m, k), np.float32)
+    b = syn.uniform(12, (k, n), np.float32)
+    rows, dt = 64, 0.0
+    while True:
+        t0 = time.perf_counter()
+        _, fault = oracle.matmul(a[:rows], b, threads=threads)
+        dt = time.perf_counter() - t0
+        assert fault is None
+        if dt >= seconds / 4 or rows >= m:
+            break
+        rows = min(m, rows * 4)
+    return {
+        "value": 2.0 * rows * n * k / dt / 1e9,
+        "unit": "GFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"output rows 0..{rows - 1} of the strict F32 MatMul {m}x{k}x{n} with the "
+                  f"oracle's fast path ({threads} OpenMP threads); {dt:.1f} s",
+    }
+
+
 def probe(pkg, M, K, N) -> int:
     """One launch of each kernel whose HBM traffic is measured with rocprofv3 --pmc:
     the strict F32 MatMul 4096^3, a copy-like calibration kernel (checked Add of +0 over
@@ -326,6 +355,9 @@ def main() -> int:
     if not args.no_cpu:
         log(f"CPU baseline: faithful port on {args.cpu_rows} rows")
         cpu = cpu_baseline(M, K, N, args.cpu_rows)
+        if not args.no_extra:
+            log("CPU reference point: the oracle's fast path on all allowed host cores")
+            extra["cpu_fast_oracle"] = cpu_fast_oracle(M, K, N)
     line = {
         "metric": METRIC,
         "value": round(mm["gflops"], 2),

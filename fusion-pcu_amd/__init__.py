@@ -193,6 +193,20 @@ class Context:
 
     MATMUL_ENGINES = {"auto": 0, "valu": 1, "mfma_products": 2}
 
+    def last_fault(self) -> Optional[CompoundFault]:
+        """First fault of the most recent program or op call (pcu_fault_read), or None."""
+        f = _abi.Fault()
+        st = self._lib.pcu_fault_read(self.handle, ctypes.byref(f))
+        if st == _abi.PCU_OK:
+            return None
+        if st != _abi.PCU_ARITHMETIC_FAULT:
+            self.check(st)
+        return _fault_from(f)
+
+    def reset_fault(self) -> None:
+        """Forget the held fault (pcu_fault_reset)."""
+        self.check(self._lib.pcu_fault_reset(self.handle))
+
     def set_matmul_engine(self, engine: str) -> None:
         """Main-kernel engine of the strict F32 MatMul ("auto", "valu", "mfma_products");
         every engine gives the same bits."""

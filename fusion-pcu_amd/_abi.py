@@ -78,6 +78,8 @@ SIGNATURES = {
     "pcu_program_begin": (_i32, [_vp]),
     "pcu_program_end": (_i32, [_vp, _FP]),
     "pcu_program_next_node": (_u32, [_vp]),
+    "pcu_fault_read": (_i32, [_vp, _FP]),
+    "pcu_fault_reset": (_i32, [_vp]),
     "pcu_mark": (_i32, [_vp, _i32]),
     "pcu_elapsed_ms": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_float)]),
     "pcu_profile_enable": (_i32, [_vp, _i32]),

@@ -43,7 +43,9 @@ struct Ctx {
     unsigned long long *host_words = nullptr;  // pinned mirror
     bool in_program = false;
     bool implicit_program = false;
-    bool words_pending = false; // the open program's fault words and gate await their reset
+    bool words_pending = false;
+    pcu_fault held_fault{};      // first fault of the most recent program
+    bool has_held_fault = false; // the open program's fault words and gate await their reset
     std::vector<NodeInfo> nodes;
     std::string error;
 

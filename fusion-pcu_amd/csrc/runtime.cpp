@@ -373,6 +373,9 @@ pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
         f.node = (uint32_t)i;
         faults->push_back(f);
     }
+    has_held_fault = !faults->empty();
+    if (has_held_fault)
+        held_fault = faults->front();
     return PCU_OK;
 }
 
@@ -1017,6 +1020,25 @@ pcu_status pcu_program_end(pcu_ctx *ctx, pcu_fault *first_fault)
 uint32_t pcu_program_next_node(const pcu_ctx *ctx)
 {
     return ctx ? (uint32_t)reinterpret_cast<const Ctx *>(ctx)->nodes.size() : 0;
+}
+
+pcu_status pcu_fault_read(const pcu_ctx *ctx, pcu_fault *fault)
+{
+    if (!ctx || !fault)
+        return PCU_ERR_ARGUMENT;
+    const Ctx *c = reinterpret_cast<const Ctx *>(ctx);
+    if (!c->has_held_fault)
+        return PCU_OK;
+    *fault = c->held_fault;
+    return PCU_ARITHMETIC_FAULT;
+}
+
+pcu_status pcu_fault_reset(pcu_ctx *ctx)
+{
+    if (!ctx)
+        return bad_ctx();
+    reinterpret_cast<Ctx *>(ctx)->has_held_fault = false;
+    return PCU_OK;
 }
 
 pcu_status pcu_ctx_set_matmul_engine(pcu_ctx *ctx, pcu_matmul_engine engine)

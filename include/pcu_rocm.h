@@ -210,6 +210,15 @@ pcu_status pcu_program_begin(pcu_ctx *ctx);
 pcu_status pcu_program_end(pcu_ctx *ctx, pcu_fault *first_fault);
 /* Node number the next op call will receive inside the current program. */
 uint32_t pcu_program_next_node(const pcu_ctx *ctx);
+/* The first fault of the most recent program (an op call outside a program is a program of
+ * one node), as that call returned it: PCU_ARITHMETIC_FAULT with *fault filled, or PCU_OK
+ * when that program completed without a fault or after pcu_fault_reset. Replaces the
+ * reference's per-node read and decode of the packed fault word
+ * (backends/rocm/owned_dispatch.rs:76-110) for callers that pass no pcu_fault to the ops. */
+pcu_status pcu_fault_read(const pcu_ctx *ctx, pcu_fault *fault);
+/* Forget the held fault (the reference re-arms each node's word with the u64::MAX sentinel,
+ * backends/rocm/owned_dispatch.rs:20-21). */
+pcu_status pcu_fault_reset(pcu_ctx *ctx);
 
 /* ------------------------------------------------------- kernel timing hooks
  * HIP events recorded on the ordered stream around enqueued work, so a caller can time

@@ -513,6 +513,30 @@ def test_program_reports_first_node_and_recovers(ctx, pcu_pkg):
     np.testing.assert_array_equal(_bits(y.numpy()), _bits(ref2))
 
 
+def test_held_fault_read_and_reset(ctx, pcu_pkg):
+    """pcu_fault_read returns the first fault of the most recent call, as that call
+    reported it; a clean call clears it, and so does pcu_fault_reset."""
+    a = np.ones((3, 4), np.float32)
+    b = np.ones((4, 2), np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    ctx.strict_matmul(da, db)
+    assert ctx.last_fault() is None
+    a[1, 2] = np.nan
+    dbad = ctx.upload(a)
+    with pytest.raises(pcu_pkg.PcuExecutionError) as e:
+        ctx.strict_matmul(dbad, db)
+    held = ctx.last_fault()
+    assert held == e.value.tensor_fault
+    assert (held.element_index, held.reduction_index) == (2, 2)  # row 1, col 0, k = 2
+    ctx.reset_fault()
+    assert ctx.last_fault() is None
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        ctx.strict_matmul(dbad, db)
+    assert ctx.last_fault() is not None
+    ctx.strict_matmul(da, db)
+    assert ctx.last_fault() is None
+
+
 @pytest.mark.parametrize("engine_name", ["valu", "mfma_products"])
 def test_program_stage_gate_skips_nodes_after_a_fault(ctx, pcu_pkg, engine_name):
     """Stage gating (backends/rocm/owned_dispatch/guarded/guarded.rs): once a node has
