@@ -372,7 +372,9 @@ def engine(request, ctx):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 @pytest.mark.parametrize("shape", [(1, 1, 1), (2, 3, 2), (65, 3, 17), (128, 128, 128),
                                    (129, 67, 255), (300, 257, 130), (512, 1024, 256),
-                                   (33, 1, 257), (1, 513, 1), (255, 17, 129)])
+                                   (33, 1, 257), (1, 513, 1), (255, 17, 129),
+                                   # whole-slab kernels: one slab, and whole in two of three
+                                   (128, 16, 128), (256, 32, 384), (256, 48, 130), (130, 64, 256)])
 def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape, engine):
     m, k, n = shape
     rng = np.random.default_rng(m * 7 + k * 3 + n)
