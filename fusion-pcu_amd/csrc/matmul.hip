@@ -295,17 +295,25 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 b[j] = Bs[cur][k][col_of(j)];
+            // Per row, the eight rounded products first and then the eight rounded sums:
+            // no add waits on the multiply just before it (F64 measured 4% faster than
+            // alternating multiply/add through one temporary).
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < 8; i++) {
+                if (NATIVE) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (NATIVE) {
+                    for (int j = 0; j < 8; j++)
                         acc[i][j] = fma(a[i], b[j], acc[i][j]);
-                    } else {
-                        T p = a[i] * b[j];
-                        acc[i][j] = acc[i][j] + p;
-                    }
+                } else {
+                    T p[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        p[j] = a[i] * b[j];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        acc[i][j] = acc[i][j] + p[j];
                 }
+            }
         }
         if (kt + 1 < ktiles)
             stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
