@@ -731,6 +731,11 @@ template <typename T> struct WalkShared {
                                      // wave walk (offset); kNoStep: no crossing
     typename SumBits<T>::U total[2]; // total after the crossing Add or the wave walk
     int stop[2];                     // an Add faulted
+    int first_cand[2];               // candidate summary the stopping chunk matched, or -1
+    // Result of a chunk's run-prefix fold (written by the one thread holding the crossing).
+    uint64_t run_m;
+    int run_status, run_ue;
+    uint32_t run_resume;
     uint64_t limit;
 };
 
@@ -860,16 +865,16 @@ __device__ bool wave_walk(const typename SumBits<T>::U *vals, uint64_t base, uin
     return true;
 }
 
-// Exact fold of the chunk at base (len elements) from the phase (ue, m, mmax): by the wave
-// walk where crossings are dense, elsewhere window by window, where the one thread whose
-// run holds the window's first step to reach the binade's end executes that step as the
-// contract's Add and the next window starts after it in the new binade. Returns false when
-// an Add faulted (recorded).
+// Exact fold of elements [start, len) of the chunk at base from the phase (ue, m, mmax): by
+// the wave walk where crossings are dense, elsewhere window by window, where the one thread
+// whose run holds the window's first step to reach the binade's end executes that step as
+// the contract's Add and the next window starts after it in the new binade. Returns false
+// when an Add faulted (recorded).
 template <typename T>
 __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint64_t base,
-                            uint32_t len, double mean, int policy, unsigned long long *fault,
-                            int &ue, typename SumBits<T>::C &m, typename SumBits<T>::C &mmax,
-                            WalkShared<T> &sh, const NodeGate &gate)
+                            uint32_t len, uint32_t start, double mean, int policy,
+                            unsigned long long *fault, int &ue, typename SumBits<T>::C &m,
+                            typename SumBits<T>::C &mmax, WalkShared<T> &sh, const NodeGate &gate)
 {
     using U = typename SumBits<T>::U;
     using C = typename SumBits<T>::C;
@@ -880,7 +885,7 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint
     if (tid == 0)
         sh.at[0] = sh.at[1] = kNoStep;
     __syncthreads();
-    uint32_t off = 0, per = 0; // per = 0: no window has run yet
+    uint32_t off = start, per = 0; // per = 0: no window has run yet
     bool wave_ok = true;
     for (int it = 0; off < len; it++) {
         const int slot = it & 1;
@@ -977,6 +982,118 @@ __device__ bool exact_chunk(const typename SumBits<T>::U *__restrict__ src, uint
     return true;
 }
 
+// Summaries kept per chunk: the estimate's binade less and plus 1/512 of it (lo, hi) and,
+// when the estimate says the chunk crosses a binade, the binade after hi (where the rest
+// of the chunk lands after one crossing).
+constexpr int kCands = 3;
+
+template <typename T>
+__device__ __forceinline__ SumScan<T> scan_of_summary(const ChunkSummary &c)
+{
+    using C = typename SumBits<T>::C;
+    const C r0 = (C)c.r0, r1 = (C)c.r1;
+    return SumScan<T>{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
+}
+
+// Run-prefix fold of the chunk at base whose summary `cand` (made for the running binade)
+// reaches the binade's end. runs_c holds, per candidate, each thread run's exclusive prefix
+// (run t = elements [P*t, P*t + P)). The run where the count reaches the end is the one
+// whose prefixes straddle it; its thread walks the run with the automaton, executes the
+// crossing step as the contract's Add, and walks the rest of the run in the new binade.
+// The runs after it fold at once from the prefixes of a candidate made for the new binade:
+// from parity q at the chunk start a candidate's prefix adds E(q) before run t and T(q) over
+// the whole chunk, so the runs from t on add T(q) - E(q), for the q whose parity after E is
+// the parity actually standing there. Returns 1 when the chunk is folded, 0 when the Add
+// faulted (recorded), -1 when a second crossing (or a missing candidate) leaves elements
+// [*resume, len) to the windowed path, with (ue, m, mmax) standing before element *resume.
+template <typename T>
+__device__ int run_prefix_chunk(const typename SumBits<T>::U *__restrict__ src,
+                                const SumScan<T> *__restrict__ runs_c,
+                                const ChunkSummary *__restrict__ summ_c, int cand, uint64_t base,
+                                uint32_t len, int policy, unsigned long long *fault, int &ue,
+                                typename SumBits<T>::C &m, typename SumBits<T>::C &mmax,
+                                uint32_t &resume, WalkShared<T> &sh, const NodeGate &gate)
+{
+    using U = typename SumBits<T>::U;
+    using C = typename SumBits<T>::C;
+    constexpr uint32_t P = SumBits<T>::kPer;
+    const int tid = threadIdx.x;
+    const SumScan<T> *ry = runs_c + (size_t)cand * kSumThreads;
+    const SumScan<T> E = ry[tid];
+    const SumScan<T> E1 = tid + 1 < kSumThreads ? ry[tid + 1] : scan_of_summary<T>(summ_c[cand]);
+    const uint32_t p0 = (uint32_t)(m & 1u);
+    const C mt = sat_add<T>(m, p0 ? E.r1 : E.r0), mt1 = sat_add<T>(m, p0 ? E1.r1 : E1.r0);
+    // Counts only grow along the chunk: exactly one run starts below the end and reaches it.
+    if (mt < mmax && mt1 >= mmax) {
+        uint32_t pt = p0 ? (E.p >> 1) & 1u : E.p & 1u;
+        C mm = mt, mx = mmax;
+        int u = ue, status = 1;
+        bool crossed = false;
+        const uint32_t i0 = (uint32_t)tid * P, i1 = i0 + P < len ? i0 + P : len;
+        uint32_t at = i1;
+        for (uint32_t i = i0; i < i1; i++) {
+            const U b = src[base + i];
+            C nn;
+            uint32_t cls;
+            sum_elem<T>(b, u, nn, cls);
+            const C r = sum_step<C>(nn, cls, pt);
+            if (cls == kRForce || mm + r >= mx) {
+                if (crossed) { // a second crossing inside the run
+                    status = -1;
+                    at = i;
+                    break;
+                }
+                const T acc = from_bits<T>(sum_bits<T>(u, mm));
+                const T s_i = from_bits<T>(b);
+                const T res = acc + s_i;
+                const uint32_t kind = classify_add(acc, s_i, res, policy);
+                if (kind != kOk) {
+                    atomicMin(fault, (unsigned long long)pack_fault(3 * (base + i) + 2, kind));
+                    gate_record(gate);
+                    status = 0;
+                    break;
+                }
+                sum_phase<T>((U)bits_of(res), u, mm, mx);
+                pt = (uint32_t)(mm & 1u);
+                crossed = true;
+                continue;
+            }
+            mm += r;
+            pt = (pt + (uint32_t)r) & 1u;
+        }
+        if (status == 1 && i1 < len) {
+            // The runs after this one, from the prefixes of a candidate for the new binade.
+            status = -1;
+            for (int y = 0; y < kCands; y++) {
+                if (summ_c[y].ue != u)
+                    continue;
+                const SumScan<T> Ey = runs_c[(size_t)y * kSumThreads + tid + 1];
+                const SumScan<T> Ty = scan_of_summary<T>(summ_c[y]);
+                const int q = (Ey.p & 1u) == pt ? 0 : (((Ey.p >> 1) & 1u) == pt ? 1 : -1);
+                if (q < 0)
+                    break;
+                const C tq = q ? Ty.r1 : Ty.r0, eq = q ? Ey.r1 : Ey.r0;
+                if (tq < SumBits<T>::kCap && mm + (tq - eq) < mx) {
+                    mm += tq - eq;
+                    status = 1;
+                }
+                break;
+            }
+        }
+        sh.run_status = status;
+        sh.run_ue = u;
+        sh.run_m = (uint64_t)mm;
+        sh.run_resume = at;
+    }
+    __syncthreads();
+    const int status = sh.run_status;
+    if (status == 0)
+        return 0;
+    sum_phase<T>(sum_bits<T>(sh.run_ue, (C)sh.run_m), ue, m, mmax);
+    resume = sh.run_resume;
+    return status;
+}
+
 // A: chunk sums in binary64 (order inside a chunk does not matter: only an estimate).
 template <typename T>
 __global__ __launch_bounds__(256) void k_mse_chunk_sums(const T *__restrict__ sq, uint64_t n,
@@ -1039,11 +1156,13 @@ __global__ __launch_bounds__(kPrefixThreads) void k_mse_chunk_prefix(const doubl
 }
 
 // C: summary of chunk blockIdx.x for candidate blockIdx.y (0: the binade of the estimate
-// less 1/512 of it, 1: plus 1/512; the second is skipped when both agree).
+// less 1/512 of it; 1: plus 1/512, skipped when both agree; 2: the binade after candidate 1,
+// only when the estimate says the chunk crosses), with every thread run's exclusive prefix.
 template <typename T>
 __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     const T *__restrict__ sq, uint64_t n, const unsigned long long *fault,
-    const double *__restrict__ chunk_pre, ChunkSummary *__restrict__ summ, NodeGate gate)
+    const double *__restrict__ chunk_sum, const double *__restrict__ chunk_pre,
+    ChunkSummary *__restrict__ summ, SumScan<T> *__restrict__ runs, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -1055,13 +1174,14 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     const uint64_t limit = sum_limit(fault, n);
     const double pre = chunk_pre[c];
     const int32_t lo = phase_ue_of<T>(pre * (1.0 - 1.0 / 512)), hi = phase_ue_of<T>(pre * (1.0 + 1.0 / 512));
-    ChunkSummary *out = summ + 2 * c + blockIdx.y;
-    if (blockIdx.y == 1 && hi == lo) {
+    const int32_t end = phase_ue_of<T>((pre + chunk_sum[c]) * (1.0 + 1.0 / 512));
+    ChunkSummary *out = summ + kCands * c + blockIdx.y;
+    if ((blockIdx.y == 1 && hi == lo) || (blockIdx.y == 2 && end <= lo)) {
         if (tid == 0)
             *out = ChunkSummary{0, 0, kNoPhase, 0};
         return;
     }
-    const int ue = blockIdx.y ? hi : lo;
+    const int ue = blockIdx.y == 0 ? lo : (blockIdx.y == 1 ? hi : hi + 1);
     const U *src = reinterpret_cast<const U *>(sq);
     U cur[P];
     const uint64_t base = c * sum_chunk_len<T>();
@@ -1078,6 +1198,7 @@ __global__ __launch_bounds__(kSumThreads) void k_mse_chunk_summaries(
     }
     SumScan<T> excl, total;
     block_scan<T>(mine, lane, wave, wave_tot, excl, total);
+    runs[(kCands * c + blockIdx.y) * kSumThreads + tid] = excl;
     if (tid == 0)
         *out = ChunkSummary{(uint64_t)total.r0, (uint64_t)total.r1, ue, 0};
 }
@@ -1087,7 +1208,7 @@ template <typename T>
 __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_mse_ordered_walk(
     const T *__restrict__ sq, uint64_t n, T count, int policy, T *__restrict__ out,
     unsigned long long *fault, const double *__restrict__ chunk_sum,
-    const ChunkSummary *__restrict__ summ, NodeGate gate)
+    const ChunkSummary *__restrict__ summ, const SumScan<T> *__restrict__ runs, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -1114,15 +1235,14 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
         const int slot = it & 1;
         const uint64_t c = c0 + tid;
         SumScan<T> mine = scan_identity<T>();
+        int cand = -1;
         if (c < chunks) {
-            const ChunkSummary a = summ[2 * c], b = summ[2 * c + 1];
-            if (a.ue == ue || b.ue == ue) {
-                // Summary counts saturate at kCap, past any crossing: they fit C.
-                const C r0 = (C)(a.ue == ue ? a.r0 : b.r0), r1 = (C)(a.ue == ue ? a.r1 : b.r1);
-                mine = SumScan<T>{r0, r1, (uint32_t)(r0 & 1u) | ((uint32_t)((r1 + 1) & 1u) << 1)};
-            } else {
-                mine = SumScan<T>{kBig, kBig, 2u}; // no summary for this binade: stop here
-            }
+            for (int y = kCands - 1; y >= 0; y--)
+                if (summ[kCands * c + y].ue == ue)
+                    cand = y;
+            // Summary counts saturate at kCap, past any crossing: they fit C. No summary for
+            // this binade: stop here.
+            mine = cand >= 0 ? scan_of_summary<T>(summ[kCands * c + cand]) : SumScan<T>{kBig, kBig, 2u};
         }
         SumScan<T> before, total;
         block_scan<T>(mine, lane, wave, sh.wave_tot, before, total);
@@ -1132,10 +1252,12 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
         if (c < chunks && mt < mmax && sat_add<T>(mt, pt ? mine.r1 : mine.r0) >= mmax) {
             sh.first[slot] = (uint32_t)tid;
             sh.m_first[slot] = (uint64_t)mt;
+            sh.first_cand[slot] = cand;
         }
         __syncthreads();
         const uint32_t first = sh.first[slot];
         const C m_first = (C)sh.m_first[slot];
+        const int first_cand = sh.first_cand[slot];
         if (tid == 0)
             sh.first[slot ^ 1] = kNoStep;
         if (first == kNoStep) {
@@ -1143,13 +1265,22 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
             c0 += kSumThreads;
             continue;
         }
-        // Chunks before the stopping one fold; it runs exactly from the count before it.
+        // Chunks before the stopping one fold; it runs exactly from the count before it:
+        // from its run prefixes when it has a summary for this binade, and in windows from
+        // wherever that leaves off.
         m = m_first;
         const uint64_t cc = c0 + first;
         const uint64_t base = cc * L;
         const uint32_t len = (uint32_t)(base + L <= limit ? L : limit - base);
-        if (!exact_chunk<T>(src, base, len, chunk_sum[cc] / (double)len, policy, fault, ue, m,
-                            mmax, sh, gate))
+        uint32_t resume = 0;
+        const int folded = first_cand < 0 ? -1
+                                          : run_prefix_chunk<T>(src, runs + kCands * cc * kSumThreads,
+                                                                summ + kCands * cc, first_cand, base, len,
+                                                                policy, fault, ue, m, mmax, resume, sh, gate);
+        if (folded == 0)
+            return;
+        if (folded < 0 && !exact_chunk<T>(src, base, len, resume, chunk_sum[cc] / (double)len, policy,
+                                          fault, ue, m, mmax, sh, gate))
             return;
         c0 = cc + 1;
     }
@@ -1430,14 +1561,17 @@ size_t mse_scratch_bytes(int dtype, uint64_t n)
 {
     const size_t es = dtype == 0 ? 4 : 8;
     const size_t chunks = dtype == 0 ? mse_chunks<float>(n) : mse_chunks<double>(n);
+    const size_t run_bytes = dtype == 0 ? sizeof(SumScan<float>) : sizeof(SumScan<double>);
     return round256(n * es) + 2 * round256(chunks * sizeof(double)) +
-           round256(2 * chunks * sizeof(ChunkSummary));
+           round256(kCands * chunks * sizeof(ChunkSummary)) +
+           round256(kCands * chunks * kSumThreads * run_bytes);
 }
 
 template <typename T> struct MseScratch {
     T *squares;
     double *chunk_sum, *chunk_pre;
     ChunkSummary *summ;
+    SumScan<T> *runs;
     size_t chunks;
     MseScratch(void *scratch, uint64_t n)
     {
@@ -1447,6 +1581,7 @@ template <typename T> struct MseScratch {
         chunk_sum = (double *)(base + round256(n * sizeof(T)));
         chunk_pre = (double *)((char *)chunk_sum + round256(chunks * sizeof(double)));
         summ = (ChunkSummary *)((char *)chunk_pre + round256(chunks * sizeof(double)));
+        runs = (SumScan<T> *)((char *)summ + round256(kCands * chunks * sizeof(ChunkSummary)));
     }
 };
 
@@ -1464,7 +1599,7 @@ static hipError_t mse_prepare_t(hipStream_t s, uint64_t n, const void *p, const 
         hipLaunchKernelGGL((k_mse_squares<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)p, (const T *)t, m.squares, n, policy, fault, gate);
     hipLaunchKernelGGL((k_mse_chunk_sums<T>), dim3((unsigned)m.chunks), dim3(256), 0, s, (const T *)m.squares, n, (const unsigned long long *)fault, m.chunk_sum, gate);
     hipLaunchKernelGGL(k_mse_chunk_prefix, dim3(1), dim3(kPrefixThreads), 0, s, (const double *)m.chunk_sum, (uint64_t)m.chunks, m.chunk_pre, gate);
-    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)m.chunks, 2), dim3(kSumThreads), 0, s, (const T *)m.squares, n, (const unsigned long long *)fault, (const double *)m.chunk_pre, m.summ, gate);
+    hipLaunchKernelGGL((k_mse_chunk_summaries<T>), dim3((unsigned)m.chunks, kCands), dim3(kSumThreads), 0, s, (const T *)m.squares, n, (const unsigned long long *)fault, (const double *)m.chunk_sum, (const double *)m.chunk_pre, m.summ, m.runs, gate);
     return hipGetLastError();
 }
 
@@ -1473,7 +1608,7 @@ static hipError_t mse_walk_t(hipStream_t s, uint64_t n, void *scratch, T count, 
                              int policy, unsigned long long *fault, NodeGate gate)
 {
     const MseScratch<T> m(scratch, n);
-    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)m.squares, n, count, policy, (T *)out, fault, (const double *)m.chunk_sum, (const ChunkSummary *)m.summ, gate);
+    hipLaunchKernelGGL((k_mse_ordered_walk<T>), dim3(1), dim3(kSumThreads), 0, s, (const T *)m.squares, n, count, policy, (T *)out, fault, (const double *)m.chunk_sum, (const ChunkSummary *)m.summ, (const SumScan<T> *)m.runs, gate);
     return hipGetLastError();
 }
 
