@@ -192,6 +192,21 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
     }
 }
 
+// The column minima targets of a MatMul whose two prefilter jobs are both column jobs,
+// and its first-suspect word: a = kExpNone over [0, na), b over [0, nb), *suspect empty.
+__global__ void k_open_col_targets(int *a, uint64_t na, int *b, uint64_t nb,
+                                   unsigned long long *suspect)
+{
+    const uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = i0; i < na; i += step)
+        a[i] = kExpNone;
+    for (uint64_t i = i0; i < nb; i += step)
+        b[i] = kExpNone;
+    if (i0 == 0)
+        *suspect = kNoFault;
+}
+
 __global__ void k_fill_i32(int *p, uint64_t n, int v)
 {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -524,12 +539,13 @@ static void prefilter(hipStream_t s, const ExpJob<T> &ja, const ExpJob<T> &jb,
             cols[nc++] = j;
     }
     if (nr == 0) {
-        // Both jobs fold with atomics: open their targets and the suspect word first.
-        for (int k = 0; k < nc; k++) {
-            const unsigned fg = (unsigned)((cols[k]->C + 255) / 256 < 1024 ? (cols[k]->C + 255) / 256 : 1024);
-            hipLaunchKernelGGL(k_fill_i32, dim3(fg ? fg : 1), dim3(256), 0, s, cols[k]->out, cols[k]->C, kExpNone);
-        }
-        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, suspect, (uint64_t)1, (unsigned long long)kNoFault);
+        // Both jobs fold with atomics: open their targets and the suspect word first, in
+        // one launch.
+        const uint64_t n0 = cols[0]->C, n1 = nc > 1 ? cols[1]->C : 0;
+        const uint64_t most = n0 > n1 ? n0 : n1;
+        const unsigned fg = (unsigned)((most + 255) / 256 < 1024 ? (most + 255) / 256 : 1024);
+        hipLaunchKernelGGL(k_open_col_targets, dim3(fg ? fg : 1), dim3(256), 0, s, cols[0]->out, n0,
+                           nc > 1 ? cols[1]->out : nullptr, n1, suspect);
     } else {
         exp_rows<T>(s, *rows[0], nc ? cols[0]->out : nullptr, nc ? cols[0]->C : 0, suspect, gate);
         if (nr == 2)
