@@ -244,9 +244,10 @@ def cpu_fast_oracle(m, k, n, seconds=5.0):
 
 
 def probe(pkg, M, K, N) -> int:
-    """One launch of each kernel whose HBM traffic is measured with rocprofv3 --pmc:
-    the strict F32 MatMul 4096^3, a copy-like calibration kernel (checked Add of +0 over
-    2^26 f32: 256 MiB read + 256 MiB written) and strict SGD over 2^26 f32."""
+    """One launch of each kernel whose counters are read with rocprofv3 --pmc: the strict
+    F32 MatMul 4096^3 (both engines), a copy-like calibration kernel (checked Add of +0 over
+    2^26 f32: 256 MiB read + 256 MiB written), strict SGD over 2^26 f32 and the strict F64
+    MatMul 4096^3 (after one warm-up launch)."""
     from fusion_pcu_amd import synthetic as syn
     n = 1 << 26
     with pkg.Context(0) as ctx:
@@ -267,6 +268,14 @@ def probe(pkg, M, K, N) -> int:
         ctx.set_matmul_engine("valu")
         ctx.strict_matmul(da, db, out=dc)
         ctx.set_matmul_engine("auto")
+        log("probe: F64 MatMul (C3 shape), warm-up then one launch")
+        for x_ in (da, db, dc):
+            x_.free()
+        da = ctx.upload(syn.uniform(31, (M, K), np.float64))
+        db = ctx.upload(syn.uniform(32, (K, N), np.float64))
+        dc = ctx.empty((M, N), np.float64)
+        ctx.strict_matmul(da, db, out=dc)
+        ctx.strict_matmul(da, db, out=dc)
         ctx.synchronize()
     log("probe: done")
     return 0
