@@ -83,6 +83,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // 4096^3 when op(A) and op(B) are staged alike (both transposed or neither) and about
     // 0.4% slower otherwise, so it is used only there.
     constexpr bool kIssuePrio = TA == TB;
+    // The k loop is peeled and run two pairs a trip only for whole slabs with neither
+    // operand staged transposed: about 0.5% faster there, while the other stagings spill
+    // with it.
+    constexpr bool kPeel = !TA && !TB && WHOLE;
     auto mma = [&](float a, float b) {
         if (kIssuePrio)
             __builtin_amdgcn_s_setprio(1);
@@ -91,14 +95,16 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             __builtin_amdgcn_s_setprio(0);
         return r;
     };
-    // Fold one MFMA's products into a subtile: each cell adds its k product, then its
-    // k+1 product (registers r and 16 + r of the same cell).
+    // Fold one MFMA's products into a subtile: each cell adds its k product (register r),
+    // then its k+1 product (register 16 + r). The sixteen k sums go first, so no add waits
+    // on the add just before it (measured 2-3% faster with a transposed operand).
     auto fold = [&](float (&c)[16], const v32f &p) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[r];
+#pragma unroll
+        for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[16 + r];
-        }
     };
 
     const int ktiles = (K + BK - 1) / BK;
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // Software pipeline: one MFMA is in flight while the vector unit folds the previous
         // one (the group barriers ask the scheduler for that alternation). Lanes 0-31 carry
         // k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
-        float a[SM], b[SN];
+        float a[SM], b[SN], na[SM], nb[SN];
 #pragma unroll
         for (int i = 0; i < SM; i++)
             a[i] = As[cur][half][wm + 32 * i + col];
@@ -132,18 +138,20 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         for (int j = 0; j < SN; j++)
             b[j] = Bs[cur][half][wn + 32 * j + col];
         v32f p = mma(a[0], b[0]);
-#pragma unroll 1
-        for (int kk = 0; kk < BK - 2; kk += 2) {
-            float na[SM], nb[SN];
+        // One k-pair: read the operands of pair kk + 2 into (ya, yb), then issue the rest
+        // of pair kk's MFMAs from (xa, xb) and pair kk + 2's first, each beside the fold of
+        // the product issued before it.
+        auto pair = [&](int kk, const float (&xa)[SM], const float (&xb)[SN], float (&ya)[SM],
+                        float (&yb)[SN]) {
 #pragma unroll
             for (int i = 0; i < SM; i++)
-                na[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
+                ya[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
 #pragma unroll
             for (int j = 0; j < SN; j++)
-                nb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
+                yb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
 #pragma unroll
             for (int t = 0; t < S; t++) {
-                const v32f q = t + 1 < S ? mma(a[(t + 1) / SN], b[(t + 1) % SN]) : mma(na[0], nb[0]);
+                const v32f q = t + 1 < S ? mma(xa[(t + 1) / SN], xb[(t + 1) % SN]) : mma(ya[0], yb[0]);
                 fold(acc[t], p);
                 p = q;
             }
@@ -152,18 +160,56 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 32, 0); // 32 VALU (a fold)
             }
+        };
+        if constexpr (kPeel) {
+            // The first pair runs before the loop, so the loop is entered long after the
+            // MFMA above and its first fold needs no wait states inside the loop; each trip
+            // runs two pairs with the operand registers swapped between them.
+            static_assert((BK - 4) % 4 == 0, "pairs after the first come in twos");
+            pair(0, a, b, na, nb);
+#pragma unroll 1
+            for (int kk = 2; kk < BK - 2; kk += 4) {
+                pair(kk, na, nb, a, b);
+                pair(kk + 2, a, b, na, nb);
+            }
+        } else {
+            // The same pair written out in the loop: called through `pair` here, the
+            // transposed stagings compile with an extra wait inside the loop (7-16% slower).
+#pragma unroll 1
+            for (int kk = 0; kk < BK - 2; kk += 2) {
+                float ya[SM], yb[SN];
 #pragma unroll
-            for (int i = 0; i < SM; i++)
-                a[i] = na[i];
+                for (int i = 0; i < SM; i++)
+                    ya[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
 #pragma unroll
-            for (int j = 0; j < SN; j++)
-                b[j] = nb[j];
+                for (int j = 0; j < SN; j++)
+                    yb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
+#pragma unroll
+                for (int t = 0; t < S; t++) {
+                    const v32f q = t + 1 < S ? mma(a[(t + 1) / SN], b[(t + 1) % SN]) : mma(ya[0], yb[0]);
+                    fold(acc[t], p);
+                    p = q;
+                }
+#pragma unroll
+                for (int t = 0; t < S; t++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 32, 0); // 32 VALU (a fold)
+                }
+#pragma unroll
+                for (int i = 0; i < SM; i++)
+                    a[i] = ya[i];
+#pragma unroll
+                for (int j = 0; j < SN; j++)
+                    b[j] = yb[j];
+            }
         }
         // Last k-pair of the stage: nothing further to issue after its final subtile.
+        const float(&la)[SM] = kPeel ? na : a;
+        const float(&lb)[SN] = kPeel ? nb : b;
 #pragma unroll
         for (int t = 0; t < S; t++) {
             if (t + 1 < S) {
-                const v32f q = mma(a[(t + 1) / SN], b[(t + 1) % SN]);
+                const v32f q = mma(la[(t + 1) / SN], lb[(t + 1) % SN]);
                 fold(acc[t], p);
                 p = q;
             } else {
