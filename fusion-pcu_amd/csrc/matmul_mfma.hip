@@ -83,10 +83,6 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // 4096^3 when op(A) and op(B) are staged alike (both transposed or neither) and about
     // 0.4% slower otherwise, so it is used only there.
     constexpr bool kIssuePrio = TA == TB;
-    // The k loop is peeled and run two pairs a trip only for whole slabs with neither
-    // operand staged transposed: about 0.5% faster there, while the other stagings spill
-    // with it.
-    constexpr bool kPeel = !TA && !TB && WHOLE;
     auto mma = [&](float a, float b) {
         if (kIssuePrio)
             __builtin_amdgcn_s_setprio(1);
@@ -105,6 +101,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 #pragma unroll
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[16 + r];
+        // Emits nothing; ties the sixteen sums to this point of the instruction stream.
+        asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
+                     "+v"(c[6]), "+v"(c[7]), "+v"(c[8]), "+v"(c[9]), "+v"(c[10]), "+v"(c[11]),
+                     "+v"(c[12]), "+v"(c[13]), "+v"(c[14]), "+v"(c[15]));
     };
 
     const int ktiles = (K + BK - 1) / BK;
@@ -127,94 +127,37 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             else
                 stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
         }
-        // Software pipeline: one MFMA is in flight while the vector unit folds the previous
-        // one (the group barriers ask the scheduler for that alternation). Lanes 0-31 carry
-        // k = kk, lanes 32-63 carry k = kk + 1 (the MFMA's two blocks).
-        float a[SM], b[SN], na[SM], nb[SN];
-#pragma unroll
-        for (int i = 0; i < SM; i++)
-            a[i] = As[cur][half][wm + 32 * i + col];
-#pragma unroll
-        for (int j = 0; j < SN; j++)
-            b[j] = Bs[cur][half][wn + 32 * j + col];
-        v32f p = mma(a[0], b[0]);
-        // One k-pair: read the operands of pair kk + 2 into (ya, yb), then issue the rest
-        // of pair kk's MFMAs from (xa, xb) and pair kk + 2's first, each beside the fold of
-        // the product issued before it.
-        auto pair = [&](int kk, const float (&xa)[SM], const float (&xb)[SN], float (&ya)[SM],
-                        float (&yb)[SN]) {
+        // Software pipeline over the whole slab, unrolled: each MFMA is issued, then the
+        // products of the one before it are folded. sched_barrier pins that order (left to
+        // the scheduler, the same sequence measured about 8% slower), and each k-pair's
+        // operands are read from LDS one pair ahead. Lanes 0-31 carry k = 2j, lanes 32-63
+        // carry k = 2j + 1 (the MFMA's two blocks).
+        constexpr int NP = BK / 2;
+        float oa[NP][SM], ob[NP][SN];
+        auto rd = [&](int j) {
 #pragma unroll
             for (int i = 0; i < SM; i++)
-                ya[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
+                oa[j][i] = As[cur][2 * j + half][wm + 32 * i + col];
 #pragma unroll
-            for (int j = 0; j < SN; j++)
-                yb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
-#pragma unroll
-            for (int t = 0; t < S; t++) {
-                const v32f q = t + 1 < S ? mma(xa[(t + 1) / SN], xb[(t + 1) % SN]) : mma(ya[0], yb[0]);
-                fold(acc[t], p);
-                p = q;
-            }
-#pragma unroll
-            for (int t = 0; t < S; t++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 32, 0); // 32 VALU (a fold)
-            }
+            for (int jj = 0; jj < SN; jj++)
+                ob[j][jj] = Bs[cur][2 * j + half][wn + 32 * jj + col];
         };
-        if constexpr (kPeel) {
-            // The first pair runs before the loop, so the loop is entered long after the
-            // MFMA above and its first fold needs no wait states inside the loop; each trip
-            // runs two pairs with the operand registers swapped between them.
-            static_assert((BK - 4) % 4 == 0, "pairs after the first come in twos");
-            pair(0, a, b, na, nb);
-#pragma unroll 1
-            for (int kk = 2; kk < BK - 2; kk += 4) {
-                pair(kk, na, nb, a, b);
-                pair(kk + 2, a, b, na, nb);
-            }
-        } else {
-            // The same pair written out in the loop: called through `pair` here, the
-            // transposed stagings compile with an extra wait inside the loop (7-16% slower).
-#pragma unroll 1
-            for (int kk = 0; kk < BK - 2; kk += 2) {
-                float ya[SM], yb[SN];
+        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
+        rd(0);
+        v32f p = mma(oa[0][0], ob[0][0]);
 #pragma unroll
-                for (int i = 0; i < SM; i++)
-                    ya[i] = As[cur][kk + 2 + half][wm + 32 * i + col];
-#pragma unroll
-                for (int j = 0; j < SN; j++)
-                    yb[j] = Bs[cur][kk + 2 + half][wn + 32 * j + col];
-#pragma unroll
-                for (int t = 0; t < S; t++) {
-                    const v32f q = t + 1 < S ? mma(a[(t + 1) / SN], b[(t + 1) % SN]) : mma(ya[0], yb[0]);
-                    fold(acc[t], p);
-                    p = q;
-                }
-#pragma unroll
-                for (int t = 0; t < S; t++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 32, 0); // 32 VALU (a fold)
-                }
-#pragma unroll
-                for (int i = 0; i < SM; i++)
-                    a[i] = ya[i];
-#pragma unroll
-                for (int j = 0; j < SN; j++)
-                    b[j] = yb[j];
-            }
-        }
-        // Last k-pair of the stage: nothing further to issue after its final subtile.
-        const float(&la)[SM] = kPeel ? na : a;
-        const float(&lb)[SN] = kPeel ? nb : b;
-#pragma unroll
-        for (int t = 0; t < S; t++) {
-            if (t + 1 < S) {
-                const v32f q = mma(la[(t + 1) / SN], lb[(t + 1) % SN]);
-                fold(acc[t], p);
-                p = q;
-            } else {
-                fold(acc[t], p);
-            }
+        for (int j = 0; j < NP; j++) {
+            if (j + 1 < NP)
+                rd(j + 1);
+            const v32f q = mma(oa[j][0], ob[j][1]);
+            __builtin_amdgcn_sched_barrier(0);
+            fold(acc[0], p);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j + 1 < NP)
+                p = mma(oa[j + 1][0], ob[j + 1][0]);
+            __builtin_amdgcn_sched_barrier(0);
+            fold(acc[1], q);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (kt + 1 < ktiles)
             stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
