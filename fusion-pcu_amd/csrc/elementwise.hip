@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
                                                        T *__restrict__ out, uint64_t n,
                                                        int policy, unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T 
                                                      uint64_t n, int policy,
                                                      unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restric
                                                               int policy,
                                                               unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a
                                                          unsigned long long *fault_add,
                                                          unsigned long long *fault_relu, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key_add = kNoFault, key_relu = kNoFault;
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kEwThreads) void k_sgd(const T *__restrict__ w,
                                                     T *__restrict__ out, uint64_t n, int policy,
                                                     unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kEwThreads) void k_mse_squares(const T *__restrict_
                                                             int policy,
                                                             unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
@@ -1308,7 +1308,7 @@ __global__ __launch_bounds__(kEwThreads) void k_native_sgd(const T *__restrict__
                                                            const T *__restrict__ g, T rate,
                                                            T *__restrict__ out, uint64_t n, NodeGate gate)
 {
-    if (block_gate_closed(gate))
+    if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     PCU_EW_LOOP(W)
