@@ -79,7 +79,16 @@ struct Ctx {
     pcu_status release(void *p);
     pcu_status copy(void *dst, const void *src, size_t bytes, bool upload);
     pcu_status join_side();
-    pcu_status scratch(size_t bytes, hipStream_t s, void **out);
+    // Device scratch kept for the context's lifetime and grown on demand, so an op does not
+    // allocate and free per call (a stream-ordered free left a gap of about 6 us before the
+    // next kernel). The MatMul screen's buffer is used on the ordered stream only; the MSE
+    // buffer is also read by the walk on the side stream, so taking it joins that stream.
+    struct Scratch {
+        void *p = nullptr;
+        size_t cap = 0;
+    };
+    Scratch matmul_scratch, mse_scratch;
+    pcu_status scratch(Scratch &buf, size_t bytes, bool side_reader, void **out);
 
     pcu_status open_words();
     pcu_status begin_program(bool implicit);

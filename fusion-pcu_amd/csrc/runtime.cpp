@@ -102,6 +102,11 @@ Ctx::~Ctx()
         (void)hipStreamSynchronize(stream);
     if (side)
         (void)hipStreamSynchronize(side);
+    for (Scratch *b : {&matmul_scratch, &mse_scratch})
+        if (b->p)
+            (void)hipFreeAsync(b->p, stream);
+    if (stream)
+        (void)hipStreamSynchronize(stream);
     if (fault_words)
         (void)hipFree(fault_words);
     if (host_words)
@@ -414,9 +419,23 @@ pcu_status Ctx::start_op()
 
 // Scratch comes from the stream-ordered pool and is released on the same stream right
 // after the op's kernels, so later ops reuse it without a host round trip.
-pcu_status Ctx::scratch(size_t bytes, hipStream_t s, void **out)
+pcu_status Ctx::scratch(Scratch &buf, size_t bytes, bool side_reader, void **out)
 {
-    return hip(hipMallocFromPoolAsync(out, bytes ? bytes : 1, pool, s), "hipMallocFromPoolAsync");
+    pcu_status st;
+    if (side_reader && (st = join_side())) // an earlier walk may still read the buffer
+        return st;
+    if (bytes > buf.cap) {
+        // Ordered after every earlier use on this stream.
+        if (buf.p && (st = hip(hipFreeAsync(buf.p, stream), "hipFreeAsync")))
+            return st;
+        buf.p = nullptr;
+        buf.cap = 0;
+        if ((st = hip(hipMallocFromPoolAsync(&buf.p, bytes, pool, stream), "hipMallocFromPoolAsync")))
+            return st;
+        buf.cap = bytes;
+    }
+    *out = buf.p;
+    return PCU_OK;
 }
 
 // ------------------------------------------------------------------ timing
@@ -501,7 +520,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     if (rows == 0 || cols == 0)
         return PCU_OK;
     void *sc = nullptr;
-    if ((st = scratch(matmul_scratch_bytes(rows, cols), stream, &sc)))
+    if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols), false, &sc)))
         return st;
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
 
@@ -521,7 +540,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         timings.push_back({PCU_KERNEL_STRICT_GEMM, ev[1], ev[2]});
         timings.push_back({PCU_KERNEL_GEMM_REPLAY, ev[2], ev[3]});
     }
-    return hip(hipFreeAsync(sc, stream), "hipFreeAsync");
+    return PCU_OK;
 }
 
 pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const void *b,
@@ -673,7 +692,7 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     if (st)
         return st;
     void *sq = nullptr;
-    if ((st = scratch(mse_scratch_bytes(dtype, n), stream, &sq)))
+    if ((st = scratch(mse_scratch, mse_scratch_bytes(dtype, n), true, &sq)))
         return st;
     if ((st = open_words()))
         return st;
@@ -698,7 +717,7 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
                   "strict_mse launch")))
         return st;
     timer_stop(PCU_KERNEL_MSE, t1, s);
-    return hip(hipFreeAsync(sq, s), "hipFreeAsync");
+    return PCU_OK;
 }
 
 // ------------------------------------------------------------ native compounds
@@ -778,16 +797,14 @@ pcu_status Ctx::op_native_mse(int dtype, uint64_t n, const void *p, const void *
         scale = 1.0 / count_as(dtype, n);
     }
     void *sc = nullptr;
-    if ((st = scratch(native_mse_scratch_bytes(dtype, n), stream, &sc)))
+    if ((st = scratch(mse_scratch, native_mse_scratch_bytes(dtype, n), true, &sc)))
         return st;
     if ((st = open_words()))
         return st;
     hipEvent_t t0 = timer_start(stream);
     st = hip(launch_native_mse(stream, dtype, n, p, t, sc, scale, out, gate_for(word)), "native_mse launch");
     timer_stop(PCU_KERNEL_NATIVE_MSE, t0, stream);
-    if (st)
-        return st;
-    return hip(hipFreeAsync(sc, stream), "hipFreeAsync");
+    return st;
 }
 
 } // namespace pcu
