@@ -1188,7 +1188,8 @@ pcu_status pcu_prepared_take_output(pcu_prepared *ph, uint32_t index, void **dev
     int published_bank = p->bank ^ 1; // execute() flips after publishing
     void *fresh = nullptr;
     size_t bytes = p->graph.elements(id) * (nd.dtype == 0 ? 4 : 8);
-    pcu_status st = p->ctx->alloc(bytes, &fresh);
+    // The replacement bank is written only by later executions, in stream order.
+    pcu_status st = p->ctx->alloc(bytes, &fresh, true);
     if (st)
         return st;
     *device_ptr = p->buf[published_bank][id];

@@ -75,7 +75,9 @@ struct Ctx {
     void fail(const char *fmt, ...) __attribute__((format(printf, 2, 3)));
     pcu_status hip(hipError_t e, const char *what);
 
-    pcu_status alloc(size_t bytes, void **out);
+    // ordered_only: the buffer is used only by work later enqueued on the ordered stream
+    // (a prepared program's bank), so the allocation is not waited for.
+    pcu_status alloc(size_t bytes, void **out, bool ordered_only = false);
     pcu_status release(void *p);
     pcu_status copy(void *dst, const void *src, size_t bytes, bool upload);
     pcu_status join_side();

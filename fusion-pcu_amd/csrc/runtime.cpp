@@ -135,7 +135,7 @@ Ctx::~Ctx()
         (void)hipStreamDestroy(side);
 }
 
-pcu_status Ctx::alloc(size_t bytes, void **out)
+pcu_status Ctx::alloc(size_t bytes, void **out, bool ordered_only)
 {
     if (!out) {
         fail("null output pointer");
@@ -145,8 +145,8 @@ pcu_status Ctx::alloc(size_t bytes, void **out)
     if (bytes == 0)
         bytes = 1;
     pcu_status st = hip(hipMallocFromPoolAsync(out, bytes, pool, stream), "hipMallocFromPoolAsync");
-    if (st || in_program)
-        return st; // inside a program the buffer is used in stream order until the end
+    if (st || in_program || ordered_only)
+        return st; // used in stream order (inside a program, until its end)
     // Usable from any stream once the allocation is ordered.
     return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
