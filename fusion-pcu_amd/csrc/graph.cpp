@@ -593,24 +593,36 @@ pcu_status Graph::plan(const std::vector<uint32_t> &outputs, std::vector<uint32_
 
 static size_t dsize(int dtype) { return dtype == 0 ? 4 : 8; }
 
-Prepared::~Prepared()
+void prepared_detach(Prepared *p)
 {
+    Ctx *ctx = p->ctx;
     if (!ctx)
         return;
     (void)ctx->join_side();
     (void)hipStreamSynchronize(ctx->stream);
     for (int b = 0; b < 2; b++)
-        for (void *p : buf[b])
-            if (p)
-                (void)ctx->release(p);
-    for (void *p : dense_uniform)
-        if (p)
-            (void)ctx->release(p);
+        for (void *&q : p->buf[b])
+            if (q) {
+                (void)ctx->release(q);
+                q = nullptr;
+            }
+    for (void *&q : p->dense_uniform)
+        if (q) {
+            (void)ctx->release(q);
+            q = nullptr;
+        }
+    auto &list = ctx->prepared;
+    list.erase(std::remove(list.begin(), list.end(), p), list.end());
+    p->ctx = nullptr;
+    p->published = false;
 }
+
+Prepared::~Prepared() { prepared_detach(this); }
 
 pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &outs)
 {
     ctx = c;
+    c->prepared.push_back(this);
     graph = g;
     outputs = outs;
     pcu_status st = graph.plan(outputs, &order);
@@ -1154,6 +1166,10 @@ pcu_status pcu_prepared_execute(pcu_prepared *ph, uint32_t n_inputs, const void 
     Prepared *p = reinterpret_cast<Prepared *>(ph);
     if (!p || (n_inputs && !device_inputs))
         return PCU_ERR_ARGUMENT;
+    if (!p->ctx) {
+        pcu::g_thread_error = "prepared_execute: its context was closed";
+        return PCU_ERR_STATE;
+    }
     std::vector<const void *> in(device_inputs, device_inputs + n_inputs);
     pcu_status st = p->execute(in, fault);
     if (st && st != PCU_ARITHMETIC_FAULT)
@@ -1175,6 +1191,10 @@ pcu_status pcu_prepared_take_output(pcu_prepared *ph, uint32_t index, void **dev
     if (!p || !device_ptr || index >= p->outputs.size())
         return PCU_ERR_ARGUMENT;
     *device_ptr = nullptr;
+    if (!p->ctx) {
+        pcu::g_thread_error = "take_output: its context was closed";
+        return PCU_ERR_STATE;
+    }
     if (!p->published || !p->published_ptr[index]) {
         p->ctx->fail("take_output: output %u is not published", index);
         return PCU_ERR_STATE;

@@ -25,6 +25,11 @@ struct NodeInfo {
 
 double count_as(int dtype, uint64_t n);
 
+struct Prepared;
+// A prepared graph gives its device buffers back and forgets its context (defined with the
+// graph executor).
+void prepared_detach(Prepared *p);
+
 struct Ctx {
     static constexpr unsigned kMaxNodes = 4096;
     static constexpr size_t kStagingBytes = 64u << 20;
@@ -90,6 +95,9 @@ struct Ctx {
         size_t cap = 0;
     };
     Scratch matmul_scratch, mse_scratch;
+    // Prepared graphs built on this context: closing the context detaches them (their
+    // buffers are released while the context's streams still exist).
+    std::vector<Prepared *> prepared;
     pcu_status scratch(Scratch &buf, size_t bytes, bool side_reader, void **out);
 
     pcu_status open_words();

@@ -98,6 +98,8 @@ Ctx::~Ctx()
     if (device < 0)
         return;
     (void)hipSetDevice(device);
+    while (!prepared.empty())
+        prepared_detach(prepared.back()); // removes itself from the list
     if (stream)
         (void)hipStreamSynchronize(stream);
     if (side)

@@ -198,3 +198,30 @@ def test_first_faulting_node_matches_oracle(G, pcu_pkg):
     rf = ref["fault"]
     assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
         (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step, rf.fault.kind)
+
+
+def test_prepared_graph_outliving_its_context(G, pcu_pkg):
+    """Closing a context releases the device buffers of the prepared graphs built on it and
+    detaches them: a later execution is refused (PcuExecutionError) and destroying the
+    prepared graph afterwards touches nothing of the closed context."""
+    import gc
+    ctx = pcu_pkg.Context(0)
+    g = G.Graph()
+    g.set_numerical_mode(True)
+    x = g.input((8, 4), np.float32)
+    w = g.input((4, 8), np.float32)
+    out = g.relu(g.matmul(x, w))
+    prep = g.prepare(ctx, [out])
+    dx = ctx.upload(np.ones((8, 4), np.float32))
+    dw = ctx.upload(np.full((4, 8), 0.5, np.float32))
+    prep.execute([dx.ptr, dw.ptr])
+    got = prep.take_output(0).numpy()
+    assert np.array_equal(got, np.full((8, 8), 2.0, np.float32))
+    ptrs = [dx.ptr, dw.ptr]
+    dx.free()
+    dw.free()
+    ctx.close()
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        prep.execute(ptrs)  # refused before any pointer is used
+    del prep
+    gc.collect()
