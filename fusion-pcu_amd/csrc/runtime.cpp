@@ -107,6 +107,8 @@ Ctx::~Ctx()
     for (Scratch *b : {&matmul_scratch, &mse_scratch})
         if (b->p)
             (void)hipFreeAsync(b->p, stream);
+    for (const Released &r : reuse)
+        (void)hipFreeAsync(r.p, stream);
     if (stream)
         (void)hipStreamSynchronize(stream);
     if (fault_words)
@@ -146,9 +148,18 @@ pcu_status Ctx::alloc(size_t bytes, void **out, bool ordered_only)
     *out = nullptr;
     if (bytes == 0)
         bytes = 1;
-    pcu_status st = hip(hipMallocFromPoolAsync(out, bytes, pool, stream), "hipMallocFromPoolAsync");
-    if (st || in_program || ordered_only)
-        return st; // used in stream order (inside a program, until its end)
+    pcu_status st = PCU_OK;
+    auto hit = std::find_if(reuse.begin(), reuse.end(), [&](const Released &r) { return r.bytes == bytes; });
+    if (hit != reuse.end()) {
+        *out = hit->p;
+        reuse_bytes -= hit->bytes;
+        reuse.erase(hit);
+    } else if ((st = hip(hipMallocFromPoolAsync(out, bytes, pool, stream), "hipMallocFromPoolAsync"))) {
+        return st;
+    }
+    alloc_bytes[*out] = bytes;
+    if (in_program || ordered_only)
+        return PCU_OK; // used in stream order (inside a program, until its end)
     // Usable from any stream once the allocation is ordered.
     return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
@@ -161,6 +172,16 @@ pcu_status Ctx::release(void *p)
     pcu_status st = join_side();
     if (st)
         return st;
+    auto it = alloc_bytes.find(p);
+    if (it != alloc_bytes.end()) {
+        const size_t bytes = it->second;
+        alloc_bytes.erase(it);
+        if (reuse.size() < kReuseSlots && reuse_bytes + bytes <= kReuseMaxBytes) {
+            reuse.push_back({p, bytes}); // reused in stream order after its queued users
+            reuse_bytes += bytes;
+            return PCU_OK;
+        }
+    }
     return hip(hipFreeAsync(p, stream), "hipFreeAsync");
 }
 
