@@ -227,9 +227,10 @@ static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, co
     else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
 }
 
-// 8 waves of 32 x 64 over a 128 x 128 tile, 127 VGPRs (4 waves per SIMD). On MI355X at
+// 8 waves of 32 x 64 over a 128 x 128 tile, 123-126 VGPRs (4 waves per SIMD). On MI355X at
 // 4096^3 this measured ahead of 4 waves of 64 x 64 (2 waves per SIMD), 16 waves of
-// 32 x 32, a 256 x 128 tile, and BK = 32.
+// 32 x 32, a 256 x 128 tile, 4-wave tiles of 128 x 64 and 64 x 64, and BK = 32 (which
+// spills with the pinned slab).
 using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
