@@ -56,35 +56,39 @@ __device__ __forceinline__ int wave_min_i32(int v)
     return v;
 }
 
-// Minimum exponents for the underflow screen. Both kernels read their operand once with
-// 16-byte loads (VEC: rows or columns of whole runs, 16-byte aligned).
+// Minimum exponents for the underflow screen, one entry per row of op(A) and per column of
+// op(B). Depending on the transposes, each is the minimum over a row or over a column of a
+// stored matrix. An entry is a 64-bit word (generation << 32) | (kExpBias - e): the column
+// jobs fold their 64-row groups with atomicMax, under which a word of the current MatMul
+// (larger generation) replaces any older one and, within it, the largest kExpBias - e is the
+// smallest e. So no entry needs opening before the screen, and both jobs of a MatMul run in
+// one launch. Readers take e = kExpBias - (low 32 bits).
 
-// out[r] = min over c of ilog2|X[r, c]| for a row-major R x C matrix; one wave per row.
-// The first prefilter launch of a MatMul also opens the other kernel's atomicMin targets
-// (init[0, n_init) = kExpNone) and clears the first-suspect word, saving two fill launches.
+// One exponent job: per-row minima of a stored R x C matrix (rows) or per-column (cols).
+template <typename T> struct ExpJob {
+    const T *X;
+    uint64_t R, C;
+    bool rows;
+    bool vec; // C a multiple of 16 bytes and X 16-byte aligned
+    unsigned long long *out;
+};
+
+// Rows job, block `bid`: one wave per row, four rows per 256-thread block; four 16-byte loads
+// per lane in flight.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, uint64_t R,
-                                                      uint64_t C, int *__restrict__ out,
-                                                      int *__restrict__ init, uint64_t n_init,
-                                                      unsigned long long *suspect, NodeGate gate)
+__device__ __forceinline__ void exp_rows_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen)
 {
-    if (block_gate_closed(gate))
-        return;
-    const uint64_t gtid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (uint64_t i = gtid; i < n_init; i += (uint64_t)gridDim.x * blockDim.x)
-        init[i] = kExpNone;
-    if (suspect && gtid == 0)
-        *suspect = kNoFault;
-    const uint64_t r = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64;
-    if (r >= R)
+    const uint64_t r = bid * 4 + threadIdx.x / 64;
+    if (r >= j.R)
         return; // whole wave exits together
     const int lane = threadIdx.x % 64;
+    const uint64_t C = j.C;
     int m = kExpNone;
-    const T *row = X + r * C;
+    const T *row = j.X + r * C;
     if (VEC) {
         constexpr int P = 16 / sizeof(T);
         constexpr uint64_t S = 64 * P; // elements one pass of the wave covers
-        constexpr int U = 4;           // 16-byte loads per lane in flight
+        constexpr int U = 4;
         uint64_t c = (uint64_t)lane * P;
         for (; c + (U - 1) * S < C; c += U * S) {
             uint4 q[U];
@@ -95,8 +99,8 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
             for (int u = 0; u < U; u++) {
                 const T *v = reinterpret_cast<const T *>(&q[u]);
 #pragma unroll
-                for (int j = 0; j < P; j++) {
-                    const int e = ilog2_abs(v[j]);
+                for (int k = 0; k < P; k++) {
+                    const int e = ilog2_abs(v[k]);
                     m = e < m ? e : m;
                 }
             }
@@ -105,8 +109,8 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
             const uint4 q = *reinterpret_cast<const uint4 *>(row + c);
             const T *v = reinterpret_cast<const T *>(&q);
 #pragma unroll
-            for (int j = 0; j < P; j++) {
-                const int e = ilog2_abs(v[j]);
+            for (int k = 0; k < P; k++) {
+                const int e = ilog2_abs(v[k]);
                 m = e < m ? e : m;
             }
         }
@@ -118,29 +122,29 @@ __global__ __launch_bounds__(256) void k_exp_min_rows(const T *__restrict__ X, u
     }
     m = wave_min_i32(m);
     if (lane == 0)
-        out[r] = m;
+        j.out[r] = exp_word(gen, m);
 }
 
-// out[c] = min over r of ilog2|X[r, c]|. A block is 64 column-runs (16 bytes each) by 4 row
-// groups over 64 rows; the row groups meet in LDS and the block folds its minimum into out
-// with one atomicMin per column (out opened to kExpNone beforehand). Fewer rows per block
-// measured slower: the atomics on one column then contend.
+// Columns job, block `bid` = (column block cb, 64-row group rg): 64 column-runs (16 bytes
+// each) by 4 row groups of 16 rows; the row groups meet in LDS and the block folds its
+// minimum into out with one atomicMax per column. Fewer rows per block measured slower: the
+// atomics on one column then contend.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, uint64_t R,
-                                                      uint64_t C, int *__restrict__ out, NodeGate gate)
+__device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen,
+                                               int (*part)[64 * 16 / sizeof(T)])
 {
     constexpr int P = VEC ? 16 / sizeof(T) : 1;
-    __shared__ int part[4][64 * P];
-    if (block_gate_closed(gate))
-        return;
+    const uint64_t R = j.R, C = j.C, ncb = (C + 64 * P - 1) / (64 * P);
+    const uint64_t cb = bid % ncb, rg = bid / ncb;
     const int cx = threadIdx.x % 64, ry = threadIdx.x / 64;
-    const uint64_t c0 = ((uint64_t)blockIdx.x * 64 + cx) * P;
-    const uint64_t r0 = (uint64_t)blockIdx.y * 64;
+    const uint64_t c0 = (cb * 64 + cx) * P;
+    const uint64_t r0 = rg * 64;
     const uint64_t r1 = r0 + 64 < R ? r0 + 64 : R;
+    const T *X = j.X;
     int m[P];
 #pragma unroll
-    for (int j = 0; j < P; j++)
-        m[j] = kExpNone;
+    for (int k = 0; k < P; k++)
+        m[k] = kExpNone;
     if (c0 < C) {
         uint64_t r = r0 + ry;
         if (VEC) {
@@ -154,9 +158,9 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
                 for (int u = 0; u < 4; u++) {
                     const T *v = reinterpret_cast<const T *>(&q[u]);
 #pragma unroll
-                    for (int j = 0; j < P; j++) {
-                        const int e = ilog2_abs(v[j]);
-                        m[j] = e < m[j] ? e : m[j];
+                    for (int k = 0; k < P; k++) {
+                        const int e = ilog2_abs(v[k]);
+                        m[k] = e < m[k] ? e : m[k];
                     }
                 }
             }
@@ -167,9 +171,9 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
                 const uint4 q = *reinterpret_cast<const uint4 *>(p);
                 const T *v = reinterpret_cast<const T *>(&q);
 #pragma unroll
-                for (int j = 0; j < P; j++) {
-                    const int e = ilog2_abs(v[j]);
-                    m[j] = e < m[j] ? e : m[j];
+                for (int k = 0; k < P; k++) {
+                    const int e = ilog2_abs(v[k]);
+                    m[k] = e < m[k] ? e : m[k];
                 }
             } else {
                 const int e = ilog2_abs(p[0]);
@@ -178,33 +182,55 @@ __global__ __launch_bounds__(256) void k_exp_min_cols(const T *__restrict__ X, u
         }
     }
 #pragma unroll
-    for (int j = 0; j < P; j++)
-        part[ry][cx * P + j] = m[j];
+    for (int k = 0; k < P; k++)
+        part[ry][cx * P + k] = m[k];
     __syncthreads();
     if (ry == 0 && c0 < C) {
 #pragma unroll
-        for (int j = 0; j < P; j++) {
-            int v = part[0][cx * P + j];
+        for (int k = 0; k < P; k++) {
+            int v = part[0][cx * P + k];
             for (int g = 1; g < 4; g++)
-                v = part[g][cx * P + j] < v ? part[g][cx * P + j] : v;
-            atomicMin(&out[c0 + j], v);
+                v = part[g][cx * P + k] < v ? part[g][cx * P + k] : v;
+            atomicMax(&j.out[c0 + k], exp_word(gen, v));
         }
     }
 }
 
-// The column minima targets of a MatMul whose two prefilter jobs are both column jobs,
-// and its first-suspect word: a = kExpNone over [0, na), b over [0, nb), *suspect empty.
-__global__ void k_open_col_targets(int *a, uint64_t na, int *b, uint64_t nb,
-                                   unsigned long long *suspect)
+template <typename T> __host__ __device__ inline uint64_t exp_blocks(const ExpJob<T> &j)
 {
-    const uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = i0; i < na; i += step)
-        a[i] = kExpNone;
-    for (uint64_t i = i0; i < nb; i += step)
-        b[i] = kExpNone;
-    if (i0 == 0)
+    if (j.rows)
+        return (j.R + 3) / 4;
+    const uint64_t P = j.vec ? 16 / sizeof(T) : 1;
+    return ((j.C + 64 * P - 1) / (64 * P)) * ((j.R + 63) / 64);
+}
+
+// Both jobs of a MatMul in one launch: blocks [0, na) run job a, the rest job b. A block's
+// branches are uniform, so the columns job's barrier is reached by all of its threads. The
+// launch also clears the MatMul's first-suspect word.
+template <typename T>
+__global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, uint64_t na,
+                                                    uint32_t gen, unsigned long long *suspect,
+                                                    NodeGate gate)
+{
+    __shared__ int part[4][64 * 16 / sizeof(T)];
+    if (block_gate_closed(gate))
+        return;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
         *suspect = kNoFault;
+    const bool first = blockIdx.x < na;
+    const ExpJob<T> &j = first ? a : b;
+    const uint64_t bid = first ? blockIdx.x : blockIdx.x - na;
+    if (j.rows) {
+        if (j.vec)
+            exp_rows_block<T, true>(j, bid, gen);
+        else
+            exp_rows_block<T, false>(j, bid, gen);
+    } else {
+        if (j.vec)
+            exp_cols_block<T, true>(j, bid, gen, part);
+        else
+            exp_cols_block<T, false>(j, bid, gen, part);
+    }
 }
 
 __global__ void k_fill_i32(int *p, uint64_t n, int v)
@@ -247,8 +273,8 @@ template <typename T> struct ValuCfg {
 template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false, bool WHOLE = false>
 __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
-    const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr, int check_risk,
-    int vec_c, unsigned long long *suspect, NodeGate gate)
+    const unsigned long long *__restrict__ row_exp, const unsigned long long *__restrict__ col_exp,
+    int thr, int check_risk, int vec_c, unsigned long long *suspect, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -398,7 +424,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
         int r = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
         if (r >= M)
             continue;
-        int rexp = check_risk ? row_exp[r] : 0;
+        int rexp = check_risk ? exp_of(row_exp[r]) : 0;
 #pragma unroll
         for (int h = 0; h < RUNS; h++) {
             int c0 = n0 + col_of(h * RUN);
@@ -422,7 +448,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                     continue;
                 bool bad = !finite_bits(acc[i][h * RUN + j]);
                 if (check_risk)
-                    bad |= rexp + col_exp[c] < thr;
+                    bad |= rexp + exp_of(col_exp[c]) < thr;
                 if (bad) {
                     uint64_t cell = (uint64_t)r * N + c;
                     key = cell < key ? cell : key;
@@ -439,8 +465,8 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 template <typename T>
 __global__ __launch_bounds__(256) void k_strict_gemm_replay(
     const T *__restrict__ A, const T *__restrict__ B, const T *__restrict__ C, uint64_t M,
-    uint64_t N, uint64_t K, int ta, int tb, const int *__restrict__ row_exp,
-    const int *__restrict__ col_exp, int thr, int check_risk, int policy,
+    uint64_t N, uint64_t K, int ta, int tb, const unsigned long long *__restrict__ row_exp,
+    const unsigned long long *__restrict__ col_exp, int thr, int check_risk, int policy,
     const unsigned long long *suspect, unsigned long long *fault, NodeGate gate)
 {
     if (block_gate_closed(gate))
@@ -461,7 +487,7 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
         uint64_t r = cell / N, c = cell % N;
         bool bad = !finite_bits(C[cell]);
         if (check_risk)
-            bad |= row_exp[r] + col_exp[c] < thr;
+            bad |= exp_of(row_exp[r]) + exp_of(col_exp[c]) < thr;
         if (!bad)
             continue;
         T total = (T)0;
@@ -491,19 +517,19 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
 
 size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols)
 {
-    size_t r = ((rows * sizeof(int)) + 255) & ~(size_t)255;
-    size_t c = ((cols * sizeof(int)) + 255) & ~(size_t)255;
+    size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
+    size_t c = ((cols * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     return r + c + 256;
 }
 
 MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols)
 {
     char *p = (char *)base;
-    size_t r = ((rows * sizeof(int)) + 255) & ~(size_t)255;
-    size_t c = ((cols * sizeof(int)) + 255) & ~(size_t)255;
+    size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
+    size_t c = ((cols * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     MatmulScratch s;
-    s.row_exp = (int *)p;
-    s.col_exp = (int *)(p + r);
+    s.row_exp = (unsigned long long *)p;
+    s.col_exp = (unsigned long long *)(p + r);
     s.suspect = (unsigned long long *)(p + r + c);
     return s;
 }
@@ -547,74 +573,21 @@ hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t 
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// One exponent job: per-row minima of a stored R x C matrix (rows) or per-column (cols).
-template <typename T> struct ExpJob {
-    const T *X;
-    uint64_t R, C;
-    bool rows;
-    int *out;
-};
-
+// The exponent screen of op(A) rows and op(B) columns, both jobs in one launch.
 template <typename T>
-static void exp_rows(hipStream_t s, const ExpJob<T> &j, int *init, uint64_t n_init,
-                     unsigned long long *suspect, NodeGate gate)
-{
-    const bool vec = j.C % (16 / sizeof(T)) == 0 && aligned16(j.X);
-    const dim3 grid((unsigned)((j.R + 3) / 4));
-    if (vec)
-        hipLaunchKernelGGL((k_exp_min_rows<T, true>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, init, n_init, suspect, gate);
-    else
-        hipLaunchKernelGGL((k_exp_min_rows<T, false>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, init, n_init, suspect, gate);
-}
-
-template <typename T>
-static void exp_cols(hipStream_t s, const ExpJob<T> &j, NodeGate gate)
-{
-    constexpr uint64_t P = 16 / sizeof(T);
-    const bool vec = j.C % P == 0 && aligned16(j.X);
-    const uint64_t cols_per_block = 64 * (vec ? P : 1);
-    const dim3 grid((unsigned)((j.C + cols_per_block - 1) / cols_per_block), (unsigned)((j.R + 63) / 64));
-    if (vec)
-        hipLaunchKernelGGL((k_exp_min_cols<T, true>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, gate);
-    else
-        hipLaunchKernelGGL((k_exp_min_cols<T, false>), grid, dim3(256), 0, s, j.X, j.R, j.C, j.out, gate);
-}
-
-// Prefilter of op(A) rows and op(B) columns, plus the first-suspect word: the rows jobs run
-// first and open the columns jobs' targets.
-template <typename T>
-static void prefilter(hipStream_t s, const ExpJob<T> &ja, const ExpJob<T> &jb,
+static void prefilter(hipStream_t s, ExpJob<T> ja, ExpJob<T> jb, uint32_t gen,
                       unsigned long long *suspect, NodeGate gate)
 {
-    const ExpJob<T> *rows[2], *cols[2];
-    int nr = 0, nc = 0;
-    for (const ExpJob<T> *j : {&ja, &jb}) {
-        if (j->rows)
-            rows[nr++] = j;
-        else
-            cols[nc++] = j;
-    }
-    if (nr == 0) {
-        // Both jobs fold with atomics: open their targets and the suspect word first, in
-        // one launch.
-        const uint64_t n0 = cols[0]->C, n1 = nc > 1 ? cols[1]->C : 0;
-        const uint64_t most = n0 > n1 ? n0 : n1;
-        const unsigned fg = (unsigned)((most + 255) / 256 < 1024 ? (most + 255) / 256 : 1024);
-        hipLaunchKernelGGL(k_open_col_targets, dim3(fg ? fg : 1), dim3(256), 0, s, cols[0]->out, n0,
-                           nc > 1 ? cols[1]->out : nullptr, n1, suspect);
-    } else {
-        exp_rows<T>(s, *rows[0], nc ? cols[0]->out : nullptr, nc ? cols[0]->C : 0, suspect, gate);
-        if (nr == 2)
-            exp_rows<T>(s, *rows[1], nullptr, 0, nullptr, gate);
-    }
-    for (int k = 0; k < nc; k++)
-        exp_cols<T>(s, *cols[k], gate);
+    for (ExpJob<T> *j : {&ja, &jb})
+        j->vec = j->C % (16 / sizeof(T)) == 0 && aligned16(j->X);
+    const uint64_t na = exp_blocks(ja), nb = exp_blocks(jb);
+    hipLaunchKernelGGL(k_exp_screen<T>, dim3((unsigned)(na + nb)), dim3(256), 0, s, ja, jb, na, gen, suspect, gate);
 }
 
 template <typename T, bool TA, bool TB>
 static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C, int M, int N,
-                          int K, const int *re, const int *ce, int thr, int risk,
-                          unsigned long long *suspect, NodeGate gate)
+                          int K, const unsigned long long *re, const unsigned long long *ce,
+                          int thr, int risk, unsigned long long *suspect, NodeGate gate)
 {
     bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
@@ -652,9 +625,9 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (risk && K > 0) {
         // op(A) row r is stored row r (A is M x K) or stored column r (A is K x M); op(B)
         // column c is stored column c (B is K x N) or stored row c (B is N x K).
-        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, sc.row_exp};
-        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, sc.col_exp};
-        prefilter<T>(s, ja, jb, sc.suspect, gate);
+        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp};
+        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp};
+        prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate);
     } else {
         risk = 0; // AllowGradual, or an empty reduction: no underflow screen
         hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);

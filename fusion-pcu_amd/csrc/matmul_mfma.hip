@@ -49,8 +49,9 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
 template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
-    int N, int K, const int *__restrict__ row_exp, const int *__restrict__ col_exp, int thr,
-    int check_risk, unsigned long long *suspect, NodeGate gate)
+    int N, int K, const unsigned long long *__restrict__ row_exp,
+    const unsigned long long *__restrict__ col_exp, int thr, int check_risk,
+    unsigned long long *suspect, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         const int i = t / SN, j = t % SN;
         const int c = n0 + wn + 32 * j + col;
         const bool cin = c < N;
-        const int cexp = (check_risk && cin) ? col_exp[c] : 0;
+        const int cexp = (check_risk && cin) ? exp_of(col_exp[c]) : 0;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             C[(size_t)row * N + c] = v;
             bool bad = !finite_bits(v);
             if (check_risk)
-                bad |= row_exp[row] + cexp < thr;
+                bad |= exp_of(row_exp[row]) + cexp < thr;
             if (bad) {
                 const uint64_t cell = (uint64_t)row * N + c;
                 key = cell < key ? cell : key;
@@ -196,8 +197,8 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; 
 
 template <class Cfg, bool TA, bool TB>
 static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
-                          int K, const int *re, const int *ce, int thr, int risk,
-                          unsigned long long *suspect, NodeGate gate)
+                          int K, const unsigned long long *re, const unsigned long long *ce,
+                          int thr, int risk, unsigned long long *suspect, NodeGate gate)
 {
     const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
     const dim3 block(Cfg::kThreads);
@@ -218,7 +219,8 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
 
 template <class Cfg>
 static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, const float *A,
-                        const float *B, float *C, const int *re, const int *ce, int thr,
+                        const float *B, float *C, const unsigned long long *re,
+                        const unsigned long long *ce, int thr,
                         int risk, unsigned long long *suspect, NodeGate gate)
 {
     if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
@@ -234,8 +236,9 @@ static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, co
 using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
-                                const float *A, const float *B, float *C, const int *row_exp,
-                                const int *col_exp, int thr, int risk,
+                                const float *A, const float *B, float *C,
+                                const unsigned long long *row_exp,
+                                const unsigned long long *col_exp, int thr, int risk,
                                 unsigned long long *suspect, NodeGate gate)
 {
     mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);

@@ -404,6 +404,16 @@ __device__ __forceinline__ bool wave_gate_closed(const NodeGate &g)
     return __builtin_amdgcn_readfirstlane(__atomic_load_n(g.word, __ATOMIC_RELAXED)) < g.node;
 }
 
+// A MatMul screen's exponent word: (generation << 32) | (kExpBias - e). Under atomicMax a
+// word of a later generation replaces any older one and, within one, the smallest e wins.
+constexpr int kExpBias = 1 << 21;
+
+__device__ __forceinline__ unsigned long long exp_word(uint32_t gen, int e)
+{
+    return ((unsigned long long)gen << 32) | (uint32_t)(kExpBias - e);
+}
+__device__ __forceinline__ int exp_of(unsigned long long w) { return kExpBias - (int)(uint32_t)w; }
+
 // Record the wave's earliest packed fault with one atomic. `key` is kNoFault on lanes
 // without a fault; the ballot keeps the fault-free path to one instruction. A fault word
 // (as opposed to a scratch word such as the MatMul's first suspect cell) also closes the

@@ -42,10 +42,14 @@ hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, 
                            void *out, int policy, unsigned long long *fault, NodeGate gate);
 
 // Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.
+// Exponent words (generation << 32 | bias - minimum exponent) of op(A) rows and op(B)
+// columns, the first suspect cell, and the screen's generation: a context increases it per
+// MatMul and clears the words when it wraps or the scratch is new.
 struct MatmulScratch {
-    int *row_exp;                  // rows entries
-    int *col_exp;                  // cols entries
-    unsigned long long *suspect;   // first suspect cell (kNoFault when none)
+    unsigned long long *row_exp; // rows entries
+    unsigned long long *col_exp; // cols entries
+    unsigned long long *suspect; // first suspect cell (kNoFault when none)
+    uint32_t gen = 1;
 };
 size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);
 MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
@@ -56,8 +60,9 @@ MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
 enum : int { kEngineAuto = 0, kEngineValu = 1, kEngineMfmaProducts = 2 };
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
-                                const float *A, const float *B, float *C, const int *row_exp,
-                                const int *col_exp, int thr, int risk,
+                                const float *A, const float *B, float *C,
+                                const unsigned long long *row_exp,
+                                const unsigned long long *col_exp, int thr, int risk,
                                 unsigned long long *suspect, NodeGate gate);
 
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.

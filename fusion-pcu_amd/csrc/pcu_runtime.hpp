@@ -96,6 +96,7 @@ struct Ctx {
         size_t cap = 0;
     };
     Scratch matmul_scratch, mse_scratch;
+    uint32_t screen_gen = 0; // generation of the latest MatMul exponent screen
     // Buffers released by the caller are kept for reuse by an allocation of the same size
     // (a training step frees its previous weights and takes as many new ones of the same
     // sizes), instead of a pool free and allocation each (about 7 us of host time per free).

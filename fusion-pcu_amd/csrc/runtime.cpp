@@ -543,9 +543,11 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     if (rows == 0 || cols == 0)
         return PCU_OK;
     void *sc = nullptr;
+    const Scratch old = matmul_scratch;
     if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols), false, &sc)))
         return st;
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
+    const bool fresh = matmul_scratch.p != old.p || matmul_scratch.cap != old.cap;
 
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     if (profiling)
@@ -553,6 +555,16 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
             x = take_event();
     if ((st = open_words()))
         return st;
+    // The screen's exponent words carry a generation that only grows, so a later screen
+    // outranks every word left by earlier ones; new scratch, or a wrapped counter, is
+    // cleared first.
+    if (fresh || screen_gen == UINT32_MAX) {
+        if ((st = hip(launch_fill_u64(stream, (unsigned long long *)sc, matmul_scratch.cap / 8, 0),
+                      "clear MatMul screen words")))
+            return st;
+        screen_gen = 0;
+    }
+    s.gen = ++screen_gen;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
                                         profiling ? ev : nullptr, matmul_engine);
