@@ -101,6 +101,9 @@ typedef struct pcu_fault {
 /* Opens `device`: one HIP stream for ordered work, one side stream for the serial MSE
  * sum, a retained stream-ordered memory pool and a pinned staging buffer. */
 pcu_status pcu_ctx_open(int device, pcu_ctx **out);
+/* Closing releases the device buffers of the prepared graphs built on the context and
+ * detaches them: pcu_prepared_execute and pcu_prepared_take_output on them then return
+ * PCU_ERR_STATE, and pcu_prepared_destroy only frees the host object. */
 void pcu_ctx_close(pcu_ctx *ctx);
 /* Last error text of `ctx` (or of the calling thread when ctx is NULL). */
 const char *pcu_last_error(const pcu_ctx *ctx);
