@@ -35,6 +35,29 @@ __device__ __forceinline__ void load_run(const T *__restrict__ p, int valid, T (
 
 __device__ __forceinline__ int clamp_valid(int rem, int e) { return rem < 0 ? 0 : (rem > e ? e : rem); }
 
+// E elements of a row-major operand as 16-byte runs RS elements apart, the first at p;
+// `rem` elements lie between p and the end of the row.
+template <typename T, int E, int RS, bool VEC>
+__device__ __forceinline__ void load_runs(const T *__restrict__ p, int rem, T (&v)[E])
+{
+    constexpr int P = 16 / (int)sizeof(T);
+#pragma unroll
+    for (int q = 0; q < E / P; q++) {
+        const int valid = clamp_valid(rem - q * RS, P);
+        if (VEC && valid == P) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(p + q * RS);
+            const T *xs = reinterpret_cast<const T *>(&x);
+#pragma unroll
+            for (int j = 0; j < P; j++)
+                v[P * q + j] = xs[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < P; j++)
+                v[P * q + j] = j < valid ? p[q * RS + j] : (T)0;
+        }
+    }
+}
+
 // E elements to LDS at p as 16-byte stores (p 16-byte aligned).
 template <typename T, int E>
 __device__ __forceinline__ void store_run(T *p, const T (&v)[E])
@@ -68,11 +91,17 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &
     tn = (L % per_group) / gsize;
 }
 
-// Cfg provides T-independent BM, BN, BK, kThreads, EA, EB, LDA, LDB.
+// Cfg provides T-independent BM, BN, BK, kThreads, EA, EB, LDA, LDB and kSplitRunsB.
 template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct SlabStager {
     static constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
     static_assert(EA % (16 / sizeof(T)) == 0 && EB % (16 / sizeof(T)) == 0,
                   "staging moves whole 16-byte runs");
+    // Untransposed B under Cfg::kSplitRunsB: a thread's EB elements of a k-row are NRB
+    // 16-byte runs RSB apart, so adjacent lanes store adjacent runs to LDS (contiguous runs
+    // of EB elements put the stores of lanes EB elements apart on the same banks).
+    static constexpr bool kRunsB = Cfg::kSplitRunsB && !TB;
+    static constexpr int RUN = 16 / (int)sizeof(T), NRB = kRunsB ? EB / RUN : 1;
+    static constexpr int TPRB = BN / EB, RSB = BN / NRB, WB = kRunsB ? RUN : EB;
     T ra[EA], rb[EB];
     // Whole slabs (the tile inside M and N, K a multiple of BK, 16-byte loads allowed): the
     // thread's run pointers advance one slab per fetch, with no bound checks.
@@ -89,7 +118,7 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
             sa = (size_t)BK * M;
         }
         if (!TB) {
-            pb = B + (size_t)(tid / (BN / EB)) * N + n0 + (tid % (BN / EB)) * EB;
+            pb = B + (size_t)(tid / TPRB) * N + n0 + (tid % TPRB) * WB;
             sb = (size_t)BK * N;
         } else {
             pb = B + (size_t)(n0 + tid / (BK / EB)) * K + (tid % (BK / EB)) * EB;
@@ -99,7 +128,10 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
     __device__ __forceinline__ void fetch_whole()
     {
         load_run<T, EA, true>(pa, EA, ra);
-        load_run<T, EB, true>(pb, EB, rb);
+        if constexpr (kRunsB)
+            load_runs<T, EB, RSB, true>(pb, BN, rb);
+        else
+            load_run<T, EB, true>(pb, EB, rb);
         pa += sa;
         pb += sb;
     }
@@ -115,8 +147,11 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
             load_run<T, EA, VA>(A + (size_t)k * M + m, k < K ? clamp_valid(M - m, EA) : 0, ra);
         }
         if (!TB) { // B is K x N: BN/EB threads per k-row
-            const int k = k0 + tid / (BN / EB), n = n0 + (tid % (BN / EB)) * EB;
-            load_run<T, EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
+            const int k = k0 + tid / TPRB, n = n0 + (tid % TPRB) * WB;
+            if constexpr (kRunsB)
+                load_runs<T, EB, RSB, VB>(B + (size_t)k * N + n, k < K ? N - n : 0, rb);
+            else
+                load_run<T, EB, VB>(B + (size_t)k * N + n, k < K ? clamp_valid(N - n, EB) : 0, rb);
         } else {   // B is N x K: BK/EB threads per row
             const int n = n0 + tid / (BK / EB), k = k0 + (tid % (BK / EB)) * EB;
             load_run<T, EB, VB>(B + (size_t)n * K + k, n < N ? clamp_valid(K - k, EB) : 0, rb);
@@ -135,8 +170,20 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
             store_run<T, EA>(&As[k][m], ra);
         }
         if (!TB) {
-            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
-            store_run<T, EB>(&Bs[k][n], rb);
+            const int k = tid / TPRB, n = (tid % TPRB) * WB;
+            if constexpr (kRunsB) {
+#pragma unroll
+                for (int q = 0; q < NRB; q++) {
+                    uint4 x;
+                    T *xs = reinterpret_cast<T *>(&x);
+#pragma unroll
+                    for (int j = 0; j < RUN; j++)
+                        xs[j] = rb[RUN * q + j];
+                    *reinterpret_cast<uint4 *>(&Bs[k][n + q * RSB]) = x;
+                }
+            } else {
+                store_run<T, EB>(&Bs[k][n], rb);
+            }
         } else {
             const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
 #pragma unroll
