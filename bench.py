@@ -304,7 +304,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=12)
+    ap.add_argument("--cpu-rows", type=int, default=32)
     ap.add_argument("--probe", action="store_true",
                     help="run each profiled kernel once (for rocprofv3 --pmc passes) and exit")
     args = ap.parse_args()
