@@ -265,9 +265,10 @@ template <typename T> struct ValuCfg {
     static constexpr int kThreads = 256;
     static constexpr int LDA = BM + 4, LDB = BN + 4; // row pitch of the k-major LDS stages
     static constexpr int EA = BM * BK / kThreads, EB = BN * BK / kThreads;
-    // Binary64's 8 elements of a B k-row stay one contiguous run: splitting them into 16-byte
-    // runs 32 apart measured from 1.3% faster to 2.5% slower by operand layout.
-    static constexpr bool kSplitRunsB = false;
+    // Binary64 splits a thread's 8 elements of a B k-row into 16-byte runs 32 apart when A
+    // is untransposed (1.3-2% faster at 4096^3 and 2048x4096x2048) and keeps one contiguous
+    // run under a transposed A (splitting measured 2.5% slower there).
+    template <bool TA> static constexpr bool kSplitRunsB = sizeof(T) == 8 && !TA;
 };
 
 // NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per

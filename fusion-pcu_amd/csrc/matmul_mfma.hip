@@ -44,7 +44,7 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
     static_assert(EA % 4 == 0 && EB % 4 == 0, "staging moves whole float4s");
     // A thread staging several float4s of a B k-row takes them BN / (EB / 4) apart (measured
     // 1.5-2.5% faster for the native kernel's 16 elements than one contiguous run).
-    static constexpr bool kSplitRunsB = EB > 4;
+    template <bool TA> static constexpr bool kSplitRunsB = EB > 4;
 };
 
 // WHOLE: every slab of every tile is whole (M, N, K multiples of the tile and slab, 16-byte

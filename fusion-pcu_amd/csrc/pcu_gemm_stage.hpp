@@ -91,15 +91,15 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &
     tn = (L % per_group) / gsize;
 }
 
-// Cfg provides T-independent BM, BN, BK, kThreads, EA, EB, LDA, LDB and kSplitRunsB.
+// Cfg provides BM, BN, BK, kThreads, EA, EB, LDA, LDB and kSplitRunsB<TA>.
 template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct SlabStager {
     static constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
     static_assert(EA % (16 / sizeof(T)) == 0 && EB % (16 / sizeof(T)) == 0,
                   "staging moves whole 16-byte runs");
-    // Untransposed B under Cfg::kSplitRunsB: a thread's EB elements of a k-row are NRB
+    // Untransposed B under Cfg::kSplitRunsB<TA>: a thread's EB elements of a k-row are NRB
     // 16-byte runs RSB apart, so adjacent lanes store adjacent runs to LDS (contiguous runs
     // of EB elements put the stores of lanes EB elements apart on the same banks).
-    static constexpr bool kRunsB = Cfg::kSplitRunsB && !TB;
+    static constexpr bool kRunsB = Cfg::template kSplitRunsB<TA> && !TB;
     static constexpr int RUN = 16 / (int)sizeof(T), NRB = kRunsB ? EB / RUN : 1;
     static constexpr int TPRB = BN / EB, RSB = BN / NRB, WB = kRunsB ? RUN : EB;
     T ra[EA], rb[EB];
