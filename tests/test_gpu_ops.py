@@ -454,6 +454,35 @@ def test_matmul_fault_variants_parity(ctx, pcu_pkg, dtype, engine):
                 np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_random_fault_placement_fuzz(ctx, pcu_pkg, dtype, engine):
+    """Seeded fuzz of the first-fault search: 24 random shapes, layouts and underflow
+    policies, each with up to three operands of A and of B replaced by NaN, an infinity, a
+    huge value (overflowing products and sums), a value whose products are tiny and mostly
+    inexact, or a subnormal. The GPU must report the oracle's first (cell, k, step, kind)
+    or, when the oracle has none, its bits."""
+    rng = np.random.default_rng(7 if dtype == np.float32 else 8)
+    info = np.finfo(dtype)
+    specials = np.array([np.nan, np.inf, -np.inf, info.max, -info.max,
+                         info.tiny * dtype(2.0 ** 20), -info.tiny * dtype(3.0),
+                         info.smallest_subnormal * dtype(3.0)], dtype=dtype)
+    for case in range(24):
+        m, k, n = (int(v) for v in rng.integers(1, 200, size=3))
+        tl, tr = bool(rng.integers(2)), bool(rng.integers(2))
+        policy = int(rng.integers(3))
+        a = rng.uniform(-1, 1, (k, m) if tl else (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (n, k) if tr else (k, n)).astype(dtype)
+        for x in (a, b):
+            cnt = min(int(rng.integers(0, 4)), x.size)
+            if cnt:
+                x.reshape(-1)[rng.choice(x.size, cnt, replace=False)] = rng.choice(specials, size=cnt)
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(a), ctx.upload(b), tl, tr, policy).numpy())
+        ref, rf = oracle.matmul(a, b, tl, tr, policy=policy)
+        assert gf == _ofault(rf), (case, m, k, n, tl, tr, policy, gf, rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
 @pytest.mark.parametrize("policy", [0, 1, 2])
 def test_matmul_signed_zero_and_subnormal_products(ctx, pcu_pkg, policy, engine):
     """Operands whose products are exact zeros of either sign, subnormal, or straddle the
