@@ -544,6 +544,69 @@ def test_program_reports_first_node_and_recovers(ctx, pcu_pkg):
     np.testing.assert_array_equal(_bits(y.numpy()), _bits(ref2))
 
 
+def _chain_inputs(rng, dtype, m, k, n):
+    """Fresh inputs of the fuzzed chain; some get one special value planted."""
+    info = np.finfo(dtype)
+    specials = np.array([np.nan, np.inf, -np.inf, info.max, info.tiny * dtype(0.75),
+                         info.smallest_subnormal], dtype=dtype)
+    shapes = {"x": (m, k), "w": (k, n), "bias": (m, n), "up": (m, n), "g": (k, n), "t": (m, n)}
+    out = {}
+    for name, shape in shapes.items():
+        v = rng.uniform(-1, 1, shape).astype(dtype)
+        if rng.random() < 0.3:
+            v.reshape(-1)[int(rng.integers(v.size))] = rng.choice(specials)
+        out[name] = v
+    return out
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_program_random_chains_fuzz(ctx, pcu_pkg, dtype):
+    """Seeded fuzz of program mode over 16 chains: y = x.w (node 0), z = y + bias (1),
+    r = relu(z) (2), relu_backward(z, up) (3), sgd(w, g) (4), mse(r, t) (5), with random
+    shapes and a special value planted in some fresh inputs. The program reports the first
+    faulting node in node order with the oracle's coordinates (later nodes are gated); when
+    no node faults, every node's bits match the oracle's."""
+    rng = np.random.default_rng(41 if dtype == np.float32 else 42)
+    rate = 0.01
+    for case in range(16):
+        m, k, n = (int(v) for v in rng.integers(1, 160, size=3))
+        v = _chain_inputs(rng, dtype, m, k, n)
+        # Oracle, node by node, stopping at the first fault.
+        expect, outs = None, []
+        for node, run in enumerate([
+                lambda: oracle.matmul(v["x"], v["w"]),
+                lambda: oracle.binary(0, outs[0], v["bias"]),
+                lambda: oracle.relu(outs[1]),
+                lambda: oracle.relu_backward(outs[1], v["up"]),
+                lambda: oracle.sgd(v["w"], v["g"], rate),
+                lambda: oracle.mse(outs[2], v["t"])]):
+            res, fault = run()
+            if fault is not None:
+                expect = (node,) + _ofault(fault)
+                break
+            outs.append(res)
+        d = {name: ctx.upload(arr) for name, arr in v.items()}
+        got = []
+        try:
+            with ctx.program():
+                gy = ctx.strict_matmul(d["x"], d["w"])
+                gz = ctx.checked_binary(0, gy, d["bias"])
+                gr = ctx.checked_relu(gz)
+                gb = ctx.checked_relu_backward(gz, d["up"])
+                gw = ctx.strict_sgd(d["w"], d["g"], rate)
+                gl = ctx.strict_mse(gr, d["t"])
+                got = [gy, gz, gr, gb, gw, gl]
+            gf = None
+        except pcu_pkg.PcuExecutionError as e:
+            f = e.tensor_fault
+            gf = (f.node, f.element_index, f.reduction_index, int(f.step), int(f.kind))
+        assert gf == expect, (case, m, k, n, gf, expect)
+        if expect is None:
+            for node, (g, r) in enumerate(zip(got, outs)):
+                np.testing.assert_array_equal(_bits(np.asarray(g.numpy()).reshape(-1)),
+                                              _bits(np.asarray(r).reshape(-1)), err_msg=str((case, node)))
+
+
 def test_held_fault_read_and_reset(ctx, pcu_pkg):
     """pcu_fault_read returns the first fault of the most recent call, as that call
     reported it; a clean call clears it, and so does pcu_fault_reset."""
