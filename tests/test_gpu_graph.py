@@ -225,3 +225,34 @@ def test_prepared_graph_outliving_its_context(G, pcu_pkg):
         prep.execute(ptrs)  # refused before any pointer is used
     del prep
     gc.collect()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_c1_graph_random_shapes_and_faults_fuzz(G, pcu_pkg, dtype):
+    """Seeded fuzz of the prepared C1 training graph (forward, MSE, reverse mode, SGD) over
+    12 random shapes, with a special value planted in some inputs: the step's outputs, or
+    its first faulting node and coordinates, match the oracle's graph restatement."""
+    rng = np.random.default_rng(17 if dtype == np.float32 else 18)
+    info = np.finfo(dtype)
+    specials = np.array([np.nan, np.inf, info.max, info.tiny * dtype(0.5),
+                         info.smallest_subnormal], dtype=dtype)
+    step = G.c1_training_step(0.01)
+    for case in range(12):
+        m, k, n = (int(v) for v in rng.integers(1, 96, size=3))
+        x, w, b, y = (rng.uniform(-1, 1, s).astype(dtype) for s in ((m, k), (k, n), (m, n), (m, n)))
+        for arr in (x, w, b, y):
+            if rng.random() < 0.25:
+                arr.reshape(-1)[int(rng.integers(arr.size))] = rng.choice(specials)
+        ref = oracle.graph_c1_step(x, w, b, y, 0.01)
+        if ref["fault"] is None:
+            w2, b2, loss = step(x, w, b, y)
+            assert _bits(loss.numpy()).item() == _bits(ref["loss"]).item(), case
+            np.testing.assert_array_equal(_bits(w2.numpy()), _bits(ref["weights"]), err_msg=str(case))
+            np.testing.assert_array_equal(_bits(b2.numpy()), _bits(ref["bias"]), err_msg=str(case))
+        else:
+            with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                step(x, w, b, y)
+            tf, rf = exc.value.tensor_fault, ref["fault"]
+            assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                 rf.fault.kind), (case, m, k, n)
