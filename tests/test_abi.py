@@ -79,3 +79,34 @@ def test_opening_a_context_without_gpu_fails_loudly(pcu_pkg):
         pytest.skip("a GPU is present")
     with pytest.raises(pcu_pkg.PcuExecutionError):
         pcu_pkg.Context(0)
+
+
+def test_product_package_never_reaches_the_oracle():
+    """No CPU fallback: no module of the product package imports `oracle`, no native source
+    includes or loads anything from it, and importing the package with its graph front end
+    leaves `oracle` unimported (checked in a fresh interpreter)."""
+    import ast
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "fusion-pcu_amd")
+    for name in os.listdir(pkg):
+        if name.endswith(".py"):
+            tree = ast.parse(open(os.path.join(pkg, name)).read())
+            for node in ast.walk(tree):
+                if isinstance(node, ast.Import):
+                    assert not any(a.name.split(".")[0] == "oracle" for a in node.names), name
+                elif isinstance(node, ast.ImportFrom):
+                    assert (node.module or "").split(".")[0] != "oracle", name
+    csrc = os.path.join(pkg, "csrc")
+    for name in os.listdir(csrc):
+        text = open(os.path.join(csrc, name)).read()
+        assert "oracle/" not in text and "_ref/" not in text, name
+    probe = (
+        "import importlib.util, os, sys\n"
+        f"pkg = {pkg!r}\n"
+        "spec = importlib.util.spec_from_file_location('fusion_pcu_amd', os.path.join(pkg, '__init__.py'), "
+        "submodule_search_locations=[pkg])\n"
+        "m = importlib.util.module_from_spec(spec); sys.modules['fusion_pcu_amd'] = m; spec.loader.exec_module(m)\n"
+        "import fusion_pcu_amd.graph, fusion_pcu_amd.synthetic\n"
+        "assert not any(k == 'oracle' or k.startswith('oracle.') for k in sys.modules), 'oracle imported'\n")
+    subprocess.run([sys.executable, "-c", probe], check=True, cwd="/", timeout=120)
