@@ -110,6 +110,16 @@ def dtype_code(dtype) -> int:
         raise PcuExecutionError(_abi.PCU_ERR_UNSUPPORTED, f"unsupported scalar type {dtype}")
 
 
+def _require(what: str, x: "DeviceArray", shape, dtype) -> None:
+    """TensorError::ShapeMismatch / ScalarTypeMismatch before any pointer reaches the C ABI:
+    the kernels take one element count and raw pointers, so a smaller or narrower buffer
+    would be read or written past its end."""
+    if x.shape != tuple(shape) or x.dtype != np.dtype(dtype):
+        raise PcuExecutionError(
+            _abi.PCU_ERR_SHAPE,
+            f"ShapeMismatch: {what} is {x.shape} {x.dtype}, expected {tuple(shape)} {np.dtype(dtype)}")
+
+
 def _fault_from(f: _abi.Fault) -> CompoundFault:
     return CompoundFault(int(f.node), int(f.element_index), int(f.reduction_index),
                          TensorArithmeticStep(int(f.step)), PcuExecutionFaultKind(int(f.kind)))
@@ -300,16 +310,18 @@ class Context:
             raise PcuExecutionError(_abi.PCU_ERR_SHAPE, f"MatMulShape {a.shape} x {b.shape}")
         if out is None:
             out = self.empty((rows, cols), a.dtype)
+        _require("out", out, (rows, cols), a.dtype)
         self._call(self._lib.pcu_strict_matmul, dtype_code(a.dtype), rows, inner, cols,
                    int(transpose_left), int(transpose_right), a.ptr, b.ptr, out.ptr, int(policy))
         return out
 
     def checked_binary(self, op: int, a: DeviceArray, b, policy=0, out=None):
+        if isinstance(b, DeviceArray):
+            _require("right", b, a.shape, a.dtype)
         if out is None:
             out = self.empty(a.shape, a.dtype)
+        _require("out", out, a.shape, a.dtype)
         if isinstance(b, DeviceArray):
-            if b.shape != a.shape or b.dtype != a.dtype:
-                raise PcuExecutionError(_abi.PCU_ERR_SHAPE, f"ShapeMismatch {a.shape} {b.shape}")
             self._call(self._lib.pcu_checked_binary, dtype_code(a.dtype), op, a.size, a.ptr,
                        b.ptr, out.ptr, int(policy))
         else:
@@ -321,33 +333,42 @@ class Context:
     def checked_relu(self, x: DeviceArray, policy=0, out=None):
         if out is None:
             out = self.empty(x.shape, x.dtype)
+        _require("out", out, x.shape, x.dtype)
         self._call(self._lib.pcu_checked_relu, dtype_code(x.dtype), x.size, x.ptr, out.ptr, int(policy))
         return out
 
     def checked_relu_backward(self, x: DeviceArray, up: DeviceArray, policy=0, out=None):
+        _require("upstream", up, x.shape, x.dtype)
         if out is None:
             out = self.empty(x.shape, x.dtype)
+        _require("out", out, x.shape, x.dtype)
         self._call(self._lib.pcu_checked_relu_backward, dtype_code(x.dtype), x.size, x.ptr,
                    up.ptr, out.ptr, int(policy))
         return out
 
     def checked_add_relu(self, a: DeviceArray, b: DeviceArray, policy=0, out=None):
+        _require("right", b, a.shape, a.dtype)
         if out is None:
             out = self.empty(a.shape, a.dtype)
+        _require("out", out, a.shape, a.dtype)
         self._call(self._lib.pcu_checked_add_relu, dtype_code(a.dtype), a.size, a.ptr, b.ptr,
                    out.ptr, int(policy))
         return out
 
     def strict_sgd(self, w: DeviceArray, g: DeviceArray, learning_rate: float, policy=0, out=None):
+        _require("gradient", g, w.shape, w.dtype)
         if out is None:
             out = self.empty(w.shape, w.dtype)
+        _require("out", out, w.shape, w.dtype)
         self._call(self._lib.pcu_strict_sgd, dtype_code(w.dtype), w.size, w.ptr, g.ptr,
                    float(np.float32(learning_rate)), out.ptr, int(policy))
         return out
 
     def strict_mse(self, p: DeviceArray, t: DeviceArray, policy=0, out=None):
+        _require("target", t, p.shape, p.dtype)
         if out is None:
             out = self.empty((), p.dtype)
+        _require("out", out, (), p.dtype)
         self._call(self._lib.pcu_strict_mse, dtype_code(p.dtype), p.size, p.ptr, t.ptr,
                    out.ptr, int(policy))
         return out
@@ -365,22 +386,27 @@ class Context:
             raise PcuExecutionError(_abi.PCU_ERR_SHAPE, f"MatMulShape {a.shape} x {b.shape}")
         if out is None:
             out = self.empty((rows, cols), a.dtype)
+        _require("out", out, (rows, cols), a.dtype)
         self.check(self._lib.pcu_native_matmul(self.handle, dtype_code(a.dtype), rows, inner, cols,
                                                int(transpose_left), int(transpose_right), a.ptr,
                                                b.ptr, out.ptr))
         return out
 
     def native_mse(self, p: DeviceArray, t: DeviceArray, out=None):
+        _require("target", t, p.shape, p.dtype)
         if out is None:
             out = self.empty((), p.dtype)
+        _require("out", out, (), p.dtype)
         self.check(self._lib.pcu_native_mse(self.handle, dtype_code(p.dtype), p.size, p.ptr, t.ptr,
                                             out.ptr))
         return out
 
     def native_sgd(self, w: DeviceArray, g: DeviceArray, learning_rate: float, contracted=False,
                    out=None):
+        _require("gradient", g, w.shape, w.dtype)
         if out is None:
             out = self.empty(w.shape, w.dtype)
+        _require("out", out, w.shape, w.dtype)
         self.check(self._lib.pcu_native_sgd(self.handle, dtype_code(w.dtype), w.size, w.ptr, g.ptr,
                                             float(np.float32(learning_rate)), int(contracted),
                                             out.ptr))

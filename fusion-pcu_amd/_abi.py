@@ -123,6 +123,7 @@ SIGNATURES.update({
     "pcu_graph_set_numerical_mode": (_i32, [_vp, _i32]),
     "pcu_graph_input": (_i32, [_vp, _i32, _u32, _U64P, _U32P]),
     "pcu_graph_uniform": (_i32, [_vp, _i32, _u32, _U64P, _u64, _U32P]),
+    "pcu_graph_constant": (_i32, [_vp, _i32, _u32, _U64P, _vp, _U32P]),
     "pcu_graph_binary": (_i32, [_vp, _i32, _u32, _u32, _U32P]),
     "pcu_graph_relu": (_i32, [_vp, _u32, _U32P]),
     "pcu_graph_relu_backward": (_i32, [_vp, _u32, _u32, _U32P]),
@@ -148,7 +149,7 @@ SIGNATURES.update({
 })
 
 GRAPH_OPS = ["Input", "Uniform", "Add", "Sub", "Mul", "Div", "SgdUpdate", "MatMul", "Relu",
-             "ReluBackward", "MeanSquaredError"]
+             "ReluBackward", "MeanSquaredError", "Constant"]
 
 KERNEL_IDS = {
     "strict_gemm": 0, "gemm_prefilter": 1, "gemm_replay": 2, "sgd": 3, "binary": 4,

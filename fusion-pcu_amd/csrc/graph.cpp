@@ -95,6 +95,43 @@ pcu_status Graph::uniform(int dtype, const std::vector<uint64_t> &shape, uint64_
     return PCU_OK;
 }
 
+// Graph::constant_value / constant_typed (core/dialect/tensor.rs:3669-3679): an owned dense tensor constant,
+// a leaf of the graph like Input. Its elements are copied into the graph here and uploaded
+// once when a program that uses it is prepared.
+pcu_status Graph::constant(int dtype, const std::vector<uint64_t> &shape, const void *host_data,
+                           uint32_t *id)
+{
+    if (!is_float(dtype) || !id) {
+        error = "constant: unsupported scalar type";
+        return PCU_ERR_UNSUPPORTED;
+    }
+    if (shape_overflows(shape)) {
+        error = "constant: ShapeOverflow";
+        return PCU_ERR_SHAPE;
+    }
+    unsigned __int128 bytes = dtype == 0 ? 4 : 8;
+    for (uint64_t d : shape)
+        bytes *= d;
+    if (bytes > (unsigned __int128)(SIZE_MAX / 2)) {
+        error = "constant: ShapeOverflow";
+        return PCU_ERR_SHAPE;
+    }
+    if (bytes && !host_data) {
+        error = "constant: null data";
+        return PCU_ERR_ARGUMENT;
+    }
+    auto data = std::make_shared<std::vector<unsigned char>>((size_t)bytes);
+    if (bytes)
+        memcpy(data->data(), host_data, (size_t)bytes);
+    Node n;
+    n.op = Op::Constant;
+    n.shape = shape;
+    n.dtype = dtype;
+    n.data = std::move(data);
+    *id = push(n);
+    return PCU_OK;
+}
+
 // same_shape_binary (tensor.rs:4067-4110): equal shapes and scalar types.
 pcu_status Graph::binary(Op op, uint32_t a, uint32_t b, uint32_t *id)
 {
@@ -370,6 +407,7 @@ struct Backward {
         pcu_status st;
         switch (n.op) {
         case Op::Input:
+        case Op::Constant:
         case Op::Uniform:
             return PCU_OK;
         case Op::Add:
@@ -533,7 +571,7 @@ pcu_status Graph::backward(uint32_t loss, const std::vector<uint32_t> *targets,
         if (grad == UINT32_MAX)
             continue;
         Node src = nodes[i]; // copy: the vector grows while rules append
-        if (src.op == Op::Input || src.op == Op::Uniform)
+        if (src.op == Op::Input || src.op == Op::Constant || src.op == Op::Uniform)
             continue;
         if (src.op == Op::MeanSquaredError && loss_requested && (uint32_t)i == loss) {
             st = with_source_scope(*this, (uint32_t)i, [&] { return bw.mse_rule(src.a, src.b); });
@@ -606,11 +644,12 @@ void prepared_detach(Prepared *p)
                 (void)ctx->release(q);
                 q = nullptr;
             }
-    for (void *&q : p->dense_uniform)
-        if (q) {
-            (void)ctx->release(q);
-            q = nullptr;
-        }
+    for (auto *list : {&p->dense_uniform, &p->constant_buf})
+        for (void *&q : *list)
+            if (q) {
+                (void)ctx->release(q);
+                q = nullptr;
+            }
     auto &list = ctx->prepared;
     list.erase(std::remove(list.begin(), list.end(), p), list.end());
     p->ctx = nullptr;
@@ -637,6 +676,7 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
     fused_into.assign(n, -1);
     mse_side.assign(n, 0);
     dense_uniform.assign(n, nullptr);
+    constant_buf.assign(n, nullptr);
     for (uint32_t o : outputs)
         is_output[o] = 1;
     std::vector<uint32_t> uses(n, 0);
@@ -695,9 +735,19 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
         if (graph.nodes[i].op == Op::MeanSquaredError && uses[i] == 0 && route[i] == Route::Strict)
             mse_side[i] = 1;
     // Device storage: one buffer per computed node; outputs get two banks so a faulting
-    // execution never overwrites the published results.
+    // execution never overwrites the published results. A Constant is uploaded once here
+    // and stays resident for every execution (the reference allocates and uploads its
+    // constants with the plan's scratch: backends/rocm/tensor.rs:2955-2980).
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
+        if (nd.op == Op::Constant) {
+            const size_t bytes = nd.data ? nd.data->size() : 0;
+            if ((st = ctx->alloc(bytes, &constant_buf[i])))
+                return st;
+            if (bytes && (st = ctx->copy(constant_buf[i], nd.data->data(), bytes, true)))
+                return st;
+            continue;
+        }
         if (nd.op == Op::Input || nd.op == Op::Uniform || fused_into[i] >= 0)
             continue;
         size_t bytes = graph.elements(i) * dsize(nd.dtype);
@@ -720,6 +770,8 @@ void *Prepared::value_ptr(uint32_t id, const std::vector<const void *> &in, int 
     }
     if (nd.op == Op::Uniform)
         return dense_uniform[id];
+    if (nd.op == Op::Constant)
+        return constant_buf[id];
     return buf[is_output[id] ? bank : 0][id];
 }
 
@@ -765,7 +817,7 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     auto ptr = [&](uint32_t id) { return value_ptr(id, in, bank_w); };
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
-        if (nd.op == Op::Input || nd.op == Op::Uniform || fused_into[i] >= 0)
+        if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0)
             continue;
         uint64_t n = graph.elements(i);
         int policy = nd.policy < 0 ? 0 : nd.policy;
@@ -852,6 +904,10 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     // node wins (a node that the reference would never reach may also have faulted here).
     std::vector<pcu_fault> faults;
     st = ctx->end_program_all(&faults);
+    if (st == PCU_ERR_PROTOCOL && fault) {
+        *fault = ctx->protocol_fault;
+        fault->node = prog_to_graph[ctx->protocol_fault.node];
+    }
     if (st) {
         error = ctx->error;
         return st;
@@ -928,6 +984,15 @@ pcu_status pcu_graph_uniform(pcu_graph *gh, pcu_dtype dtype, uint32_t rank, cons
     if (!g || (rank && !shape))
         return PCU_ERR_ARGUMENT;
     return graph_fail(g, g->uniform(dtype, std::vector<uint64_t>(shape, shape + rank), value_bits, id));
+}
+
+pcu_status pcu_graph_constant(pcu_graph *gh, pcu_dtype dtype, uint32_t rank, const uint64_t *shape,
+                              const void *host_data, uint32_t *id)
+{
+    Graph *g = reinterpret_cast<Graph *>(gh);
+    if (!g || (rank && !shape))
+        return PCU_ERR_ARGUMENT;
+    return graph_fail(g, g->constant(dtype, std::vector<uint64_t>(shape, shape + rank), host_data, id));
 }
 
 pcu_status pcu_graph_binary(pcu_graph *gh, pcu_binary_op op, uint32_t a, uint32_t b, uint32_t *id)
@@ -1201,7 +1266,7 @@ pcu_status pcu_prepared_take_output(pcu_prepared *ph, uint32_t index, void **dev
     }
     uint32_t id = p->outputs[index];
     const pcu::Node &nd = p->graph.nodes[id];
-    if (nd.op == Op::Input || nd.op == Op::Uniform || p->fused_into[id] >= 0) {
+    if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || p->fused_into[id] >= 0) {
         p->ctx->fail("take_output: output %u is not computed by the program", index);
         return PCU_ERR_UNSUPPORTED;
     }

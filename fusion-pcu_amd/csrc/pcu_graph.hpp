@@ -5,6 +5,7 @@
 #include "pcu_runtime.hpp"
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -22,6 +23,7 @@ enum class Op : uint32_t {
     Relu = 8,
     ReluBackward = 9,
     MeanSquaredError = 10,
+    Constant = 11,
 };
 
 enum class Mode : int32_t { None = -1, Boundary = 0, Strict = 1 };
@@ -43,6 +45,9 @@ struct Node {
     bool tl = false, tr = false;             // MatMul transposes
     float lr = 0.0f;                         // SgdUpdate rate
     uint64_t value_bits = 0;                 // Uniform value (dtype-sized bit pattern)
+    // Constant payload: the dense row-major elements, owned by the graph (shared by the
+    // copies a prepared program keeps).
+    std::shared_ptr<const std::vector<unsigned char>> data;
     std::vector<uint64_t> shape;
     int dtype = 0;                           // 0 f32, 1 f64
     Mode mode = Mode::None;                  // numerical mode (MatMul/MSE/SGD/ReluBackward)
@@ -62,6 +67,8 @@ struct Graph {
 
     pcu_status input(int dtype, const std::vector<uint64_t> &shape, uint32_t *id);
     pcu_status uniform(int dtype, const std::vector<uint64_t> &shape, uint64_t bits, uint32_t *id);
+    pcu_status constant(int dtype, const std::vector<uint64_t> &shape, const void *host_data,
+                        uint32_t *id);
     pcu_status binary(Op op, uint32_t a, uint32_t b, uint32_t *id);
     pcu_status relu(uint32_t x, uint32_t *id);
     pcu_status relu_backward(uint32_t x, uint32_t up, uint32_t *id);
@@ -88,6 +95,7 @@ struct Prepared {
     std::vector<int> mse_side;      // MSE runs on the side stream
     std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
+    std::vector<void *> constant_buf; // resident copy of each planned Constant, uploaded at build
     int bank = 0;                   // bank written by the next execution
     bool published = false;
     std::vector<void *> published_ptr;

@@ -51,6 +51,7 @@ struct Ctx {
     bool implicit_program = false;
     bool words_pending = false;
     pcu_fault held_fault{};      // first fault of the most recent program
+    pcu_fault protocol_fault{};  // node and raw word of the last malformed fault status
     bool has_held_fault = false; // the open program's fault words and gate await their reset
     std::vector<NodeInfo> nodes;
     std::string error;

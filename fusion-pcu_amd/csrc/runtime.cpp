@@ -396,6 +396,12 @@ pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
         memset(&f, 0, sizeof f);
         if (!decode_word(nodes[i], w, &f)) {
             fail("malformed fault word 0x%016llx at node %zu", (unsigned long long)w, i);
+            // The raw word travels back as (ordinal << 3) | kind for the caller's
+            // InvalidExecutionFaultWord(word) (backends/rocm/owned_dispatch.rs:95).
+            memset(&protocol_fault, 0, sizeof protocol_fault);
+            protocol_fault.node = (uint32_t)i;
+            protocol_fault.kind = (uint32_t)(w & 7);
+            protocol_fault.ordinal = w >> 3;
             return PCU_ERR_PROTOCOL;
         }
         f.node = (uint32_t)i;
@@ -411,6 +417,8 @@ pcu_status Ctx::end_program(pcu_fault *first)
 {
     std::vector<pcu_fault> faults;
     pcu_status st = end_program_all(&faults);
+    if (st == PCU_ERR_PROTOCOL && first)
+        *first = protocol_fault;
     if (st)
         return st;
     if (faults.empty())
@@ -527,12 +535,43 @@ static bool valid_dtype(int d) { return d == PCU_F32 || d == PCU_F64; }
 static bool valid_policy(int p) { return p >= 0 && p <= 2; }
 static size_t dsize(int d) { return d == PCU_F32 ? 4 : 8; }
 
+// [p, p + pb) and [q, q + qb) share a byte.
+static bool ranges_overlap(const void *p, uint64_t pb, const void *q, uint64_t qb)
+{
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return p && q && pb && qb && a < b + qb && b < a + pb;
+}
+
+// Elementwise kernels read element i of each operand and then write element i of out, so
+// an out that is exactly an operand (an in-place update) is safe; any other overlap lets a
+// lane overwrite an element another lane has yet to read.
+static bool partial_overlap(const void *out, const void *in, uint64_t bytes)
+{
+    return out != in && ranges_overlap(out, bytes, in, bytes);
+}
+
+// A MatMul reads every operand element many times, from many workgroups, while others
+// write the output (and the replay re-reads the operands after the output is written), so
+// the output may share no byte with either operand. The reference cannot meet this case:
+// its outputs are always fresh owners.
+static bool matmul_out_overlaps(int dtype, uint64_t rows, uint64_t inner, uint64_t cols,
+                                const void *a, const void *b, const void *c)
+{
+    const uint64_t ds = dsize(dtype);
+    return ranges_overlap(c, rows * cols * ds, a, rows * inner * ds) ||
+           ranges_overlap(c, rows * cols * ds, b, inner * cols * ds);
+}
+
 pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
                           int tr, const void *a, const void *b, void *c, int policy)
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || !c || ((rows * inner) && !a) ||
         ((inner * cols) && !b)) {
         fail("strict_matmul: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (matmul_out_overlaps(dtype, rows, inner, cols, a, b, c)) {
+        fail("strict_matmul: the output overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
     unsigned long long *word;
@@ -586,6 +625,10 @@ pcu_status Ctx::op_binary(int dtype, int op, uint64_t n, const void *a, const vo
         fail("checked_binary: invalid argument");
         return PCU_ERR_ARGUMENT;
     }
+    if (partial_overlap(out, a, n * dsize(dtype)) || partial_overlap(out, b, n * dsize(dtype))) {
+        fail("checked_binary: the output partly overlaps an operand");
+        return PCU_ERR_ARGUMENT;
+    }
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
@@ -602,6 +645,10 @@ pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int pol
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!x || !out))) {
         fail("checked_relu: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (partial_overlap(out, x, n * dsize(dtype))) {
+        fail("checked_relu: the output partly overlaps the input");
         return PCU_ERR_ARGUMENT;
     }
     unsigned long long *word;
@@ -623,6 +670,10 @@ pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const voi
         fail("checked_relu_backward: invalid argument");
         return PCU_ERR_ARGUMENT;
     }
+    if (partial_overlap(out, x, n * dsize(dtype)) || partial_overlap(out, up, n * dsize(dtype))) {
+        fail("checked_relu_backward: the output partly overlaps an operand");
+        return PCU_ERR_ARGUMENT;
+    }
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
     if (st)
@@ -641,6 +692,10 @@ pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!a || !out || (!b && !b_value)))) {
         fail("checked_add_relu: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (partial_overlap(out, a, n * dsize(dtype)) || partial_overlap(out, b, n * dsize(dtype))) {
+        fail("checked_add_relu: the output partly overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
     unsigned long long *w_add, *w_relu;
@@ -665,6 +720,10 @@ pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, floa
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!w || !g || !out))) {
         fail("strict_sgd: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (partial_overlap(out, w, n * dsize(dtype)) || partial_overlap(out, g, n * dsize(dtype))) {
+        fail("strict_sgd: the output partly overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
     uint32_t rb;
@@ -718,6 +777,11 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
         fail("strict_mse: invalid argument");
         return PCU_ERR_ARGUMENT;
     }
+    if (ranges_overlap(out, dsize(dtype), p, n * dsize(dtype)) ||
+        ranges_overlap(out, dsize(dtype), t, n * dsize(dtype))) {
+        fail("strict_mse: the output overlaps an operand");
+        return PCU_ERR_ARGUMENT;
+    }
     if (n == 0) {
         fail("strict_mse: empty input (TensorError::ShapeMismatch)");
         return PCU_ERR_SHAPE;
@@ -766,6 +830,10 @@ pcu_status Ctx::op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint6
         fail("native_matmul: invalid argument");
         return PCU_ERR_ARGUMENT;
     }
+    if (matmul_out_overlaps(dtype, rows, inner, cols, a, b, c)) {
+        fail("native_matmul: the output overlaps an operand");
+        return PCU_ERR_ARGUMENT;
+    }
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Native, rows * cols, inner}, &word);
     if (st)
@@ -786,6 +854,10 @@ pcu_status Ctx::op_native_sgd(int dtype, uint64_t n, const void *w, const void *
 {
     if (!valid_dtype(dtype) || (n && (!w || !g || !out))) {
         fail("native_sgd: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (partial_overlap(out, w, n * dsize(dtype)) || partial_overlap(out, g, n * dsize(dtype))) {
+        fail("native_sgd: the output partly overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
     uint32_t rb;
@@ -811,6 +883,11 @@ pcu_status Ctx::op_native_mse(int dtype, uint64_t n, const void *p, const void *
 {
     if (!valid_dtype(dtype) || !p || !t || !out) {
         fail("native_mse: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    if (ranges_overlap(out, dsize(dtype), p, n * dsize(dtype)) ||
+        ranges_overlap(out, dsize(dtype), t, n * dsize(dtype))) {
+        fail("native_mse: the output overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
     if (n == 0) {

@@ -96,6 +96,15 @@ class Graph:
         bits = int(np.array(value, dtype=dt).view(np.uint32 if dt == np.float32 else np.uint64))
         return self._id(self._lib.pcu_graph_uniform, dtype_code(dt), r, s, bits)
 
+    def constant(self, array) -> int:
+        """Graph::constant_value (core/dialect/tensor.rs:3669-3679): the array's elements
+        are copied into the graph; a prepared program uploads them once."""
+        src = np.asarray(array)
+        arr = np.ascontiguousarray(src).reshape(src.shape)  # keeps rank 0
+        r, s = self._shape(arr.shape)
+        return self._id(self._lib.pcu_graph_constant, dtype_code(arr.dtype), r, s,
+                        arr.ctypes.data_as(ctypes.c_void_p))
+
     def binary(self, op: int, a: int, b: int) -> int:
         return self._id(self._lib.pcu_graph_binary, op, a, b)
 
@@ -318,8 +327,6 @@ class _Capture:
         if options:
             self.graph.set_numerical_options(**options)
         self.policy = policy
-        self.constants: List[np.ndarray] = []
-        self.constant_nodes: List[int] = []
         self.gradient_sets: Dict[int, Dict[int, int]] = {}
 
     def value(self, node: int) -> CaptureValue:
@@ -411,12 +418,11 @@ def identity(x) -> CaptureValue:
 
 
 def constant(array) -> CaptureValue:
-    """pcu::constant: a captured constant, uploaded once and kept resident."""
+    """pcu::constant: a Constant graph node (OpDescriptor::Constant), uploaded once when the
+    function is prepared and kept resident for every call."""
     cap = _cap()
-    arr = np.ascontiguousarray(array)
-    node = cap.graph.input(arr.shape, arr.dtype)
-    cap.constants.append(arr)
-    cap.constant_nodes.append(node)
+    arr = np.asarray(array)
+    node = cap.graph.constant(arr)
     return CaptureValue(cap, node, arr.shape, arr.dtype)
 
 
@@ -424,12 +430,10 @@ def constant(array) -> CaptureValue:
 
 
 class _Entry:
-    def __init__(self, ctx: Context, prepared: Prepared, arg_nodes: List[int],
-                 constants: List[Tuple[int, DeviceArray]], single: bool):
+    def __init__(self, ctx: Context, prepared: Prepared, arg_nodes: List[int], single: bool):
         self.ctx = ctx
         self.prepared = prepared
         self.arg_nodes = arg_nodes
-        self.constants = constants
         self.single = single
 
     def call(self, args):
@@ -445,8 +449,6 @@ class _Entry:
                     d = self.ctx.upload(np.ascontiguousarray(a))
                     staged.append(d)
                     by_node[node] = d.ptr
-            for node, d in self.constants:
-                by_node[node] = d.ptr
             ptrs = [by_node[n] for n in self.prepared.input_ids]
             self.prepared.execute(ptrs)
             outs = tuple(self.prepared.take_output(i) for i in range(len(self.prepared.outputs)))
@@ -508,8 +510,7 @@ def _capture(fn, args, strict: bool, policy: int, ctx: Context,
     results = (result,) if single else result
     outs = [_v_in(cap, r).node for r in results]
     prepared = cap.graph.prepare(ctx, outs)
-    consts = [(n, ctx.upload(a)) for n, a in zip(cap.constant_nodes, cap.constants)]
-    return _Entry(ctx, prepared, [v.node for v in vals], consts, single)
+    return _Entry(ctx, prepared, [v.node for v in vals], single)
 
 
 def _v_in(cap, x) -> CaptureValue:

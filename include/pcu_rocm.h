@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define PCU_ROCM_ABI_VERSION 2
+#define PCU_ROCM_ABI_VERSION 3
 
 typedef struct pcu_ctx pcu_ctx;
 
@@ -48,7 +48,10 @@ typedef enum pcu_status {
     PCU_ERR_DEVICE = 5,        /* HIP runtime error (message in pcu_last_error) */
     PCU_ERR_OUT_OF_MEMORY = 6,
     PCU_ERR_STATE = 7,         /* call not allowed in the context's current mode */
-    PCU_ERR_PROTOCOL = 8       /* malformed device fault status (owned_dispatch.rs:127-141) */
+    PCU_ERR_PROTOCOL = 8       /* malformed device fault status (owned_dispatch.rs:76-141); when
+                                * the call takes a pcu_fault*, it holds the node and the raw
+                                * word as (ordinal << 3) | kind, for the reference's
+                                * HipError::InvalidExecutionFaultWord(word) */
 } pcu_status;
 
 typedef enum pcu_dtype { PCU_F32 = 0, PCU_F64 = 1 } pcu_dtype;
@@ -142,11 +145,15 @@ pcu_status pcu_download(pcu_ctx *ctx, void *host_dst, const void *device_src, si
  * (`fault` may be NULL). Inside program mode the call only enqueues; faults are reported
  * by pcu_program_end. On a fault the output's contents are unspecified and must not be
  * published (the reference never publishes a faulting node's output:
- * backends/cpu/prepared_tensor/prepared_tensor.rs:258-310). */
+ * backends/cpu/prepared_tensor/prepared_tensor.rs:258-310). The elementwise and SGD calls
+ * accept an `out` equal to one of their operands (in place); an `out` that overlaps an
+ * operand any other way is rejected with PCU_ERR_ARGUMENT. */
 
 /* out[rows x cols] = op(left) * op(right); op(X) = X^T when the flag is set. Stored
  * shapes: left rows x inner (inner x rows if transposed), right inner x cols (cols x
- * inner if transposed). Ordered k, separately rounded multiply then add, from +0. */
+ * inner if transposed). Ordered k, separately rounded multiply then add, from +0.
+ * `out` must not share any byte with `left` or `right` (PCU_ERR_ARGUMENT otherwise; the
+ * same holds for pcu_native_matmul and, for the one output element, the MSE calls). */
 pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
                              uint64_t cols, int transpose_left, int transpose_right,
                              const void *left, const void *right, void *out,
@@ -274,7 +281,8 @@ typedef enum pcu_graph_op {
     PCU_GRAPH_MATMUL = 7,
     PCU_GRAPH_RELU = 8,
     PCU_GRAPH_RELU_BACKWARD = 9,
-    PCU_GRAPH_MEAN_SQUARED_ERROR = 10
+    PCU_GRAPH_MEAN_SQUARED_ERROR = 10,
+    PCU_GRAPH_CONSTANT = 11
 } pcu_graph_op;
 
 /* PcuNumericalOptions (core/numerical/numerical.rs:21-78): independent compound-arithmetic,
@@ -319,6 +327,13 @@ pcu_status pcu_graph_input(pcu_graph *graph, pcu_dtype dtype, uint32_t rank, con
  * unless a consumer needs it dense. */
 pcu_status pcu_graph_uniform(pcu_graph *graph, pcu_dtype dtype, uint32_t rank,
                              const uint64_t *shape, uint64_t value_bits, uint32_t *id);
+/* An owned dense tensor constant (OpDescriptor::Constant, core/dialect/tensor.rs:377; built
+ * by Graph::constant_value / constant_typed, :3669-3679): `host_data` holds the product of
+ * `shape` elements of `dtype`, row-major, and is copied into the graph by this call. A
+ * program that uses the node uploads it once at pcu_prepare and keeps it resident for every
+ * execution. It is a leaf: it takes no derivative and is not a prepared input. */
+pcu_status pcu_graph_constant(pcu_graph *graph, pcu_dtype dtype, uint32_t rank,
+                              const uint64_t *shape, const void *host_data, uint32_t *id);
 pcu_status pcu_graph_binary(pcu_graph *graph, pcu_binary_op op, uint32_t left, uint32_t right,
                             uint32_t *id);
 pcu_status pcu_graph_relu(pcu_graph *graph, uint32_t input, uint32_t *id);

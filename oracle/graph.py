@@ -66,6 +66,11 @@ class Graph:
     def uniform(self, shape, dtype, value) -> int:
         return self.push("Uniform", (), shape, dtype, value=np.array(value, dtype=dtype))
 
+    def constant(self, array) -> int:
+        """Graph::constant_value (core/dialect/tensor.rs:3669-3679): a dense leaf."""
+        arr = np.array(array, copy=True)
+        return self.push("Constant", (), arr.shape, arr.dtype, value=arr)
+
     def _same(self, a, b):
         if self.nodes[a].shape != self.nodes[b].shape or self.nodes[a].dtype != self.nodes[b].dtype:
             raise ValueError("ShapeMismatch")
@@ -153,7 +158,7 @@ class Graph:
     def _rule(self, grads, i, g, needed):
         """append_node_gradients (gradients.rs:31-137) and append_matmul_gradients (:203-239)."""
         n = self.nodes[i]
-        if n.op in ("Input", "Uniform"):
+        if n.op in ("Input", "Constant", "Uniform"):
             return
         if n.op == "Add":
             a, b = n.operands
@@ -282,6 +287,8 @@ class Graph:
             ops = [vals.get(o) for o in n.operands]
             if n.op == "Input":
                 v, f = np.ascontiguousarray(inputs[i], dtype=n.dtype).reshape(n.shape), None
+            elif n.op == "Constant":
+                v, f = n.params["value"].reshape(n.shape), None
             elif n.op == "Uniform":
                 v, f = np.full(n.shape, n.params["value"], dtype=n.dtype), None
             elif n.op in ("Add", "Sub", "Mul", "Div"):

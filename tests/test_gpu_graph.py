@@ -256,3 +256,91 @@ def test_c1_graph_random_shapes_and_faults_fuzz(G, pcu_pkg, dtype):
             assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
                 (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
                  rf.fault.kind), (case, m, k, n)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_constant_node_graph_parity(G, pcu_pkg, dtype):
+    """OpDescriptor::Constant (core/dialect/tensor.rs:377): relu(X @ W + C) with C a graph
+    constant, MSE vs Y, gradients for W and C, SGD on W. C is uploaded once at prepare and
+    is not a prepared input; three executions with W fed back are bit-exact against the
+    oracle's graph. A NaN in a second graph's constant faults at the Add, at the oracle's
+    element."""
+    from fusion_pcu_amd import synthetic as syn
+    x = syn.uniform(61, (32, 48), dtype)
+    w0 = syn.uniform(62, (48, 24), dtype)
+    c = syn.uniform(63, (32, 24), dtype)
+    y = syn.uniform(64, (32, 24), dtype)
+
+    def build(g, cval):
+        xi, wi = g.input(x.shape, dtype), g.input(w0.shape, dtype)
+        k = g.constant(cval)
+        yi = g.input(y.shape, dtype)
+        loss = g.mean_squared_error(g.relu(g.add(g.matmul(xi, wi), k)), yi)
+        gw, gk = g.backward_mse_for_targets(loss, [wi, k])
+        return xi, wi, yi, [g.sgd_update(wi, gw, 0.01), gk, loss]
+
+    ctx = G.default_context()
+    g = G.Graph()
+    g.set_numerical_mode(True)
+    xi, wi, yi, outs = build(g, c)
+    prep = g.prepare(ctx, outs)
+    assert sorted(prep.input_ids) == sorted([xi, wi, yi])
+    r = og.Graph()
+    r.mode = "Strict"
+    rxi, rwi, ryi, routs = build(r, c)
+    dx, dy = ctx.upload(x), ctx.upload(y)
+    w_dev, w_ref = ctx.upload(w0), w0
+    for it in range(3):
+        by_id = {xi: dx.ptr, wi: w_dev.ptr, yi: dy.ptr}
+        prep.execute([by_id[i] for i in prep.input_ids])
+        vals, fault = r.evaluate({rxi: x, rwi: w_ref, ryi: y}, routs)
+        assert fault is None
+        got = [prep.take_output(k).numpy() for k in range(3)]
+        for have, want in zip(got, [vals[o] for o in routs]):
+            np.testing.assert_array_equal(_bits(have), _bits(want), err_msg=f"step {it}")
+        w_ref = vals[routs[0]]
+        w_dev = ctx.upload(got[0])
+
+    bad = c.copy()
+    bad[5, 7] = np.nan
+    g2 = G.Graph()
+    g2.set_numerical_mode(True)
+    xi2, wi2, yi2, outs2 = build(g2, bad)
+    prep2 = g2.prepare(ctx, outs2)
+    r2 = og.Graph()
+    r2.mode = "Strict"
+    rx2, rw2, ry2, routs2 = build(r2, bad)
+    _, rfault = r2.evaluate({rx2: x, rw2: w0, ry2: y}, routs2)
+    by_id = {xi2: dx.ptr, wi2: ctx.upload(w0).ptr, yi2: dy.ptr}
+    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+        prep2.execute([by_id[i] for i in prep2.input_ids])
+    tf = exc.value.tensor_fault
+    assert rfault is not None and tf.node == rfault.node
+    assert (tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+        (rfault.fault.element_index, rfault.fault.reduction_index, rfault.fault.step,
+         rfault.fault.kind) == (5 * 24 + 7, 0, 0, 5)
+
+
+def test_constant_through_the_facade(G):
+    """pcu::constant inside a strict function: the constant is a graph node of the
+    captured program (not an extra call argument), and repeated calls reuse it."""
+    rng = np.random.default_rng(3)
+    bias = rng.uniform(-1, 1, (16, 8)).astype(np.float32)
+
+    @G.function(strict=True)
+    def affine(inp, weights):
+        return G.relu(G.matmul(inp, weights) + G.constant(bias))
+
+    x = rng.uniform(-1, 1, (16, 32)).astype(np.float32)
+    w = rng.uniform(-1, 1, (32, 8)).astype(np.float32)
+    for _ in range(2):
+        got = affine(x, w).numpy()
+    entry = next(iter(affine.cache.values()))
+    assert len(entry.prepared.input_ids) == 2
+    assert any(entry.prepared.graph.describe(i)["op"] == "Constant"
+               for i in range(entry.prepared.graph.node_count()))
+    mm, f1 = oracle.matmul(x, w)
+    s, f2 = oracle.binary(oracle.OP_ADD, mm.reshape(-1), bias.reshape(-1))
+    want, f3 = oracle.relu(s)
+    assert f1 is None and f2 is None and f3 is None
+    np.testing.assert_array_equal(_bits(got).reshape(-1), _bits(want))

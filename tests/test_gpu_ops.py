@@ -669,3 +669,46 @@ def test_program_stage_gate_skips_nodes_after_a_fault(ctx, pcu_pkg, engine_name)
         np.testing.assert_array_equal(_bits(out2.numpy()), _bits(ref))
     finally:
         ctx.set_matmul_engine("auto")
+
+
+# ------------------------------------------------------------ output aliasing
+
+
+def test_output_overlapping_an_operand_is_rejected(ctx, pcu_pkg):
+    """A MatMul output may share no byte with an operand; an elementwise or SGD output may
+    be exactly an operand (in place) but may not overlap one any other way. Rejections are
+    PCU_ERR_ARGUMENT from the C ABI, before any kernel runs; the in-place forms are
+    bit-exact."""
+    import ctypes
+    from fusion_pcu_amd import _abi
+    lib = pcu_pkg.lib()
+    rng = np.random.default_rng(17)
+    a = rng.uniform(-1, 1, (64, 64)).astype(np.float32)
+    big = ctx.upload(np.concatenate([a.reshape(-1), a.reshape(-1)]))
+    base = big.ptr
+    f = _abi.Fault()
+    st = lib.pcu_strict_matmul(ctx.handle, 0, 64, 64, 64, 0, 0, base, base + 64 * 64 * 4,
+                               base + 4 * 64, 0, ctypes.byref(f))
+    assert st == _abi.PCU_ERR_ARGUMENT, st
+    assert "overlap" in ctx.error_text()
+    st = lib.pcu_native_matmul(ctx.handle, 0, 64, 64, 64, 0, 0, base, base, base + 64 * 64 * 4 * 2 - 4)
+    assert st == _abi.PCU_ERR_ARGUMENT
+    st = lib.pcu_checked_relu(ctx.handle, 0, 64 * 64, base, base + 16, 0, ctypes.byref(f))
+    assert st == _abi.PCU_ERR_ARGUMENT
+    st = lib.pcu_strict_sgd(ctx.handle, 0, 64 * 64, base, base + 64 * 64 * 4, ctypes.c_float(0.01),
+                            base + 64 * 64 * 4 - 64, 0, ctypes.byref(f))
+    assert st == _abi.PCU_ERR_ARGUMENT
+    st = lib.pcu_strict_mse(ctx.handle, 0, 64 * 64, base, base + 64 * 64 * 4, base + 8, 0,
+                            ctypes.byref(f))
+    assert st == _abi.PCU_ERR_ARGUMENT
+    # In place: SGD into its own weights, ReLU into its own input.
+    g = rng.uniform(-1e-3, 1e-3, 64 * 64).astype(np.float32)
+    dw, dg = ctx.upload(a.reshape(-1)), ctx.upload(g)
+    ctx.strict_sgd(dw, dg, 0.01, out=dw)
+    want, wf = oracle.sgd(a.reshape(-1), g, 0.01)
+    assert wf is None
+    np.testing.assert_array_equal(_bits(dw.numpy()), _bits(want))
+    ctx.checked_relu(dw, out=dw)
+    want2, wf2 = oracle.relu(want)
+    assert wf2 is None
+    np.testing.assert_array_equal(_bits(dw.numpy()), _bits(want2))

@@ -207,3 +207,86 @@ def test_set_value_numerical_mode_rejects_scalar_nodes(G, pcu_pkg):
     m = g.mean_squared_error(r, y)
     g.set_value_numerical_mode(m, True)
     assert g.describe(m)["numerical_mode"] == "Strict"
+
+
+def _constant_pair(G, dtype, targets_include_constant):
+    """relu(X @ W + C) with C a Constant (OpDescriptor::Constant) -> MSE vs Y -> gradients
+    -> SGD on W, built on the C++ graph and on the oracle's restatement."""
+    rng = np.random.default_rng(7)
+    c = rng.uniform(-1, 1, (8, 4)).astype(dtype)
+    ids = {}
+    p, o = G.Graph(), og.Graph()
+    for g, key in ((p, "p"), (o, "o")):
+        g.set_numerical_mode(True) if key == "p" else setattr(g, "mode", "Strict")
+        x = g.input((8, 16), dtype)
+        w = g.input((16, 4), dtype)
+        k = g.constant(c)
+        y = g.input((8, 4), dtype)
+        loss = g.mean_squared_error(g.relu(g.add(g.matmul(x, w), k)), y)
+        targets = [w, k] if targets_include_constant else [w]
+        grads = g.backward_mse_for_targets(loss, targets)
+        ids[key] = {"x": x, "w": w, "k": k, "y": y, "loss": loss, "grads": grads,
+                    "upd": g.sgd_update(w, grads[0], 0.01)}
+    return p, o, ids, c
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("with_constant_target", [False, True])
+def test_constant_node_graph_matches_oracle(G, dtype, with_constant_target):
+    p, o, ids, _ = _constant_pair(G, dtype, with_constant_target)
+    assert _seq_product(p) == _seq_oracle(o)
+    k = ids["p"]["k"]
+    d = p.describe(k)
+    assert d["op"] == "Constant" and d["shape"] == (8, 4) and d["dtype"] == np.dtype(dtype)
+    assert d["numerical_mode"] is None and d["underflow_policy"] is None
+    assert d["left"] is None and d["right"] is None
+    outs = [ids["p"]["upd"], ids["p"]["loss"]]
+    assert p.plan(outs) == o.plan([ids["o"]["upd"], ids["o"]["loss"]])
+    assert k in p.plan(outs)
+    # A constant is a leaf: the reverse pass appends nothing that reads a derivative of it.
+    for i in range(p.node_count()):
+        dd = p.describe(i)
+        assert not (dd["op"] not in ("Add", "MatMul", "Relu", "MeanSquaredError") and k in
+                    (dd["left"], dd["right"]) and i > ids["p"]["loss"])
+    if with_constant_target:
+        # The constant's gradient is the cotangent its Add consumer passes on, as for an Input.
+        assert ids["p"]["grads"][1] is not None
+
+
+def test_constant_builder_errors(G, pcu_pkg):
+    import ctypes
+    from fusion_pcu_amd import _abi
+    lib = pcu_pkg.lib()
+    g = G.Graph()
+    shape = (ctypes.c_uint64 * 2)(2, 3)
+    out = ctypes.c_uint32()
+    # Non-empty constant without data.
+    assert lib.pcu_graph_constant(g.handle, _abi.PCU_F32, 2, shape, None, ctypes.byref(out)) == \
+        _abi.PCU_ERR_ARGUMENT
+    # Unsupported scalar type code.
+    data = np.zeros(6, np.float32)
+    assert lib.pcu_graph_constant(g.handle, 7, 2, shape, data.ctypes.data_as(ctypes.c_void_p),
+                                  ctypes.byref(out)) == _abi.PCU_ERR_UNSUPPORTED
+    # A shape whose element count overflows.
+    big = (ctypes.c_uint64 * 2)(1 << 40, 1 << 40)
+    assert lib.pcu_graph_constant(g.handle, _abi.PCU_F32, 2, big, data.ctypes.data_as(ctypes.c_void_p),
+                                  ctypes.byref(out)) == _abi.PCU_ERR_SHAPE
+    # An empty constant needs no data; a scalar (rank 0) holds one element.
+    zero = (ctypes.c_uint64 * 1)(0)
+    assert lib.pcu_graph_constant(g.handle, _abi.PCU_F64, 1, zero, None, ctypes.byref(out)) == _abi.PCU_OK
+    k = g.constant(np.float32(2.5))
+    assert g.describe(k)["shape"] == () and g.describe(k)["op"] == "Constant"
+    # Shape rules of its consumers apply as for any other value.
+    a = g.input((2, 3), np.float32)
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        g.add(a, k)
+
+
+def test_constant_data_is_copied_at_append(G):
+    """The graph owns its copy: changing the caller's array afterwards changes nothing
+    (checked through the oracle's restatement, which also copies)."""
+    arr = np.arange(6, dtype=np.float32).reshape(2, 3)
+    o = og.Graph()
+    k = o.constant(arr)
+    arr[:] = -1
+    assert o.nodes[k].params["value"].tolist() == [[0, 1, 2], [3, 4, 5]]
