@@ -65,6 +65,7 @@ SIGNATURES = {
     "pcu_upload": (_i32, [_vp, _vp, _vp, _sz]),
     "pcu_download": (_i32, [_vp, _vp, _vp, _sz]),
     "pcu_strict_matmul": (_i32, [_vp, _i32, _u64, _u64, _u64, _i32, _i32, _vp, _vp, _vp, _i32, _FP]),
+    "pcu_strict_matmul_noalloc": (_i32, [_vp, _i32, _u64, _u64, _u64, _i32, _i32, _vp, _vp, _vp, _i32, _FP]),
     "pcu_checked_binary": (_i32, [_vp, _i32, _i32, _u64, _vp, _vp, _vp, _i32, _FP]),
     "pcu_checked_binary_uniform": (_i32, [_vp, _i32, _i32, _u64, _vp, _u64, _vp, _i32, _FP]),
     "pcu_checked_relu": (_i32, [_vp, _i32, _u64, _vp, _vp, _i32, _FP]),

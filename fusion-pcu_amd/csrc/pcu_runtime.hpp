@@ -117,6 +117,8 @@ struct Ctx {
 
     pcu_status open_words();
     pcu_status begin_program(bool implicit);
+    pcu_status read_words(size_t *used);
+    pcu_status decode_node(size_t i, pcu_fault *f);
     pcu_status end_program(pcu_fault *first);
     // Every faulted node in node order (empty when none).
     pcu_status end_program_all(std::vector<pcu_fault> *faults);
@@ -130,8 +132,10 @@ struct Ctx {
     pcu_status start_op();
     pcu_status finish_op(pcu_status launched, pcu_fault *fault);
 
+    // noalloc: the screen's scratch is the library's fixed per-device array
+    // (pcu_strict_matmul_noalloc), so the call allocates nothing.
     pcu_status op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl, int tr,
-                         const void *a, const void *b, void *c, int policy);
+                         const void *a, const void *b, void *c, int policy, bool noalloc = false);
     pcu_status op_binary(int dtype, int op, uint64_t n, const void *a, const void *b,
                          const void *b_value, void *out, int policy);
     pcu_status op_relu(int dtype, uint64_t n, const void *x, void *out, int policy);

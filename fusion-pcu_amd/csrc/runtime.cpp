@@ -13,8 +13,48 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <unordered_set>
+
+// ------------------------------------------- scratch of the no-allocation strict MatMul
+// pcu_strict_matmul_noalloc keeps the exponent screen's words (one per row of op(A) and one
+// per column of op(B), then the first-suspect word) in this array instead of the context's
+// pool, so that call allocates nothing. Its size is matmul_scratch_bytes(rows, cols) at the
+// largest admitted shape: 8 * 65536 bytes of row words, the same of column words, and 256
+// bytes, i.e. 1 MiB + 256 B, which each device keeps until the process ends. In host code
+// `scratch` is a host-side stand-in: only the address hipGetSymbolAddress returns for the
+// current device (kept per device in g_noalloc) may reach a kernel, a fill or a copy.
+static constexpr size_t kNoAllocScratchWords = 2 * (size_t)PCU_NOALLOC_MAX_DIM + 32;
+static __device__ __align__(256) unsigned long long scratch[kNoAllocScratchWords];
+
+namespace {
+constexpr int kNoAllocDevices = 64;
+struct NoAllocDevice {
+    void *ptr = nullptr;  // this device's address of `scratch`
+    bool cleared = false; // its words were zeroed by a fill kernel
+    uint32_t gen = 0;     // generation of the latest screen written to it
+};
+std::mutex g_noalloc_mu;
+NoAllocDevice g_noalloc[kNoAllocDevices];
+} // namespace
+
+// Set-up, once per device, with `device` current: the device's address of `scratch`.
+static hipError_t noalloc_setup(int device)
+{
+    if (device < 0 || device >= kNoAllocDevices)
+        return hipSuccess; // pcu_strict_matmul_noalloc refuses such a device
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoAllocDevice &d = g_noalloc[device];
+    if (d.ptr)
+        return hipSuccess;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+        return e;
+    d.ptr = p;
+    return hipSuccess;
+}
 
 namespace pcu {
 
@@ -90,7 +130,8 @@ pcu_status Ctx::open(int dev)
     if ((st = hip(hipHostMalloc((void **)&host_words, sizeof(unsigned long long) * kMaxNodes,
                                 hipHostMallocDefault), "hipHostMalloc")))
         return st;
-    return PCU_OK;
+    nodes.reserve(kMaxNodes); // adding a node never reallocates
+    return hip(noalloc_setup(dev), "hipGetSymbolAddress(scratch)");
 }
 
 Ctx::~Ctx()
@@ -366,9 +407,11 @@ static bool decode_word(const NodeInfo &n, uint64_t word, pcu_fault *f)
     return false;
 }
 
-pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
+// Ends the open program: one copy of its fault words to host_words and one
+// synchronization. *used is the program's node count.
+pcu_status Ctx::read_words(size_t *used)
 {
-    faults->clear();
+    *used = 0;
     if (!in_program) {
         fail("no program open");
         return PCU_ERR_STATE;
@@ -377,34 +420,50 @@ pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
     pcu_status st = join_side();
     if (st)
         return st;
-    size_t used = nodes.size();
-    if (used) {
+    *used = nodes.size();
+    if (*used) {
         // Nodes that launched nothing (empty shapes) still have their words read.
         if ((st = open_words()))
             return st;
-        if ((st = hip(hipMemcpyAsync(host_words, fault_words, used * sizeof(unsigned long long),
+        if ((st = hip(hipMemcpyAsync(host_words, fault_words, *used * sizeof(unsigned long long),
                                      hipMemcpyDeviceToHost, stream), "hipMemcpyAsync")))
             return st;
     }
-    if ((st = hip(hipStreamSynchronize(stream), "hipStreamSynchronize")))
+    return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+}
+
+// Node i's word, read by read_words and holding a fault, as a decoded record.
+pcu_status Ctx::decode_node(size_t i, pcu_fault *f)
+{
+    memset(f, 0, sizeof *f);
+    const uint64_t w = host_words[i];
+    if (!decode_word(nodes[i], w, f)) {
+        fail("malformed fault word 0x%016llx at node %zu", (unsigned long long)w, i);
+        // The raw word travels back as (ordinal << 3) | kind for the caller's
+        // InvalidExecutionFaultWord(word) (backends/rocm/owned_dispatch.rs:95).
+        memset(&protocol_fault, 0, sizeof protocol_fault);
+        protocol_fault.node = (uint32_t)i;
+        protocol_fault.kind = (uint32_t)(w & 7);
+        protocol_fault.ordinal = w >> 3;
+        return PCU_ERR_PROTOCOL;
+    }
+    f->node = (uint32_t)i;
+    return PCU_OK;
+}
+
+pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
+{
+    faults->clear();
+    size_t used = 0;
+    pcu_status st = read_words(&used);
+    if (st)
         return st;
     for (size_t i = 0; i < used; i++) {
-        uint64_t w = host_words[i];
-        if (w == kNoFaultWord)
+        if (host_words[i] == kNoFaultWord)
             continue;
         pcu_fault f;
-        memset(&f, 0, sizeof f);
-        if (!decode_word(nodes[i], w, &f)) {
-            fail("malformed fault word 0x%016llx at node %zu", (unsigned long long)w, i);
-            // The raw word travels back as (ordinal << 3) | kind for the caller's
-            // InvalidExecutionFaultWord(word) (backends/rocm/owned_dispatch.rs:95).
-            memset(&protocol_fault, 0, sizeof protocol_fault);
-            protocol_fault.node = (uint32_t)i;
-            protocol_fault.kind = (uint32_t)(w & 7);
-            protocol_fault.ordinal = w >> 3;
-            return PCU_ERR_PROTOCOL;
-        }
-        f.node = (uint32_t)i;
+        if ((st = decode_node(i, &f)))
+            return st;
         faults->push_back(f);
     }
     has_held_fault = !faults->empty();
@@ -413,18 +472,35 @@ pcu_status Ctx::end_program_all(std::vector<pcu_fault> *faults)
     return PCU_OK;
 }
 
+// The first fault in node order; every word is still validated. Allocates nothing.
 pcu_status Ctx::end_program(pcu_fault *first)
 {
-    std::vector<pcu_fault> faults;
-    pcu_status st = end_program_all(&faults);
-    if (st == PCU_ERR_PROTOCOL && first)
-        *first = protocol_fault;
+    size_t used = 0;
+    pcu_status st = read_words(&used);
     if (st)
         return st;
-    if (faults.empty())
+    bool found = false;
+    pcu_fault earliest{};
+    for (size_t i = 0; i < used; i++) {
+        if (host_words[i] == kNoFaultWord)
+            continue;
+        pcu_fault f;
+        if ((st = decode_node(i, &f))) {
+            if (first)
+                *first = protocol_fault;
+            return st;
+        }
+        if (!found) {
+            earliest = f;
+            found = true;
+        }
+    }
+    has_held_fault = found;
+    if (!found)
         return PCU_OK;
+    held_fault = earliest;
     if (first)
-        *first = faults.front();
+        *first = earliest;
     return PCU_ARITHMETIC_FAULT;
 }
 
@@ -563,7 +639,7 @@ static bool matmul_out_overlaps(int dtype, uint64_t rows, uint64_t inner, uint64
 }
 
 pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
-                          int tr, const void *a, const void *b, void *c, int policy)
+                          int tr, const void *a, const void *b, void *c, int policy, bool noalloc)
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || !c || ((rows * inner) && !a) ||
         ((inner * cols) && !b)) {
@@ -574,6 +650,18 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         fail("strict_matmul: the output overlaps an operand");
         return PCU_ERR_ARGUMENT;
     }
+    if (noalloc) {
+        if (rows > PCU_NOALLOC_MAX_DIM || cols > PCU_NOALLOC_MAX_DIM) {
+            fail("strict_matmul_noalloc: rows and cols are each limited to %u by its fixed "
+                 "scratch (got %llu x %llu)", (unsigned)PCU_NOALLOC_MAX_DIM,
+                 (unsigned long long)rows, (unsigned long long)cols);
+            return PCU_ERR_ARGUMENT;
+        }
+        if (device >= kNoAllocDevices || !g_noalloc[device].ptr) {
+            fail("strict_matmul_noalloc: no scratch address for device %d", device);
+            return PCU_ERR_STATE;
+        }
+    }
     unsigned long long *word;
     NodeInfo info{Prim::MatMul, rows * cols, inner};
     pcu_status st = add_node(info, &word);
@@ -581,35 +669,55 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         return st;
     if (rows == 0 || cols == 0)
         return PCU_OK;
+    // The screen's exponent words carry a generation that only grows, so a later screen
+    // outranks every word left by earlier ones; new scratch, or a wrapped counter, is
+    // cleared first (by a fill kernel).
     void *sc = nullptr;
-    const Scratch old = matmul_scratch;
-    if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols), false, &sc)))
-        return st;
+    size_t clear_words = 0; // words to zero before this screen (0: none)
+    uint32_t gen = 0;
+    if (noalloc) {
+        // The device's fixed array, shared by every context on the device.
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        NoAllocDevice &d = g_noalloc[device];
+        sc = d.ptr;
+        if (!d.cleared || d.gen == UINT32_MAX) {
+            clear_words = kNoAllocScratchWords;
+            d.cleared = true;
+            d.gen = 0;
+        }
+        gen = ++d.gen;
+    } else {
+        const Scratch old = matmul_scratch;
+        if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols), false, &sc)))
+            return st;
+        if (matmul_scratch.p != old.p || matmul_scratch.cap != old.cap || screen_gen == UINT32_MAX) {
+            clear_words = matmul_scratch.cap / 8;
+            screen_gen = 0;
+        }
+        gen = ++screen_gen;
+    }
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
-    const bool fresh = matmul_scratch.p != old.p || matmul_scratch.cap != old.cap;
+    s.gen = gen;
 
+    // Per-kernel timing takes events from a pool that may grow, so the no-allocation call
+    // is never timed.
+    const bool timed = profiling && !noalloc;
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
-    if (profiling)
+    if (timed)
         for (auto &x : ev)
             x = take_event();
     if ((st = open_words()))
         return st;
-    // The screen's exponent words carry a generation that only grows, so a later screen
-    // outranks every word left by earlier ones; new scratch, or a wrapped counter, is
-    // cleared first.
-    if (fresh || screen_gen == UINT32_MAX) {
-        if ((st = hip(launch_fill_u64(stream, (unsigned long long *)sc, matmul_scratch.cap / 8, 0),
-                      "clear MatMul screen words")))
-            return st;
-        screen_gen = 0;
-    }
-    s.gen = ++screen_gen;
+    if (clear_words &&
+        (st = hip(launch_fill_u64(stream, (unsigned long long *)sc, clear_words, 0),
+                  "clear MatMul screen words")))
+        return st;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
-                                        profiling ? ev : nullptr, matmul_engine);
+                                        timed ? ev : nullptr, matmul_engine);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
-    if (profiling) {
+    if (timed) {
         timings.push_back({PCU_KERNEL_GEMM_PREFILTER, ev[0], ev[1]});
         timings.push_back({PCU_KERNEL_STRICT_GEMM, ev[1], ev[2]});
         timings.push_back({PCU_KERNEL_GEMM_REPLAY, ev[2], ev[3]});
@@ -1032,6 +1140,17 @@ pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint6
 {
     PCU_OP_PROLOGUE
     st = c->op_matmul(dtype, rows, inner, cols, transpose_left, transpose_right, left, right, out, policy);
+    return c->finish_op(st, fault);
+}
+
+pcu_status pcu_strict_matmul_noalloc(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
+                                     uint64_t cols, int transpose_left, int transpose_right,
+                                     const void *left, const void *right, void *out,
+                                     pcu_underflow policy, pcu_fault *fault)
+{
+    PCU_OP_PROLOGUE
+    st = c->op_matmul(dtype, rows, inner, cols, transpose_left, transpose_right, left, right, out,
+                      policy, true);
     return c->finish_op(st, fault);
 }
 

@@ -159,6 +159,21 @@ pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint6
                              const void *left, const void *right, void *out,
                              pcu_underflow policy, pcu_fault *fault);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * call and results as pcu_strict_matmul, with the exponent screen's scratch in a fixed array
+ * of the library on each device instead of the context's pool, so the call allocates
+ * nothing (no hipMalloc, hipFree or pool allocation; it is never per-kernel timed). rows and
+ * cols are each at most PCU_NOALLOC_MAX_DIM; larger shapes return PCU_ERR_ARGUMENT. The
+ * array (1 MiB + 256 B per device, held until the process ends) is shared by every call on
+ * the device and keeps the last call's contents; the library clears what must start at zero.
+ * Calls that overlap on one device (from two contexts or two host threads) race. */
+#define PCU_NOALLOC_MAX_DIM 65536u
+pcu_status pcu_strict_matmul_noalloc(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
+                                     uint64_t cols, int transpose_left, int transpose_right,
+                                     const void *left, const void *right, void *out,
+                                     pcu_underflow policy, pcu_fault *fault);
+
 /* out[i] = left[i] (op) right[i], checked. */
 pcu_status pcu_checked_binary(pcu_ctx *ctx, pcu_dtype dtype, pcu_binary_op op, uint64_t n,
                               const void *left, const void *right, void *out,
