@@ -691,7 +691,9 @@ def test_output_overlapping_an_operand_is_rejected(ctx, pcu_pkg):
                                base + 4 * 64, 0, ctypes.byref(f))
     assert st == _abi.PCU_ERR_ARGUMENT, st
     assert "overlap" in ctx.error_text()
-    st = lib.pcu_native_matmul(ctx.handle, 0, 64, 64, 64, 0, 0, base, base, base + 64 * 64 * 4 * 2 - 4)
+    # Every range below lies inside `big` (2 * 64 * 64 floats); each call must be refused.
+    st = lib.pcu_native_matmul(ctx.handle, 0, 64, 64, 64, 0, 0, base, base + 64 * 64 * 4,
+                               base + 64 * 64 * 4 - 4)
     assert st == _abi.PCU_ERR_ARGUMENT
     st = lib.pcu_checked_relu(ctx.handle, 0, 64 * 64, base, base + 16, 0, ctypes.byref(f))
     assert st == _abi.PCU_ERR_ARGUMENT
