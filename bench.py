@@ -49,27 +49,37 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
-    from fusion_pcu_amd import synthetic as syn
-    a = syn.uniform(seed_a, (m, k), dtype)
-    b = syn.uniform(seed_b, (k, n), dtype)
-    da, db = ctx.upload(a), ctx.upload(b)
-    dc = ctx.empty((m, n), dtype)
+def _abi_matmul(ctx, da, db, dc, m, k, n, policy=0):
+    """One strict MatMul call straight through the C ABI; returns its status (a fault
+    variant returns PCU_ARITHMETIC_FAULT without a Python exception in the timed loop)."""
+    import ctypes
+    from fusion_pcu_amd import _abi
+    f = _abi.Fault()
+    code = _abi.PCU_F32 if da.dtype == np.float32 else _abi.PCU_F64
+    return ctx._lib.pcu_strict_matmul(ctx.handle, code, m, k, n, 0, 0, da.ptr, db.ptr, dc.ptr,
+                                      policy, ctypes.byref(f))
+
+
+def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0):
+    """ms per complete call, timed with per-kernel timing off, then the kernel breakdown
+    (prefilter, main tile kernel, replay including the tiny scan) from a second timed
+    pass of the same number of calls."""
     for _ in range(warmup):
-        ctx.strict_matmul(da, db, out=dc)
+        assert _abi_matmul(ctx, da, db, dc, m, k, n) == expect
     ctx.synchronize()
-    ctx.profile(True)
     t0 = time.perf_counter()
     for _ in range(steps):
-        ctx.strict_matmul(da, db, out=dc)
+        _abi_matmul(ctx, da, db, dc, m, k, n)
     ctx.synchronize()
     t1 = time.perf_counter()
+    ctx.profile(True)
+    for _ in range(steps):
+        _abi_matmul(ctx, da, db, dc, m, k, n)
+    ctx.synchronize()
     gemm_ms, gemm_n = ctx.kernel_time("strict_gemm")
     pre_ms, _ = ctx.kernel_time("gemm_prefilter")
     rep_ms, _ = ctx.kernel_time("gemm_replay")
     ctx.profile(False)
-    for x in (da, db, dc):
-        x.free()
     ms_step = (t1 - t0) * 1e3 / steps
     return {
         "ms_per_step": ms_step,
@@ -79,6 +89,152 @@ def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
         "prefilter_avg_ms": pre_ms / max(gemm_n, 1),
         "replay_avg_ms": rep_ms / max(gemm_n, 1),
     }
+
+
+def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
+    from fusion_pcu_amd import synthetic as syn
+    a = syn.uniform(seed_a, (m, k), dtype)
+    b = syn.uniform(seed_b, (k, n), dtype)
+    da, db = ctx.upload(a), ctx.upload(b)
+    dc = ctx.empty((m, n), dtype)
+    res = time_matmul(ctx, da, db, dc, m, k, n, steps, warmup)
+    for x in (da, db, dc):
+        x.free()
+    return res
+
+
+def bench_c2_variants(pkg, ctx, steps):
+    """C2: strict F32 1024^3, clean and its two fault variants (1,049 A entries set to 3.0e38:
+    an Add overflow; 1,049 B entries NaN: a Multiply invalid at the lowest cell), plus a
+    4096^3 input whose every cell the exponent screen marks while none faults (A column 0
+    at 2^-120, B row 0 in +-[0.5, 1)): the cost of the fault search and of the replay."""
+    from fusion_pcu_amd import _abi
+    from fusion_pcu_amd import synthetic as syn
+    m = k = n = 1024
+    a = syn.uniform(21, (m, k), np.float32)
+    b = syn.uniform(22, (k, n), np.float32)
+    cnt = int(np.ceil(0.001 * m * k))
+    rng = np.random.default_rng(2)
+    a_ovf = a.copy()
+    a_ovf.reshape(-1)[rng.choice(m * k, cnt, replace=False)] = np.float32(3.0e38)
+    b_nan = b.copy()
+    b_nan.reshape(-1)[rng.choice(k * n, cnt, replace=False)] = np.float32(np.nan)
+    out = {}
+    dc = ctx.empty((m, n), np.float32)
+    for name, x, y, expect in (("clean", a, b, _abi.PCU_OK),
+                               ("variant_a_overflow", a_ovf, b, _abi.PCU_ARITHMETIC_FAULT),
+                               ("variant_b_nan", a, b_nan, _abi.PCU_ARITHMETIC_FAULT)):
+        da, db = ctx.upload(x), ctx.upload(y)
+        r = time_matmul(ctx, da, db, dc, m, k, n, steps, 3, expect)
+        if expect != _abi.PCU_OK:
+            r["fault"] = str(ctx.last_fault())
+        out[name] = r
+        da.free()
+        db.free()
+    dc.free()
+    M = 4096
+    a = syn.uniform(11, (M, M), np.float32)
+    b = syn.uniform(12, (M, M), np.float32)
+    sign = np.where(np.random.default_rng(3).random(M) < 0.5, -1.0, 1.0)
+    a[:, 0] = (2.0 ** -120 * sign).astype(np.float32)
+    b[0, :] = (np.random.default_rng(4).uniform(0.5, 1.0, M) * sign[::-1]).astype(np.float32)
+    da, db, dc = ctx.upload(a), ctx.upload(b), ctx.empty((M, M), np.float32)
+    r = time_matmul(ctx, da, db, dc, M, M, M, max(3, steps // 4), 2)
+    r["input"] = "A col 0 = +-2^-120, B row 0 in +-[0.5, 1), rest uniform[-1,1]: every cell marked, none faults"
+    out["suspect_heavy_clean_4096"] = r
+    for x in (da, db, dc):
+        x.free()
+    return out
+
+
+def bench_c3(pkg, ctx, steps):
+    """C3: strict F64 MatMul 4096^3 then checked bias add and ReLU, A, B, bias normal(0,1),
+    as one prepared strict program (the Add fuses into the ReLU)."""
+    from fusion_pcu_amd import graph as G
+    from fusion_pcu_amd import synthetic as syn
+    M = 4096
+    a = G.PcuTensor(ctx.upload(syn.normal(31, (M, M), 1.0, np.float64)))
+    b = G.PcuTensor(ctx.upload(syn.normal(32, (M, M), 1.0, np.float64)))
+    bias = G.PcuTensor(ctx.upload(syn.normal(33, (M, M), 1.0, np.float64)))
+
+    @G.function(strict=True)
+    def c3(x, y, z):
+        return G.relu(G.add(G.matmul(x, y), z))
+
+    for _ in range(2):
+        c3(a, b, bias).release()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        c3(a, b, bias).release()
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
+    return {"ms_per_step": ms, "gflops": 2.0 * M ** 3 / (ms * 1e-3) / 1e9,
+            "work": "strict F64 MatMul 4096^3 + checked bias add + ReLU, one prepared program"}
+
+
+def bench_c1(pkg, ctx, steps=10):
+    """C1: the strict F32 single-layer training step (X 64x128, W 128x64, b 64x64, Y 64x64,
+    seeds 1..4, lr 0.01) with W and b resident and fed back: microseconds per step."""
+    from fusion_pcu_amd import graph as G
+    from fusion_pcu_amd import synthetic as syn
+    x = G.PcuTensor(ctx.upload(syn.uniform(1, (64, 128), np.float32)))
+    w = G.PcuTensor(ctx.upload(syn.uniform(2, (128, 64), np.float32)))
+    b = G.PcuTensor(ctx.upload(syn.uniform(3, (64, 64), np.float32)))
+    y = G.PcuTensor(ctx.upload(syn.uniform(4, (64, 64), np.float32)))
+    step = G.c1_training_step(0.01)
+    for _ in range(5):
+        w, b, loss = step(x, w, b, y)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        w, b, loss = step(x, w, b, y)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    return {"us_per_step": (t1 - t0) * 1e6 / steps, "steps": steps,
+            "work": "forward matmul + bias + relu, MSE, reverse mode, two SGD updates; one prepared program"}
+
+
+def bench_small_calls(pkg, ctx, reps=200):
+    """Resident single calls at the sizes the reference publishes latencies for (each call
+    synchronizes and reads its fault status). The reference's numbers are on consumer GPUs
+    and include per-call allocation; they are context, not a like-for-like comparison."""
+    from fusion_pcu_amd import synthetic as syn
+    out = {}
+    for dtype, tag, ref in ((np.float32, "f32", {"Radeon RX 6900 XT": 379.33, "GeForce RTX 3080": 331.34}),
+                            (np.float64, "f64", {"Radeon RX 6900 XT": 367.36, "GeForce RTX 3080": 379.00})):
+        da = ctx.upload(syn.uniform(5, (64, 256), dtype))
+        db = ctx.upload(syn.uniform(6, (256, 64), dtype))
+        dc = ctx.empty((64, 64), dtype)
+        for _ in range(20):
+            _abi_matmul(ctx, da, db, dc, 64, 256, 64)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            _abi_matmul(ctx, da, db, dc, 64, 256, 64)
+        t1 = time.perf_counter()
+        out[f"matmul_64x256x64_{tag}_us"] = (t1 - t0) * 1e6 / reps
+        out[f"matmul_64x256x64_{tag}_reference_us"] = ref
+        for x in (da, db, dc):
+            x.free()
+    n = 1 << 20
+    for dtype, tag, ref in ((np.float32, "f32", {"Radeon RX 6900 XT": 337.224, "GeForce RTX 3080": 392.612}),
+                            (np.float64, "f64", {"Radeon RX 6900 XT": 379.015, "GeForce RTX 3080": 825.453})):
+        dw = ctx.upload(syn.normal(7, (n,), 1.0, dtype))
+        dg = ctx.upload(syn.normal(8, (n,), 1e-3, dtype))
+        do = ctx.empty((n,), dtype)
+        for _ in range(20):
+            ctx.strict_sgd(dw, dg, 0.01, out=do)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            ctx.strict_sgd(dw, dg, 0.01, out=do)
+        t1 = time.perf_counter()
+        out[f"sgd_1M_{tag}_us"] = (t1 - t0) * 1e6 / reps
+        out[f"sgd_1M_{tag}_reference_us"] = ref
+        for x in (dw, dg, do):
+            x.free()
+    out["reference_source"] = "reference README.md:236-243 (MatMul), :303-311, :334-335 (SGD), resident calls"
+    return out
 
 
 def bench_sgd(pkg, ctx, n, steps, warmup):
@@ -348,6 +504,14 @@ def main() -> int:
             }
             log("strict F32 SGD 2^28 (C4 shape)")
             extra["sgd_f32_2p28"] = bench_sgd(pkg, ctx, 1 << 28, max(5, args.steps), 2)
+            log("C2 1024^3 clean and fault variants; a fully screen-marked clean 4096^3")
+            extra["c2_and_replay"] = bench_c2_variants(pkg, ctx, max(10, args.steps))
+            log("C3 F64 MatMul + bias + ReLU program")
+            extra["c3_f64_program"] = bench_c3(pkg, ctx, max(2, args.steps // 3))
+            log("C1 training-step latency")
+            extra["c1_train_step"] = bench_c1(pkg, ctx)
+            log("small resident calls beside the reference's published latencies")
+            extra["small_calls"] = bench_small_calls(pkg, ctx)
 
     gemm_s = mm["gemm_avg_ms"] * 1e-3
     achieved = 2.0 * M * N * K / gemm_s / 1e12
@@ -386,7 +550,9 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (SplitMix64 uniform[-1,1], seeds 11/12)",
         "config": {"workload": "strict F32 MatMul 4096x4096x4096 (A,B uniform[-1,1]); one step = "
-                               "prefilter + tile kernel + replay check + fault readback",
+                               "prefilter + tile kernel + replay check + fault readback; timed "
+                               "with per-kernel timing off (the roofline's kernel duration comes "
+                               "from a second, timed pass)",
                    "m": M, "k": K, "n": N},
         "pct_fp32_vector_peak": round(100.0 * mm["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 3),
         "mlp_train_steps_per_s": (round(extra["mlp_c5"]["steps_per_s"], 3)

@@ -5,7 +5,7 @@
 // then the sum on their own (no FMA, no MFMA, no reassociation). The first fault is the
 // lowest (row-major cell, k, Multiply before Add).
 //
-// Three launches:
+// Four launches:
 //  1. prefilter   per-row minimum exponent of op(A) and per-column minimum exponent of
 //                 op(B) over finite nonzero entries (bandwidth-bound, ~2 reads of A and B).
 //  2. main        LDS-staged 128x128 output tile per 256-thread workgroup, 8x8 register
@@ -14,10 +14,14 @@
 //                 invalid operand or an overflow leaves) or when the two exponents allow a
 //                 product small enough to be tiny (the only way an underflow can arise),
 //                 and keeps the first suspect cell with one atomicMin per wave.
-//  3. replay      exact ordered re-execution of suspect cells in row-major order from the
-//                 first suspect, with per-op classification; stops once the earliest fault
-//                 found lies before the cells still to visit. Returns at once when no cell
-//                 is suspect, which is the fault-free path.
+//  3. tiny scan   (IEEE policy, only when a cell is marked) a tiled pass like the main
+//                 kernel over the tiles the screen marks, finding the cells that have a
+//                 product at most the smallest normal; see k_gemm_tiny_scan.
+//  4. replay      exact ordered re-execution in row-major order from the first suspect:
+//                 non-finite cells walked serially, per-op classified; cells the scan
+//                 flagged have their K products classified in parallel by a wave. Both stop
+//                 once the earliest fault found lies before the cells still to visit. The
+//                 fault-free path returns at once.
 #include "pcu_device.hpp"
 #include "pcu_gemm_stage.hpp"
 #include "pcu_kernels.hpp"
@@ -215,8 +219,10 @@ __global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, ui
     __shared__ int part[4][64 * 16 / sizeof(T)];
     if (block_gate_closed(gate))
         return;
-    if (blockIdx.x == 0 && threadIdx.x == 0)
-        *suspect = kNoFault;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        suspect[0] = kNoFault; // first suspect cell
+        suspect[1] = kNoFault; // first row with a cell the tiny scan flags
+    }
     const bool first = blockIdx.x < na;
     const ExpJob<T> &j = first ? a : b;
     const uint64_t bid = first ? blockIdx.x : blockIdx.x - na;
@@ -464,55 +470,288 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
         wave_record_fault(key, suspect);
 }
 
+// ------------------------------------------------------------------ tiny scan
+// IEEE policy. A cell whose result is finite met no invalid operand and no overflow (both
+// leave Inf or NaN for good), and a sum is never tiny-inexact, so its first fault can only
+// be a Multiply whose product is tiny and inexact. This tiled pass finds the cells that have
+// any product at most the smallest normal from a nonzero, finite pair of operands: per cell
+// the smallest |a * b| over k, two vector instructions per (cell, k) like the strict kernel.
+// Zero and non-finite operands are staged as 2^64, whose products are never that small (a
+// non-finite operand makes its whole row or column non-finite, which the serial replay
+// walks). For each output row it keeps the first such column, and the first such row
+// overall. It runs only when the screen marked a cell, and skips every tile whose row and
+// column exponents rule out a tiny product.
+template <typename T> __device__ __forceinline__ T tiny_scan_operand(T x)
+{
+    const T stand_in = (T)18446744073709551616.0; // 2^64
+    return (x == (T)0 || !finite_bits(x)) ? stand_in : x;
+}
+
+template <typename T, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
+    const T *__restrict__ A, const T *__restrict__ B, int M, int N, int K,
+    const unsigned long long *__restrict__ row_exp, const unsigned long long *__restrict__ col_exp,
+    int thr, const unsigned long long *suspect, unsigned long long *row_flag,
+    unsigned long long *flag_first, uint32_t gen, NodeGate gate)
+{
+    if (block_gate_closed(gate))
+        return;
+    if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault)
+        return; // no cell marked: nothing to scan (the same word for every thread)
+    using Cfg = ValuCfg<T>;
+    constexpr int BK = Cfg::BK;
+    __shared__ __align__(16) T As[2][BK][Cfg::LDA];
+    __shared__ __align__(16) T Bs[2][BK][Cfg::LDB];
+    __shared__ int tile_min[2];
+
+    const int tid = threadIdx.x;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    // Smallest row exponent of the tile's rows (wave 0) and column exponent of its columns
+    // (wave 1): the tile holds a marked cell only if their sum is below the threshold.
+    if (tid < 128) {
+        const int base = tid < 64 ? m0 : n0, lim = tid < 64 ? M : N, l = tid & 63;
+        const unsigned long long *w = tid < 64 ? row_exp : col_exp;
+        int e = kExpNone;
+        for (int i = l; i < BM; i += 64)
+            if (base + i < lim) {
+                const int x = exp_of(w[base + i]);
+                e = x < e ? x : e;
+            }
+        e = wave_min_i32(e);
+        if (l == 0)
+            tile_min[tid >> 6] = e;
+    }
+    __syncthreads();
+    if (tile_min[0] + tile_min[1] >= thr)
+        return;
+
+    const int tx = tid % 16, ty = tid / 16;
+    constexpr int RUN = 16 / sizeof(T), RUNS = 8 / RUN, RUN_STRIDE = BN / RUNS;
+    auto col_of = [&](int j) { return (j / RUN) * RUN_STRIDE + tx * RUN + (j % RUN); };
+    T mn[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            mn[i][j] = (T)INFINITY;
+
+    SlabStager<T, Cfg, TA, TB, VA, VB> stage;
+    auto stage_mapped = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < Cfg::EA; i++)
+            stage.ra[i] = tiny_scan_operand(stage.ra[i]);
+#pragma unroll
+        for (int i = 0; i < Cfg::EB; i++)
+            stage.rb[i] = tiny_scan_operand(stage.rb[i]);
+        stage.stash(As[buf], Bs[buf], tid);
+    };
+    const int ktiles = (K + BK - 1) / BK;
+    if (ktiles > 0) {
+        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        stage_mapped(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles)
+            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+#pragma unroll(sizeof(T) == 4 ? BK : 2)
+        for (int k = 0; k < BK; k++) {
+            T a[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[i] = As[cur][k][ty * 4 + i];
+                a[4 + i] = As[cur][k][64 + ty * 4 + i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                b[j] = Bs[cur][k][col_of(j)];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    mn[i][j] = fmin(mn[i][j], fabs(a[i] * b[j]));
+        }
+        if (kt + 1 < ktiles)
+            stage_mapped(cur ^ 1);
+        __syncthreads();
+    }
+    // Past the edges the operands stage as +0, mapped to 2^64: those cells never flag.
+    const T min_normal = sizeof(T) == 4 ? (T)1.17549435082228750797e-38 : (T)2.2250738585072014e-308;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+        uint32_t first = 0xffffffffu;
+#pragma unroll
+        for (int j = 7; j >= 0; j--) {
+            const int c = n0 + col_of(j);
+            if (c < N && mn[i][j] <= min_normal)
+                first = (uint32_t)c < first ? (uint32_t)c : first;
+        }
+        if (r < M && first != 0xffffffffu) {
+            atomicMax(&row_flag[r], ((unsigned long long)gen << 32) | (0xffffffffu - first));
+            atomicMin(flag_first, (unsigned long long)r);
+        }
+    }
+}
+
 // --------------------------------------------------------------- exact replay
 
+// First fault of one output cell, found by a whole wave (every lane returns the same). The
+// K products are classified 64 at a time in k order, which gives the first faulting
+// Multiply k_m. When `walk_adds` is set (a non-finite result, where a sum can overflow, or
+// RejectSubnormal, where a subnormal sum faults), the ordered sums before k_m are then
+// formed exactly as the contract orders them: the lanes form 64 products at a time and
+// every lane folds them in k order with the exact add classifier. Returns kNoFault or the
+// packed fault word.
+template <typename T>
+__device__ __forceinline__ uint64_t cell_first_fault(const T *__restrict__ A, const T *__restrict__ B,
+                                                     uint64_t M, uint64_t N, uint64_t K, int ta,
+                                                     int tb, uint64_t cell, int policy,
+                                                     bool walk_adds)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t r = cell / N, c = cell % N;
+    auto a_at = [&](uint64_t k) { return ta ? A[k * M + r] : A[r * K + k]; };
+    auto b_at = [&](uint64_t k) { return tb ? B[c * K + k] : B[k * N + c]; };
+    uint64_t k_m = K;
+    uint32_t kind_m = kOk;
+    for (uint64_t k0 = 0; k0 < K; k0 += 64) {
+        const uint64_t k = k0 + lane;
+        uint32_t kind = kOk;
+        if (k < K) {
+            const T a = a_at(k), b = b_at(k);
+            kind = classify_mul(a, b, a * b, policy);
+        }
+        const uint64_t mask = __ballot(kind != kOk);
+        if (mask) {
+            const int l = __ffsll((long long)mask) - 1;
+            k_m = k0 + l;
+            kind_m = __shfl(kind, l, 64);
+            break;
+        }
+    }
+    if (walk_adds) {
+        T total = (T)0;
+        for (uint64_t k0 = 0; k0 < k_m; k0 += 64) {
+            const uint64_t k = k0 + lane;
+            T p = (T)0;
+            if (k < k_m) {
+                const T a = a_at(k), b = b_at(k);
+                p = a * b;
+            }
+            const int here = k_m - k0 < 64 ? (int)(k_m - k0) : 64;
+            for (int j = 0; j < here; j++) {
+                const T pj = __shfl(p, j, 64);
+                const T nxt = total + pj;
+                const uint32_t kind = classify_add(total, pj, nxt, policy);
+                if (kind != kOk)
+                    return pack_fault((cell * K + k0 + j) * 2 + 1, kind);
+                total = nxt;
+            }
+        }
+    }
+    if (k_m < K)
+        return pack_fault((cell * K + k_m) * 2, kind_m);
+    return kNoFault;
+}
+
+// Lane 0's value, on every lane of the wave.
+__device__ __forceinline__ uint64_t wave_uniform_u64(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Two passes over the suspect cells, one wave per cell, each recording the earliest fault
+// it finds with atomicMin and stopping once that lies before the cells it has left. Every
+// loop is bounded, and each wave's branches are uniform, so each ballot sees its 64 lanes.
+//  1. Blocks of 64 cells in row-major order from the first suspect cell: the lanes screen
+//     the block's cells at once, and the wave takes its candidates in order (a non-finite
+//     result, and under RejectSubnormal, where a subnormal partial sum faults too, every
+//     cell the exponent screen marks) with the products and the ordered sums.
+//  2. Tiny (IEEE, after k_gemm_tiny_scan): rows in order from the first flagged row, each
+//     from its first flagged column. For a finite cell the first fault is the lowest k whose
+//     product is tiny and inexact, so only the products are classified.
 template <typename T>
 __global__ __launch_bounds__(256) void k_strict_gemm_replay(
     const T *__restrict__ A, const T *__restrict__ B, const T *__restrict__ C, uint64_t M,
     uint64_t N, uint64_t K, int ta, int tb, const unsigned long long *__restrict__ row_exp,
-    const unsigned long long *__restrict__ col_exp, int thr, int check_risk, int policy,
-    const unsigned long long *suspect, unsigned long long *fault, NodeGate gate)
+    const unsigned long long *__restrict__ col_exp, int thr, int serial_screen, int tiny,
+    int policy, const unsigned long long *suspect, const unsigned long long *row_flag,
+    const unsigned long long *flag_first, uint32_t gen, unsigned long long *fault, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return; // an earlier node faulted: that fault is the one reported
     const uint64_t first = *suspect;
-    if (first == kNoFault)
+    if (first == kNoFault || K == 0)
         return;
     const uint64_t cells = M * N;
-    const uint64_t threads = (uint64_t)gridDim.x * blockDim.x;
-    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (uint64_t base = first; base < cells; base += threads) {
-        uint64_t best = __atomic_load_n(fault, __ATOMIC_RELAXED);
-        if (best != kNoFault && K > 0 && ((best >> 3) / 2) / K < base)
-            break;
-        uint64_t cell = base + tid;
-        if (cell >= cells)
-            break;
-        uint64_t r = cell / N, c = cell % N;
-        bool bad = !finite_bits(C[cell]);
-        if (check_risk)
-            bad |= exp_of(row_exp[r]) + exp_of(col_exp[c]) < thr;
-        if (!bad)
-            continue;
-        T total = (T)0;
-        for (uint64_t k = 0; k < K; k++) {
-            T a = ta ? A[k * M + r] : A[r * K + k];
-            T b = tb ? B[c * K + k] : B[k * N + c];
-            T p = a * b;
-            uint32_t kind = classify_mul(a, b, p, policy);
-            if (kind != kOk) {
-                atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2, kind));
-                gate_record(gate);
+    // The cell of a packed MatMul fault: ordinal = 2 (cell K + k) + step.
+    auto cell_of = [&](uint64_t w) { return ((w >> 3) / 2) / K; };
+    // One value for the whole wave, so its lanes take every branch together.
+    auto best_cell = [&]() {
+        const uint64_t w = wave_uniform_u64(__atomic_load_n(fault, __ATOMIC_RELAXED));
+        return w == kNoFault ? kNoFault : cell_of(w);
+    };
+    auto record = [&](uint64_t w) {
+        if ((threadIdx.x & 63) == 0) {
+            atomicMin(fault, (unsigned long long)w);
+            gate_record(gate);
+        }
+    };
+    const int lane = threadIdx.x & 63;
+    const uint64_t waves = (uint64_t)gridDim.x * (blockDim.x / 64);
+    const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    for (uint64_t c0 = (first / 64 + wave) * 64; c0 < cells; c0 += waves * 64) {
+        if (best_cell() < c0)
+            break; // this wave's blocks only grow
+        const uint64_t cell = c0 + lane;
+        bool cand = false;
+        if (cell < cells) {
+            cand = !finite_bits(C[cell]);
+            if (serial_screen)
+                cand |= exp_of(row_exp[cell / N]) + exp_of(col_exp[cell % N]) < thr;
+        }
+        uint64_t mask = __ballot(cand);
+        while (mask) {
+            const int l = __ffsll((long long)mask) - 1;
+            mask &= mask - 1;
+            const uint64_t x = c0 + l;
+            if (best_cell() < x)
                 break;
+            const uint64_t w = cell_first_fault(A, B, M, N, K, ta, tb, x, policy, true);
+            if (w != kNoFault) {
+                record(w);
+                break; // the block's later cells come after this fault
             }
-            T nxt = total + p;
-            kind = classify_add(total, p, nxt, policy);
-            if (kind != kOk) {
-                atomicMin(fault, (unsigned long long)pack_fault((cell * K + k) * 2 + 1, kind));
-                gate_record(gate);
-                break;
+        }
+    }
+    if (!tiny)
+        return;
+    const uint64_t row0 = __atomic_load_n(flag_first, __ATOMIC_RELAXED);
+    if (row0 == kNoFault)
+        return;
+    for (uint64_t r = row0 + wave; r < M; r += waves) {
+        const unsigned long long w = wave_uniform_u64(row_flag[r]);
+        if ((uint32_t)(w >> 32) != gen)
+            continue; // no cell of this row was flagged by this MatMul's scan
+        bool done = false;
+        for (uint64_t c = 0xffffffffu - (uint32_t)w; c < N && !done; c++) {
+            const uint64_t cell = r * N + c;
+            if (best_cell() < cell)
+                return; // rows only grow: this wave has nothing earlier left
+            if (!finite_bits(C[cell]))
+                continue; // the first pass took it
+            const uint64_t f = cell_first_fault(A, B, M, N, K, ta, tb, cell, policy, false);
+            if (f != kNoFault) {
+                record(f);
+                done = true; // later cells of the row come after this fault
             }
-            total = nxt;
         }
     }
 }
@@ -523,18 +762,25 @@ size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols)
 {
     size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     size_t c = ((cols * sizeof(unsigned long long)) + 255) & ~(size_t)255;
-    return r + c + 256;
+    return r + c + r + 256;
 }
 
+// The two words reset to kNoFault (first suspect cell, first flagged row) sit in a fixed
+// 256-byte head, and the generation-tagged words folded with atomicMax (row and column
+// exponents, row flags) after it. Calls of different shapes reuse one buffer, so a word of
+// one call can lie where another call keeps a different word; kNoFault (all ones) would
+// outrank every later word under atomicMax, so it must never lie in the tagged part.
 MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols)
 {
     char *p = (char *)base;
     size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     size_t c = ((cols * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     MatmulScratch s;
-    s.row_exp = (unsigned long long *)p;
-    s.col_exp = (unsigned long long *)(p + r);
-    s.suspect = (unsigned long long *)(p + r + c);
+    s.suspect = (unsigned long long *)p;
+    s.flag_first = s.suspect + 1;
+    s.row_exp = (unsigned long long *)(p + 256);
+    s.col_exp = (unsigned long long *)(p + 256 + r);
+    s.row_flag = (unsigned long long *)(p + 256 + r + c);
     return s;
 }
 
@@ -609,6 +855,22 @@ static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C
         hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
 }
 
+template <typename T, bool TA, bool TB>
+static void tiny_scan_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, int M, int N,
+                               int K, const MatmulScratch &sc, int thr, NodeGate gate)
+{
+    const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    if (va && vb)
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+    else if (va)
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+    else if (vb)
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+    else
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+}
+
 template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
@@ -634,7 +896,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate);
     } else {
         risk = 0; // AllowGradual, or an empty reduction: no underflow screen
-        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)1, (unsigned long long)kNoFault);
+        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)2, (unsigned long long)kNoFault);
     }
     dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)));
     const int m = (int)M, n = (int)N, k = (int)K;
@@ -652,9 +914,22 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         return e;
     if (ev)
         (void)hipEventRecord(ev[2], s);
+    // Under the IEEE policy a finite cell's first fault is a tiny-inexact product: the tiled
+    // scan narrows the screen's marks to the cells that have one, for the wave-parallel pass.
+    // Under RejectSubnormal a subnormal partial sum also faults, so the serial pass walks
+    // every marked cell.
+    const bool tiny = risk && policy == kPolicyIeee;
+    if (tiny) {
+        if (!ta && !tb) tiny_scan_dispatch<T, false, false>(s, grid, A, B, m, n, k, sc, thr, gate);
+        else if (!ta && tb) tiny_scan_dispatch<T, false, true>(s, grid, A, B, m, n, k, sc, thr, gate);
+        else if (ta && !tb) tiny_scan_dispatch<T, true, false>(s, grid, A, B, m, n, k, sc, thr, gate);
+        else tiny_scan_dispatch<T, true, true>(s, grid, A, B, m, n, k, sc, thr, gate);
+    }
+    const int serial_screen = risk && !tiny;
     hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(1024), dim3(256), 0, s, A, B, (const T *)C, M, N, K,
-                       (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, risk, policy,
-                       (const unsigned long long *)sc.suspect, fault, gate);
+                       (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, serial_screen, (int)tiny, policy,
+                       (const unsigned long long *)sc.suspect, (const unsigned long long *)sc.row_flag,
+                       (const unsigned long long *)sc.flag_first, sc.gen, fault, gate);
     if (ev)
         (void)hipEventRecord(ev[3], s);
     return hipGetLastError();

@@ -41,14 +41,17 @@ hipError_t launch_mse_prepare(hipStream_t s, int dtype, uint64_t n, const void *
 hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, double count,
                            void *out, int policy, unsigned long long *fault, NodeGate gate);
 
-// Strict MatMul scratch: per-row and per-column minimum exponents plus one suspect word.
-// Exponent words (generation << 32 | bias - minimum exponent) of op(A) rows and op(B)
-// columns, the first suspect cell, and the screen's generation: a context increases it per
-// MatMul and clears the words when it wraps or the scratch is new.
+// Strict MatMul scratch. Exponent words (generation << 32 | bias - minimum exponent) of
+// op(A) rows and op(B) columns; per output row, the first column whose cell has a product
+// that may be tiny (generation << 32 | 0xffffffff - column, folded with atomicMax); the
+// first suspect cell; the first row holding such a cell; and the screen's generation: a
+// context increases it per MatMul and clears the words when it wraps or the scratch is new.
 struct MatmulScratch {
-    unsigned long long *row_exp; // rows entries
-    unsigned long long *col_exp; // cols entries
-    unsigned long long *suspect; // first suspect cell (kNoFault when none)
+    unsigned long long *row_exp;    // rows entries
+    unsigned long long *col_exp;    // cols entries
+    unsigned long long *row_flag;   // rows entries
+    unsigned long long *suspect;    // first suspect cell (kNoFault when none)
+    unsigned long long *flag_first; // first row with a flagged cell (kNoFault when none)
     uint32_t gen = 1;
 };
 size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);

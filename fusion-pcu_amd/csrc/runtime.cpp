@@ -18,14 +18,15 @@
 #include <unordered_set>
 
 // ------------------------------------------- scratch of the no-allocation strict MatMul
-// pcu_strict_matmul_noalloc keeps the exponent screen's words (one per row of op(A) and one
-// per column of op(B), then the first-suspect word) in this array instead of the context's
-// pool, so that call allocates nothing. Its size is matmul_scratch_bytes(rows, cols) at the
-// largest admitted shape: 8 * 65536 bytes of row words, the same of column words, and 256
-// bytes, i.e. 1 MiB + 256 B, which each device keeps until the process ends. In host code
+// pcu_strict_matmul_noalloc keeps the MatMul screen's words (one exponent word per row of
+// op(A) and per column of op(B), one flag word per output row, then the first-suspect and
+// first-flagged-row words) in this array instead of the context's pool, so that call
+// allocates nothing. Its size is matmul_scratch_bytes(rows, cols) at the largest admitted
+// shape: three runs of 8 * 65536 bytes and 256 bytes, i.e. 1.5 MiB + 256 B, which each device
+// keeps until the process ends. In host code
 // `scratch` is a host-side stand-in: only the address hipGetSymbolAddress returns for the
 // current device (kept per device in g_noalloc) may reach a kernel, a fill or a copy.
-static constexpr size_t kNoAllocScratchWords = 2 * (size_t)PCU_NOALLOC_MAX_DIM + 32;
+static constexpr size_t kNoAllocScratchWords = 3 * (size_t)PCU_NOALLOC_MAX_DIM + 32;
 static __device__ __align__(256) unsigned long long scratch[kNoAllocScratchWords];
 
 namespace {

@@ -165,7 +165,7 @@ pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint6
  * of the library on each device instead of the context's pool, so the call allocates
  * nothing (no hipMalloc, hipFree or pool allocation; it is never per-kernel timed). rows and
  * cols are each at most PCU_NOALLOC_MAX_DIM; larger shapes return PCU_ERR_ARGUMENT. The
- * array (1 MiB + 256 B per device, held until the process ends) is shared by every call on
+ * array (1.5 MiB + 256 B per device, held until the process ends) is shared by every call on
  * the device and keeps the last call's contents; the library clears what must start at zero.
  * Calls that overlap on one device (from two contexts or two host threads) race. */
 #define PCU_NOALLOC_MAX_DIM 65536u

@@ -714,3 +714,87 @@ def test_output_overlapping_an_operand_is_rejected(ctx, pcu_pkg):
     want2, wf2 = oracle.relu(want)
     assert wf2 is None
     np.testing.assert_array_equal(_bits(dw.numpy()), _bits(want2))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_replay_paths_for_marked_cells(ctx, pcu_pkg, dtype, engine):
+    """The replay's two passes under the IEEE policy, every layout, against the oracle:
+    (a) every cell marked by the exponent screen, no tiny product, no fault (the tiled tiny
+    scan clears everything); (b) every row flagged by exact subnormal products (no fault)
+    before a tiny-inexact product at cell (17, 33), k 9, so the wave pass walks flagged but
+    clean cells first; (c) a NaN in row 40 and an inexact tiny product in row 50: the serial
+    pass's Invalid wins; (d) the same with the tiny product moved to row 10: the wave pass's
+    Underflow wins."""
+    f32 = dtype == np.float32
+    m, k, n = 300, 200, 260
+    rng = np.random.default_rng(123 if f32 else 124)
+    p2 = lambda e: dtype(2.0 ** e)
+    clean_e = -120 if f32 else -1016
+    exact_a, exact_b = (-100, -40) if f32 else (-1000, -60)
+    inexact_a, inexact_b = (-100, -30) if f32 else (-1000, -40)
+
+    def base():
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        return a, b
+
+    cases = []
+    a, b = base()
+    a[:, 5] = p2(clean_e) * np.where(rng.random(m) < 0.5, -1, 1).astype(dtype)
+    b[5, :] = (rng.uniform(0.5, 1.0, n) * np.where(rng.random(n) < 0.5, -1, 1)).astype(dtype)
+    cases.append(("clean", a, b))
+    a, b = base()
+    a[:, 5], b[5, :] = p2(exact_a), p2(exact_b)
+    a[17, 9], b[9, 33] = dtype(1.5) * p2(inexact_a), dtype(1.3) * p2(inexact_b)
+    cases.append(("exact-then-inexact", a, b))
+    for row, name in ((50, "serial-wins"), (10, "tiny-wins")):
+        a, b = base()
+        a[40, 3] = np.nan
+        a[row, 9], b[9, 33] = dtype(1.5) * p2(inexact_a), dtype(1.3) * p2(inexact_b)
+        cases.append((name, a, b))
+    for name, a, b in cases:
+        for tl in (False, True):
+            for tr in (False, True):
+                aa = np.ascontiguousarray(a.T) if tl else a
+                bb = np.ascontiguousarray(b.T) if tr else b
+                got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), tl, tr, 0).numpy())
+                ref, rf = oracle.matmul(aa, bb, tl, tr, policy=0)
+                assert gf == _ofault(rf), (name, tl, tr, gf, rf)
+                if rf is None:
+                    np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{name} {tl} {tr}")
+        if name == "clean":
+            assert rf is None
+        elif name == "exact-then-inexact":
+            assert _ofault(rf)[:2] == (17 * n + 33, 9)
+
+
+@pytest.mark.parametrize("policy", [0, 1], ids=["ieee", "reject_subnormal"])
+def test_matmul_screen_after_calls_of_other_shapes(ctx, pcu_pkg, policy, engine):
+    """Regression: MatMul calls of different shapes share one scratch buffer. A word that one
+    call leaves at its "none" value (all ones) must never sit where a later call folds
+    generation-tagged words with atomicMax (a column's minimum exponent, a row's first
+    flagged column): nothing outranks it there, and that column or row was never screened.
+    Each column c of a small output gets its own pair of calls: a clean call of another
+    shape, then one whose only fault is a tiny inexact product in row 0, column c, at k 3."""
+    rng = np.random.default_rng(41)
+    rows, inner, cols = 8, 16, 80
+    clean = {}
+    for shape in ((8, 8), (8, 40), (8, 72), (16, 8), (24, 40), (40, 8)):
+        a = rng.uniform(-1, 1, (shape[0], 12)).astype(np.float32)
+        b = rng.uniform(-1, 1, (12, shape[1])).astype(np.float32)
+        clean[shape] = (ctx.upload(a), ctx.upload(b))
+    a = rng.uniform(-1, 1, (rows, inner)).astype(np.float32)
+    a[0, 3] = np.float32(1.5 * 2.0 ** -100)
+    da = ctx.upload(a)
+    for c in range(cols):
+        b = rng.uniform(-1, 1, (inner, cols)).astype(np.float32)
+        b[3, :] = np.float32(1.0)
+        b[3, c] = np.float32(1.3 * 2.0 ** -30)
+        db = ctx.upload(b)
+        for shape, (ca, cb) in clean.items():
+            ctx.strict_matmul(ca, cb, policy=policy).free()
+            _, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(da, db, policy=policy).numpy())
+            assert gf == (c, 3, 1, 4), (shape, c, gf)
+        db.free()
+    _, rf = oracle.matmul(a, b, policy=policy)
+    assert _ofault(rf) == (cols - 1, 3, 1, 4)
