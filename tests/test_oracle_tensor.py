@@ -180,3 +180,35 @@ def test_first_fault_order_brute_force():
         _, f = oracle.matmul(a, b, fast=False)
         assert (f.element_index, f.reduction_index, f.step, f.kind) == \
             (r0 * n, max(k0, k1), 2, 3)
+
+
+def test_c5_fixture_first_step_matches_the_oracle():
+    """tests/golden/c5_100_steps.json starts where the committed oracle does: step 0's loss
+    and weight digests are recomputed here (about 15 s on 8 host cores)."""
+    import hashlib
+    import importlib.util
+    import json
+    import os
+    from oracle import graph as og
+    here = os.path.dirname(os.path.abspath(__file__))
+    fixture = json.load(open(os.path.join(here, "golden", "c5_100_steps.json")))
+    path = os.path.join(os.path.dirname(here), "fusion-pcu_amd", "synthetic.py")
+    spec = importlib.util.spec_from_file_location("pcu_synthetic_c5", path)
+    syn = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(syn)
+    dims, batch = (1024, 4096, 4096, 1024), 4096
+    s = fixture["seeds"]
+    x = syn.uniform(s["x"], (batch, dims[0]), np.float32)
+    y = syn.uniform(s["y"], (batch, dims[3]), np.float32)
+    ws = [syn.xavier_uniform(s["w"][i], dims[i], dims[i + 1], np.float32) for i in range(3)]
+    g, ids = og.mlp_graph(dims, batch, np.float32, 1e-3)
+    vals, fault = g.evaluate({ids["x"]: x, ids["w1"]: ws[0], ids["w2"]: ws[1], ids["w3"]: ws[2],
+                              ids["y"]: y}, ids["outputs"])
+    assert fault is None
+    first = fixture["steps"][0]
+    loss = vals[ids["outputs"][3]]
+    assert "0x%08x" % int(np.asarray(loss, np.float32).view(np.uint32)) == first["loss"]
+    for i in range(3):
+        w = vals[ids["outputs"][i]]
+        assert hashlib.sha256(np.ascontiguousarray(w, dtype="<f4").tobytes()).hexdigest() == \
+            first["w_sha256"][i]
