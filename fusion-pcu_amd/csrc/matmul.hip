@@ -470,6 +470,140 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
         wave_record_fault(key, suspect);
 }
 
+// ------------------------------------------------------- binary64, narrow tile
+// Strict binary64 on a 128 x 64 output tile per 256-thread workgroup, 8 x 4 per thread:
+// 131-135 VGPRs, so three workgroups (three waves per SIMD) share a CU, against two for the
+// 8 x 8 block. It serves outputs with fewer than 256 tiles of 128 x 128, less than one
+// workgroup per CU: twice the tiles then fill the machine (1000^3: 216 us against 298). On
+// full grids the 8 x 8 block is faster (4096^3: 4.34 against 4.55 ms; the narrow block reads
+// half again as many operands from LDS per product).
+struct NarrowF64Cfg {
+    static constexpr int BM = 128, BN = 64, BK = 16;
+    static constexpr int kThreads = 256;
+    static constexpr int LDA = BM + 4, LDB = BN + 4;
+    static constexpr int EA = BM * BK / kThreads, EB = BN * BK / kThreads; // 8 and 4
+    // A thread's 4 elements of a B k-row as two 16-byte runs 32 apart (adjacent lanes then
+    // store adjacent runs) when A is untransposed.
+    template <bool TA> static constexpr bool kSplitRunsB = !TA;
+};
+
+template <bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
+__global__ __launch_bounds__(256, 3) void k_strict_gemm_f64n(
+    const double *__restrict__ A, const double *__restrict__ B, double *__restrict__ C, int M,
+    int N, int K, const unsigned long long *__restrict__ row_exp,
+    const unsigned long long *__restrict__ col_exp, int thr, int check_risk, int vec_c,
+    unsigned long long *suspect, NodeGate gate)
+{
+    if (block_gate_closed(gate))
+        return;
+    using Cfg = NarrowF64Cfg;
+    constexpr int BK = Cfg::BK, TBM = Cfg::BM, TBN = Cfg::BN;
+    __shared__ __align__(16) double As[2][BK][Cfg::LDA];
+    __shared__ __align__(16) double Bs[2][BK][Cfg::LDB];
+
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+    // The lane's 4 columns: 2 runs of 2 adjacent doubles, 32 apart, so each 16-byte LDS read
+    // of B covers 256 contiguous bytes over the 16 lanes of a row (no bank conflicts).
+    auto col_of = [&](int j) { return (j / 2) * 32 + tx * 2 + (j % 2); };
+
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * TBM, n0 = tile_n * TBN;
+
+    double acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            acc[i][j] = 0.0;
+
+    SlabStager<double, Cfg, TA, TB, VA, VB> stage;
+    const int ktiles = (K + BK - 1) / BK;
+    if (WHOLE)
+        stage.begin_whole(A, B, M, N, K, m0, n0, tid);
+    if (ktiles > 0) {
+        if (WHOLE)
+            stage.fetch_whole();
+        else
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+        stage.stash(As[0], Bs[0], tid);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles) {
+            if (WHOLE)
+                stage.fetch_whole();
+            else
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        }
+#pragma unroll 2
+        for (int k = 0; k < BK; k++) {
+            double a[8], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[i] = As[cur][k][ty * 4 + i];
+                a[4 + i] = As[cur][k][64 + ty * 4 + i];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                b[j] = Bs[cur][k][col_of(j)];
+            // Per row, the four rounded products first and then their rounded sums.
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                double p[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    p[j] = a[i] * b[j];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = acc[i][j] + p[j];
+            }
+        }
+        if (kt + 1 < ktiles)
+            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+        __syncthreads();
+    }
+
+    uint64_t key = kNoFault;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+        if (r >= M)
+            continue;
+        const int rexp = check_risk ? exp_of(row_exp[r]) : 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c0 = n0 + col_of(2 * h);
+            double *dst = C + (size_t)r * N + c0;
+            if (vec_c && c0 + 2 <= N) {
+                *reinterpret_cast<double2 *>(dst) = make_double2(acc[i][2 * h], acc[i][2 * h + 1]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    if (c0 + j < N)
+                        dst[j] = acc[i][2 * h + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int c = c0 + j;
+                if (c >= N)
+                    continue;
+                bool bad = !finite_bits(acc[i][2 * h + j]);
+                if (check_risk)
+                    bad |= rexp + exp_of(col_exp[c]) < thr;
+                if (bad) {
+                    const uint64_t cell = (uint64_t)r * N + c;
+                    key = cell < key ? cell : key;
+                }
+            }
+        }
+    }
+    wave_record_fault(key, suspect);
+}
+
 // ------------------------------------------------------------------ tiny scan
 // IEEE policy. A cell whose result is finite met no invalid operand and no overflow (both
 // leave Inf or NaN for good), and a sum is never tiny-inexact, so its first fault can only
@@ -871,6 +1005,28 @@ static void tiny_scan_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B,
         hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
 }
 
+template <bool TA, bool TB>
+static void f64n_dispatch(hipStream_t s, const double *A, const double *B, double *C, int M,
+                          int N, int K, const unsigned long long *re, const unsigned long long *ce,
+                          int thr, int risk, unsigned long long *suspect, NodeGate gate)
+{
+    using Cfg = NarrowF64Cfg;
+    const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
+    const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    const int vc = (N % 2 == 0) && aligned16(C);
+    if (va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0)
+        hipLaunchKernelGGL((k_strict_gemm_f64n<TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+    else if (va && vb)
+        hipLaunchKernelGGL((k_strict_gemm_f64n<TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+    else if (va)
+        hipLaunchKernelGGL((k_strict_gemm_f64n<TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+    else if (vb)
+        hipLaunchKernelGGL((k_strict_gemm_f64n<TA, TB, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+    else
+        hipLaunchKernelGGL((k_strict_gemm_f64n<TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+}
+
 template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
@@ -905,6 +1061,13 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (f32 && engine != kEngineValu) {
         (void)launch_gemm_mfma_f32(s, m, n, k, ta, tb, (const float *)A, (const float *)B,
                                    (float *)C, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    } else if (!f32 && (uint64_t)grid.x < 256) {
+        const double *dA = (const double *)A, *dB = (const double *)B;
+        double *dC = (double *)C;
+        if (!ta && !tb) f64n_dispatch<false, false>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else if (!ta && tb) f64n_dispatch<false, true>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else if (ta && !tb) f64n_dispatch<true, false>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else f64n_dispatch<true, true>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
     } else if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
     else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
     else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);

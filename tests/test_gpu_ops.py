@@ -798,3 +798,29 @@ def test_matmul_screen_after_calls_of_other_shapes(ctx, pcu_pkg, policy, engine)
         db.free()
     _, rf = oracle.matmul(a, b, policy=policy)
     assert _ofault(rf) == (cols - 1, 3, 1, 4)
+
+
+@pytest.mark.parametrize("shape", [(2048, 64, 2048), (2080, 33, 2050)], ids=["whole", "ragged"])
+def test_matmul_f64_full_grid_tile(ctx, pcu_pkg, shape):
+    """Binary64 outputs of at least 256 tiles of 128 x 128 take the 8 x 8-per-thread tile
+    (smaller ones the 8 x 4 tile that the other tests reach): every layout, clean and with
+    planted NaN, overflow and tiny-inexact operands, against the oracle."""
+    m, k, n = shape
+    rng = np.random.default_rng(m + k + n)
+    for tl in (False, True):
+        for tr in (False, True):
+            a = rng.uniform(-1, 1, (k, m) if tl else (m, k))
+            b = rng.uniform(-1, 1, (n, k) if tr else (k, n))
+            for plant in (None, "nan", "huge", "tiny"):
+                aa, bb = a.copy(), b.copy()
+                if plant == "nan":
+                    aa.reshape(-1)[rng.integers(aa.size)] = np.nan
+                elif plant == "huge":
+                    aa.reshape(-1)[rng.choice(aa.size, 64, replace=False)] = 1.5e308
+                elif plant == "tiny":
+                    bb.reshape(-1)[rng.choice(bb.size, 8, replace=False)] = 1.3 * 2.0 ** -1040
+                got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), tl, tr, 0).numpy())
+                ref, rf = oracle.matmul(aa, bb, tl, tr, policy=0)
+                assert gf == _ofault(rf), (shape, tl, tr, plant, gf, rf)
+                if rf is None:
+                    np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{shape} {tl} {tr}")
