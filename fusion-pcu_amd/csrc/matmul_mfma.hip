@@ -60,8 +60,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         return;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
     constexpr int S = SM * SN;
-    __shared__ __align__(16) float As[2][BK][Cfg::LDA];
-    __shared__ __align__(16) float Bs[2][BK][Cfg::LDB];
+    // Whole tiles run three LDS stages (see the slab loop); tiles with bound checks keep two,
+    // since their staging needs more registers and three spill there.
+    constexpr int kStages = WHOLE ? 3 : 2;
+    __shared__ __align__(16) float As[kStages][BK][Cfg::LDA];
+    __shared__ __align__(16) float Bs[kStages][BK][Cfg::LDB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
@@ -83,10 +86,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 #pragma unroll
     for (int r = 0; r < 32; r++)
         zero[r] = 0.0f;
-    // Raising the wave's priority around each MFMA issue measured about 0.8% faster at
-    // 4096^3 when op(A) and op(B) are staged alike (both transposed or neither) and about
-    // 0.4% slower otherwise, so it is used only there.
-    constexpr bool kIssuePrio = TA == TB;
+    // With two stages, raising the wave's priority around each MFMA issue measured about
+    // 0.8% faster at 4096^3 when op(A) and op(B) are staged alike (both transposed or
+    // neither) and about 0.4% slower otherwise, so it is used only there. With three stages
+    // it measured 1.7-4% slower in every layout.
+    constexpr bool kIssuePrio = !WHOLE && TA == TB;
     auto mma = [&](float a, float b) {
         if (kIssuePrio)
             __builtin_amdgcn_s_setprio(1);
@@ -114,58 +118,121 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     const int ktiles = (K + BK - 1) / BK;
     if (WHOLE)
         stage.begin_whole(A, B, M, N, K, m0, n0, tid);
-    if (ktiles > 0) {
-        if (WHOLE)
-            stage.fetch_whole();
-        else
-            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
-        stage.stash(As[0], Bs[0], tid);
-    }
-    __syncthreads();
     const int half = lane >> 5, col = lane & 31;
-    for (int kt = 0; kt < ktiles; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) {
+    if constexpr (kStages == 3) {
+        // Three LDS stages: while slab kt is computed from stage kt % 3, slab kt + 1 is already
+        // published (stashed during kt - 1, before that iteration's barrier) and slab kt + 2 is
+        // staged into the stage slab kt - 1 used. So each wave reads slab kt + 1's first operands
+        // and issues its first MFMA before the barrier that ends slab kt: the MFMA runs while
+        // the wave waits there, and no slab starts from an empty pipeline.
+        for (int s0 = 0; s0 < 2 && s0 < ktiles; s0++) {
+            stage.fetch_whole();
+            stage.stash(As[s0], Bs[s0], tid);
+        }
+        __syncthreads();
+        // Software pipeline over the slab, unrolled: each MFMA is issued, then the products of
+        // the one before it are folded. sched_barrier pins that order (left to the scheduler,
+        // the same sequence measured about 8% slower), and each k-pair's operands are read from
+        // LDS one pair ahead into the other of two register slots. Lanes 0-31 carry k = 2j,
+        // lanes 32-63 carry k = 2j + 1 (the MFMA's two blocks).
+        constexpr int NP = BK / 2;
+        static_assert(NP % 2 == 0, "a slab's first pair takes register slot 0");
+        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
+        float oa[2][SM], ob[2][SN];
+        auto rd = [&](int st, int j) {
+#pragma unroll
+            for (int i = 0; i < SM; i++)
+                oa[j & 1][i] = As[st][2 * j + half][wm + 32 * i + col];
+#pragma unroll
+            for (int jj = 0; jj < SN; jj++)
+                ob[j & 1][jj] = Bs[st][2 * j + half][wn + 32 * jj + col];
+        };
+        v32f p;
+        if (ktiles > 0) {
+            rd(0, 0);
+            p = mma(oa[0][0], ob[0][0]);
+        }
+        int cur = 0;
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
+            const bool has_next = kt + 1 < ktiles;
+            if (kt + 2 < ktiles)
+                stage.fetch_whole();
+#pragma unroll
+            for (int j = 0; j < NP; j++) {
+                if (j + 1 < NP)
+                    rd(cur, j + 1);
+                else if (has_next)
+                    rd(nxt, 0);
+                const v32f q = mma(oa[j & 1][0], ob[j & 1][1]);
+                __builtin_amdgcn_sched_barrier(0);
+                fold(acc[0], p);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j + 1 < NP || has_next)
+                    p = mma(oa[(j + 1) & 1][0], ob[(j + 1) & 1][0]);
+                __builtin_amdgcn_sched_barrier(0);
+                fold(acc[1], q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (kt + 2 < ktiles)
+                stage.stash(As[nn], Bs[nn], tid);
+            __syncthreads();
+            cur = nxt;
+        }
+    } else {
+        if (ktiles > 0) {
             if (WHOLE)
                 stage.fetch_whole();
             else
-                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+                stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+            stage.stash(As[0], Bs[0], tid);
         }
-        // Software pipeline over the whole slab, unrolled: each MFMA is issued, then the
-        // products of the one before it are folded. sched_barrier pins that order (left to
-        // the scheduler, the same sequence measured about 8% slower), and each k-pair's
-        // operands are read from LDS one pair ahead. Lanes 0-31 carry k = 2j, lanes 32-63
-        // carry k = 2j + 1 (the MFMA's two blocks).
-        constexpr int NP = BK / 2;
-        float oa[NP][SM], ob[NP][SN];
-        auto rd = [&](int j) {
-#pragma unroll
-            for (int i = 0; i < SM; i++)
-                oa[j][i] = As[cur][2 * j + half][wm + 32 * i + col];
-#pragma unroll
-            for (int jj = 0; jj < SN; jj++)
-                ob[j][jj] = Bs[cur][2 * j + half][wn + 32 * jj + col];
-        };
-        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
-        rd(0);
-        v32f p = mma(oa[0][0], ob[0][0]);
-#pragma unroll
-        for (int j = 0; j < NP; j++) {
-            if (j + 1 < NP)
-                rd(j + 1);
-            const v32f q = mma(oa[j][0], ob[j][1]);
-            __builtin_amdgcn_sched_barrier(0);
-            fold(acc[0], p);
-            __builtin_amdgcn_sched_barrier(0);
-            if (j + 1 < NP)
-                p = mma(oa[j + 1][0], ob[j + 1][0]);
-            __builtin_amdgcn_sched_barrier(0);
-            fold(acc[1], q);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (kt + 1 < ktiles)
-            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
         __syncthreads();
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int cur = kt & 1;
+            if (kt + 1 < ktiles) {
+                if (WHOLE)
+                    stage.fetch_whole();
+                else
+                    stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+            }
+            // Software pipeline over the whole slab, unrolled: each MFMA is issued, then the
+            // products of the one before it are folded. sched_barrier pins that order (left to
+            // the scheduler, the same sequence measured about 8% slower), and each k-pair's
+            // operands are read from LDS one pair ahead. Lanes 0-31 carry k = 2j, lanes 32-63
+            // carry k = 2j + 1 (the MFMA's two blocks).
+            constexpr int NP = BK / 2;
+            float oa[NP][SM], ob[NP][SN];
+            auto rd = [&](int j) {
+#pragma unroll
+                for (int i = 0; i < SM; i++)
+                    oa[j][i] = As[cur][2 * j + half][wm + 32 * i + col];
+#pragma unroll
+                for (int jj = 0; jj < SN; jj++)
+                    ob[j][jj] = Bs[cur][2 * j + half][wn + 32 * jj + col];
+            };
+            static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
+            rd(0);
+            v32f p = mma(oa[0][0], ob[0][0]);
+#pragma unroll
+            for (int j = 0; j < NP; j++) {
+                if (j + 1 < NP)
+                    rd(j + 1);
+                const v32f q = mma(oa[j][0], ob[j][1]);
+                __builtin_amdgcn_sched_barrier(0);
+                fold(acc[0], p);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j + 1 < NP)
+                    p = mma(oa[j + 1][0], ob[j + 1][0]);
+                __builtin_amdgcn_sched_barrier(0);
+                fold(acc[1], q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (kt + 1 < ktiles)
+                stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+            __syncthreads();
+        }
+
     }
 
     // Epilogue: for subtile (i, j) the lane owns column n0+wn+32j+col of rows
