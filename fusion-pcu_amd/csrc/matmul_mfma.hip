@@ -32,7 +32,7 @@ namespace pcu {
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 // Workgroup shape: WM x WN waves, each owning SM x SN output subtiles of 32 x 32; k-slabs
-// of BK are staged through double-buffered k-major LDS tiles.
+// of BK are staged through k-major LDS tiles (two or three stages).
 template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> struct MfmaCfg {
     static constexpr int WM = WM_, WN = WN_, SM = SM_, SN = SN_, BK = BK_;
     static constexpr int kWavesPerSimd = WAVES_PER_SIMD_; // occupancy the registers allow
@@ -125,6 +125,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // staged into the stage slab kt - 1 used. So each wave reads slab kt + 1's first operands
         // and issues its first MFMA before the barrier that ends slab kt: the MFMA runs while
         // the wave waits there, and no slab starts from an empty pipeline.
+        //
+        // Lane col of the wave's subtile j owns tile column wn + 2 col + j, so its
+        // two B operands of a k row sit side by side and one 8-byte LDS read, at an immediate
+        // offset from the lane's base, fetches both.
+        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
         for (int s0 = 0; s0 < 2 && s0 < ktiles; s0++) {
             stage.fetch_whole();
             stage.stash(As[s0], Bs[s0], tid);
@@ -137,39 +142,39 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // lanes 32-63 carry k = 2j + 1 (the MFMA's two blocks).
         constexpr int NP = BK / 2;
         static_assert(NP % 2 == 0, "a slab's first pair takes register slot 0");
-        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
-        float oa[2][SM], ob[2][SN];
-        auto rd = [&](int st, int j) {
-#pragma unroll
-            for (int i = 0; i < SM; i++)
-                oa[j & 1][i] = As[st][2 * j + half][wm + 32 * i + col];
-#pragma unroll
-            for (int jj = 0; jj < SN; jj++)
-                ob[j & 1][jj] = Bs[st][2 * j + half][wn + 32 * jj + col];
+        float oa[2], ob[2][2];
+        auto rd = [&](auto st_c, int j) {
+            constexpr int st = decltype(st_c)::value;
+            oa[j & 1] = As[st][2 * j + half][wm + col];
+            const float2 v = *reinterpret_cast<const float2 *>(&Bs[st][2 * j + half][wn + 2 * col]);
+            ob[j & 1][0] = v.x;
+            ob[j & 1][1] = v.y;
         };
         v32f p;
         if (ktiles > 0) {
-            rd(0, 0);
-            p = mma(oa[0][0], ob[0][0]);
+            rd(std::integral_constant<int, 0>{}, 0);
+            p = mma(oa[0], ob[0][0]);
         }
-        int cur = 0;
-        for (int kt = 0; kt < ktiles; kt++) {
-            const int nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
+        // One slab computed from stage CUR; the loop below runs three slabs per trip, so every
+        // stage index, and with it every LDS address, is fixed at compile time.
+        auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+            constexpr int cur = decltype(cur_c)::value, nn = (cur + 2) % 3;
+            const std::integral_constant<int, (cur + 1) % 3> nxt_c;
             const bool has_next = kt + 1 < ktiles;
             if (kt + 2 < ktiles)
                 stage.fetch_whole();
 #pragma unroll
             for (int j = 0; j < NP; j++) {
                 if (j + 1 < NP)
-                    rd(cur, j + 1);
+                    rd(cur_c, j + 1);
                 else if (has_next)
-                    rd(nxt, 0);
-                const v32f q = mma(oa[j & 1][0], ob[j & 1][1]);
+                    rd(nxt_c, 0);
+                const v32f q = mma(oa[j & 1], ob[j & 1][1]);
                 __builtin_amdgcn_sched_barrier(0);
                 fold(acc[0], p);
                 __builtin_amdgcn_sched_barrier(0);
                 if (j + 1 < NP || has_next)
-                    p = mma(oa[(j + 1) & 1][0], ob[(j + 1) & 1][0]);
+                    p = mma(oa[(j + 1) & 1], ob[(j + 1) & 1][0]);
                 __builtin_amdgcn_sched_barrier(0);
                 fold(acc[1], q);
                 __builtin_amdgcn_sched_barrier(0);
@@ -177,7 +182,13 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             if (kt + 2 < ktiles)
                 stage.stash(As[nn], Bs[nn], tid);
             __syncthreads();
-            cur = nxt;
+        };
+        for (int kt = 0; kt < ktiles; kt += 3) {
+            slab(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < ktiles)
+                slab(std::integral_constant<int, 1>{}, kt + 1);
+            if (kt + 2 < ktiles)
+                slab(std::integral_constant<int, 2>{}, kt + 2);
         }
     } else {
         if (ktiles > 0) {
@@ -235,9 +246,34 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 
     }
 
-    // Epilogue: for subtile (i, j) the lane owns column n0+wn+32j+col of rows
-    // m0+wm+32i+8(r/4)+4*half+(r%4).
+    // Epilogue: for subtile (i, j) the lane owns rows m0+wm+32i+8(r/4)+4*half+(r%4) of column
+    // n0+wn+2col+j (three stages: both columns in one 8-byte store, every cell inside M x N)
+    // or n0+wn+32j+col.
     uint64_t key = kNoFault;
+    if constexpr (kStages == 3) {
+        const int c = n0 + wn + 2 * col;
+        const int cexp0 = check_risk ? exp_of(col_exp[c]) : 0;
+        const int cexp1 = check_risk ? exp_of(col_exp[c + 1]) : 0;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
+            const float v0 = acc[0][r], v1 = acc[1][r];
+            *reinterpret_cast<float2 *>(&C[(size_t)row * N + c]) = make_float2(v0, v1);
+            bool bad0 = !finite_bits(v0), bad1 = !finite_bits(v1);
+            if (check_risk) {
+                const int rexp = exp_of(row_exp[row]);
+                bad0 |= rexp + cexp0 < thr;
+                bad1 |= rexp + cexp1 < thr;
+            }
+            const uint64_t cell = (uint64_t)row * N + c;
+            if (bad0)
+                key = cell < key ? cell : key;
+            else if (bad1)
+                key = cell + 1 < key ? cell + 1 : key;
+        }
+        wave_record_fault(key, suspect);
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < S; t++) {
         const int i = t / SN, j = t % SN;
@@ -274,7 +310,9 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0;
+    // Whole tiles store C two floats at a time.
+    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
+                       ((uintptr_t)C & 7u) == 0;
     if (whole)
         hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else if (va && vb)

@@ -374,7 +374,10 @@ def engine(request, ctx):
                                    (129, 67, 255), (300, 257, 130), (512, 1024, 256),
                                    (33, 1, 257), (1, 513, 1), (255, 17, 129),
                                    # whole-slab kernels: one slab, and whole in two of three
-                                   (128, 16, 128), (256, 32, 384), (256, 48, 130), (130, 64, 256)])
+                                   (128, 16, 128), (256, 32, 384), (256, 48, 130), (130, 64, 256),
+                                   # whole, with 3, 4 and 6 slabs (every trip count of the
+                                   # three-stage slab loop)
+                                   (128, 48, 128), (256, 64, 128), (128, 96, 256)])
 def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape, engine):
     m, k, n = shape
     rng = np.random.default_rng(m * 7 + k * 3 + n)
