@@ -47,6 +47,13 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
     template <bool TA> static constexpr bool kSplitRunsB = EB > 4;
 };
 
+// Direct global -> LDS load of 16 bytes a lane: lane l's run lands at lds + 16 l bytes (lds is
+// the wave's base, uniform across the wave).
+__device__ __forceinline__ void load_lds16(const float *g, float *lds)
+{
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
 // WHOLE: every slab of every tile is whole (M, N, K multiples of the tile and slab, 16-byte
 // loads allowed), so staging runs on advancing pointers with no bound checks.
 template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
@@ -63,8 +70,42 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // Whole tiles run three LDS stages (see the slab loop); tiles with bound checks keep two,
     // since their staging needs more registers and three spill there.
     constexpr int kStages = WHOLE ? 3 : 2;
-    __shared__ __align__(16) float As[kStages][BK][Cfg::LDA];
-    __shared__ __align__(16) float Bs[kStages][BK][Cfg::LDB];
+    // Whole tiles with op(B) untransposed load both operands from global memory straight into
+    // LDS (global_load_lds_dwordx4: no staging registers, no LDS stores); their stages are
+    // unpadded (see the layouts at the direct loads below).
+    constexpr bool kDirect = WHOLE && !TB;
+    constexpr int LDA = kDirect ? BM : Cfg::LDA, LDB = kDirect ? BN : Cfg::LDB;
+    // Two stages are indexed at run time, three at compile time. With direct loads each of the
+    // three stages is an LDS object of its own, so the compiler can tell a direct load into one
+    // stage from the reads of another (with one array it waits for the load before every read).
+    __shared__ __align__(16) float As[2][BK][LDA];
+    __shared__ __align__(16) float Bs[2][BK][LDB];
+    __shared__ __align__(16) float As3[3][BK][LDA];
+    __shared__ __align__(16) float Bs3[3][BK][LDB];
+    __shared__ __align__(16) float A0[BK][LDA], A1[BK][LDA], A2[BK][LDA];
+    __shared__ __align__(16) float B0[BK][LDB], B1[BK][LDB], B2[BK][LDB];
+    auto sa = [&](auto st_c) -> float(*)[LDA] {
+        constexpr int st = decltype(st_c)::value;
+        if constexpr (!kDirect)
+            return As3[st];
+        else if constexpr (st == 0)
+            return A0;
+        else if constexpr (st == 1)
+            return A1;
+        else
+            return A2;
+    };
+    auto sb = [&](auto st_c) -> float(*)[LDB] {
+        constexpr int st = decltype(st_c)::value;
+        if constexpr (!kDirect)
+            return Bs3[st];
+        else if constexpr (st == 0)
+            return B0;
+        else if constexpr (st == 1)
+            return B1;
+        else
+            return B2;
+    };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
@@ -130,9 +171,60 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // two B operands of a k row sit side by side and one 8-byte LDS read, at an immediate
         // offset from the lane's base, fetches both.
         static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
-        for (int s0 = 0; s0 < 2 && s0 < ktiles; s0++) {
-            stage.fetch_whole();
-            stage.stash(As[s0], Bs[s0], tid);
+        //
+        // Direct loads: each wave moves 1 KiB of op(A) and 1 KiB of op(B) per slab, lane l's 16
+        // bytes landing at the wave's LDS base + 16 l. Stage layouts (floats):
+        //  * op(B), and op(A) when transposed: k-major rows of 128; wave w fills rows 2w (lanes
+        //    0-31) and 2w + 1 (lanes 32-63), and odd rows are rotated by 32 (element x at
+        //    (x - 32) mod 128), so the two half-waves of an operand read fall on different banks;
+        //  * op(A) untransposed: k quads, element (k, m) at 512 (k / 4) + 4 m + k % 4, so each
+        //    lane's 16 bytes (four consecutive k of one row) land whole; wave w fills quad w / 2,
+        //    rows 64 (w % 2) to 64 (w % 2) + 63.
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        const int rot = half ? (col + 8) & 31 : col; // the 16-byte run a lane of row 2w + half moves
+        const float *ga = nullptr, *gb = nullptr;
+        size_t da = 0, db = 0;
+        int la = 0, lb = 0, a_off = 0, b_off = 0;
+        if constexpr (kDirect) {
+            if (!TA) {
+                ga = A + (size_t)(m0 + 64 * (wv & 1) + lane) * K + 4 * (wv >> 1);
+                da = BK;
+                la = 512 * (wv >> 1) + 256 * (wv & 1);
+                a_off = 4 * (wm + col) + half;
+            } else {
+                ga = A + (size_t)(2 * wv + half) * M + m0 + 4 * rot;
+                da = (size_t)BK * M;
+                la = 256 * wv;
+                a_off = half ? 128 + ((wm + col - 32) & 127) : wm + col;
+            }
+            gb = B + (size_t)(2 * wv + half) * N + n0 + 4 * rot;
+            db = (size_t)BK * N;
+            lb = 256 * wv;
+            b_off = half ? 128 + ((wn + 2 * col - 32) & 127) : wn + 2 * col;
+        }
+        // Stage the next slab into stage ST: direct loads, or global -> registers (the stash
+        // to LDS follows at the end of the slab).
+        auto load_slab = [&](auto st_c) {
+            if constexpr (kDirect) {
+                load_lds16(ga, &sa(st_c)[0][0] + la);
+                load_lds16(gb, &sb(st_c)[0][0] + lb);
+                ga += da;
+                gb += db;
+            } else {
+                stage.fetch_whole();
+            }
+        };
+        auto stash_slab = [&](auto st_c) {
+            if constexpr (!kDirect)
+                stage.stash(sa(st_c), sb(st_c), tid);
+        };
+        if (ktiles > 0) {
+            load_slab(std::integral_constant<int, 0>{});
+            stash_slab(std::integral_constant<int, 0>{});
+        }
+        if (ktiles > 1) {
+            load_slab(std::integral_constant<int, 1>{});
+            stash_slab(std::integral_constant<int, 1>{});
         }
         __syncthreads();
         // Software pipeline over the slab, unrolled: each MFMA is issued, then the products of
@@ -144,9 +236,15 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         static_assert(NP % 2 == 0, "a slab's first pair takes register slot 0");
         float oa[2], ob[2][2];
         auto rd = [&](auto st_c, int j) {
-            constexpr int st = decltype(st_c)::value;
-            oa[j & 1] = As[st][2 * j + half][wm + col];
-            const float2 v = *reinterpret_cast<const float2 *>(&Bs[st][2 * j + half][wn + 2 * col]);
+            float2 v;
+            if constexpr (kDirect) {
+                const float *as = &sa(st_c)[0][0], *bs = &sb(st_c)[0][0];
+                oa[j & 1] = as[a_off + (TA ? 256 * j : 512 * (j >> 1) + 2 * (j & 1))];
+                v = *reinterpret_cast<const float2 *>(bs + b_off + 256 * j);
+            } else {
+                oa[j & 1] = sa(st_c)[2 * j + half][wm + col];
+                v = *reinterpret_cast<const float2 *>(&sb(st_c)[2 * j + half][wn + 2 * col]);
+            }
             ob[j & 1][0] = v.x;
             ob[j & 1][1] = v.y;
         };
@@ -160,9 +258,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
             constexpr int cur = decltype(cur_c)::value, nn = (cur + 2) % 3;
             const std::integral_constant<int, (cur + 1) % 3> nxt_c;
+            const std::integral_constant<int, nn> nn_c;
             const bool has_next = kt + 1 < ktiles;
             if (kt + 2 < ktiles)
-                stage.fetch_whole();
+                load_slab(nn_c);
 #pragma unroll
             for (int j = 0; j < NP; j++) {
                 if (j + 1 < NP)
@@ -180,7 +279,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (kt + 2 < ktiles)
-                stage.stash(As[nn], Bs[nn], tid);
+                stash_slab(nn_c);
             __syncthreads();
         };
         for (int kt = 0; kt < ktiles; kt += 3) {
