@@ -277,6 +277,20 @@ template <typename T> struct ValuCfg {
     template <bool TA> static constexpr bool kSplitRunsB = sizeof(T) == 8 && !TA;
 };
 
+// Direct global -> LDS load of 16 bytes a lane: lane l's run lands at lds + 16 l bytes (lds is
+// the wave's base, uniform across the wave).
+// Issued from inline assembly, so the compiler does not model it: as a builtin it counts as
+// a second kind of LDS event, after which every LDS read waits for all reads before it
+// (lgkmcnt(0)) instead of only the ones it needs. The caller waits for it (wait_lds_loads)
+// before the barrier that publishes the stage.
+__device__ __forceinline__ void load_lds16(const void *g, void *lds)
+{
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per
 // (cell, k) and no fault screen.
 // WHOLE: every slab of every tile is whole (see the MFMA kernel).
@@ -293,8 +307,16 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     // Reading each k row's operands one row ahead measured 2-8% faster with a transposed
     // operand or a partial tile, and 3-9% slower for whole untransposed binary64 tiles.
     constexpr bool kAhead = TA || TB || !WHOLE;
+    // Binary64 whole tiles with op(B) untransposed move op(B), and op(A) when transposed, from
+    // global memory straight into LDS (global_load_lds_dwordx4: each wave instruction fills
+    // one 1 KiB k row of a stage, so the stages keep their padded k-major layout). Their two
+    // stages are separate LDS objects indexed at compile time, so the compiler can tell a
+    // direct load into one stage from the reads of the other.
+    constexpr bool kDirect = sizeof(T) == 8 && WHOLE && !TB;
     __shared__ __align__(16) T As[2][BK][Cfg::LDA];
     __shared__ __align__(16) T Bs[2][BK][Cfg::LDB];
+    __shared__ __align__(16) T A0[BK][Cfg::LDA], A1[BK][Cfg::LDA];
+    __shared__ __align__(16) T B0[BK][Cfg::LDB], B1[BK][Cfg::LDB];
 
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
@@ -322,22 +344,8 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const int ktiles = (K + BK - 1) / BK;
     if (WHOLE)
         stage.begin_whole(A, B, M, N, K, m0, n0, tid);
-    if (ktiles > 0) {
-        if (WHOLE)
-            stage.fetch_whole();
-        else
-            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
-        stage.stash(As[0], Bs[0], tid);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) {
-            if (WHOLE)
-                stage.fetch_whole();
-            else
-                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
-        }
+    // One slab's products and sums from the stage (Ac, Bc).
+    auto compute = [&](const T (*Ac)[Cfg::LDA], const T (*Bc)[Cfg::LDB]) __attribute__((always_inline)) {
         if constexpr (kAhead) {
             // The slab is unrolled; row k + 1's operands are read from LDS into the other
             // register set before row k is computed, and sched_barrier keeps the reads
@@ -347,12 +355,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             auto rd = [&](int k) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    a[k & 1][i] = As[cur][k][ty * 4 + i];
-                    a[k & 1][4 + i] = As[cur][k][64 + ty * 4 + i];
+                    a[k & 1][i] = Ac[k][ty * 4 + i];
+                    a[k & 1][4 + i] = Ac[k][64 + ty * 4 + i];
                 }
 #pragma unroll
                 for (int j = 0; j < 8; j++)
-                    b[k & 1][j] = Bs[cur][k][col_of(j)];
+                    b[k & 1][j] = Bc[k][col_of(j)];
             };
             rd(0);
 #pragma unroll
@@ -395,12 +403,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                 T a[8], b[8];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    a[i] = As[cur][k][ty * 4 + i];
-                    a[4 + i] = As[cur][k][64 + ty * 4 + i];
+                    a[i] = Ac[k][ty * 4 + i];
+                    a[4 + i] = Ac[k][64 + ty * 4 + i];
                 }
 #pragma unroll
                 for (int j = 0; j < 8; j++)
-                    b[j] = Bs[cur][k][col_of(j)];
+                    b[j] = Bc[k][col_of(j)];
                 // Per row, the eight rounded products first and then the eight rounded sums:
                 // no add waits on the multiply just before it (F64 measured 4% faster than
                 // alternating multiply/add through one temporary).
@@ -422,9 +430,79 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                 }
             }
         }
-        if (kt + 1 < ktiles)
-            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+    };
+    if constexpr (!kDirect) {
+        if (ktiles > 0) {
+            if (WHOLE)
+                stage.fetch_whole();
+            else
+                stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+            stage.stash(As[0], Bs[0], tid);
+        }
         __syncthreads();
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int cur = kt & 1;
+            if (kt + 1 < ktiles) {
+                if (WHOLE)
+                    stage.fetch_whole();
+                else
+                    stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+            }
+            compute(As[cur], Bs[cur]);
+            if (kt + 1 < ktiles)
+                stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+            __syncthreads();
+        }
+    } else {
+        // Wave w moves k rows w, w + 4, w + 8 and w + 12 of each directly loaded operand; lane
+        // l's 16 bytes are the row's columns 2 l and 2 l + 1.
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        const T *gb = B + (size_t)wv * N + n0 + 2 * lane;
+        const T *ga = TA ? A + (size_t)wv * M + m0 + 2 * lane : A;
+        auto load = [&](T (*Ad)[Cfg::LDA], T (*Bd)[Cfg::LDB]) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                load_lds16(gb + (size_t)4 * r * N, &Bd[wv + 4 * r][0]);
+            gb += (size_t)BK * N;
+            if constexpr (TA) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    load_lds16(ga + (size_t)4 * r * M, &Ad[wv + 4 * r][0]);
+                ga += (size_t)BK * M;
+            } else {
+                stage.fetch_whole_a();
+            }
+        };
+        auto stash = [&](T (*Ad)[Cfg::LDA]) {
+            if constexpr (!TA)
+                stage.stash_a(Ad, tid);
+        };
+        if (ktiles > 0) {
+            load(A0, B0);
+            stash(A0);
+        }
+        wait_lds_loads();
+        __syncthreads();
+        // Two slabs per trip: stage 0 holds even slabs, stage 1 odd ones.
+        auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+            constexpr int cur = decltype(cur_c)::value;
+            T (*Ac)[Cfg::LDA] = cur ? A1 : A0;
+            T (*Bc)[Cfg::LDB] = cur ? B1 : B0;
+            T (*An)[Cfg::LDA] = cur ? A0 : A1;
+            T (*Bn)[Cfg::LDB] = cur ? B0 : B1;
+            if (kt + 1 < ktiles)
+                load(An, Bn);
+            compute(Ac, Bc);
+            if (kt + 1 < ktiles)
+                stash(An);
+            wait_lds_loads();
+            __syncthreads();
+        };
+        for (int kt = 0; kt < ktiles; kt += 2) {
+            slab(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < ktiles)
+                slab(std::integral_constant<int, 1>{}, kt + 1);
+        }
     }
 
     // Epilogue: publish the tile and find the first suspect cell of this lane.

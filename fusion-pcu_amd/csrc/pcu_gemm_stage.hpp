@@ -136,6 +136,25 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
         pb += sb;
     }
 
+    // op(A) alone, for kernels that move op(B) straight to LDS.
+    __device__ __forceinline__ void fetch_whole_a()
+    {
+        load_run<T, EA, true>(pa, EA, ra);
+        pa += sa;
+    }
+    __device__ __forceinline__ void stash_a(T (*As)[Cfg::LDA], int tid) const
+    {
+        if (!TA) {
+            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
+#pragma unroll
+            for (int i = 0; i < EA; i++)
+                As[k + i][m] = ra[i];
+        } else {
+            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
+            store_run<T, EA>(&As[k][m], ra);
+        }
+    }
+
     __device__ __forceinline__ void fetch(const T *__restrict__ A, const T *__restrict__ B, int M,
                                           int N, int K, int m0, int n0, int k0, int tid)
     {
