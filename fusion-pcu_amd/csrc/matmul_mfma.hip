@@ -47,12 +47,18 @@ template <int WM_, int WN_, int SM_, int SN_, int BK_, int WAVES_PER_SIMD_> stru
     template <bool TA> static constexpr bool kSplitRunsB = EB > 4;
 };
 
-// Direct global -> LDS load of 16 bytes a lane: lane l's run lands at lds + 16 l bytes (lds is
-// the wave's base, uniform across the wave).
-__device__ __forceinline__ void load_lds16(const float *g, float *lds)
+// Direct global -> LDS load of 16 bytes a lane from base + off bytes: lane l's run lands at
+// lds + 16 l bytes. base and lds are uniform across the wave; base stays in scalar registers
+// (the scalar unit advances it), which the compiler's form of this load does not do. Issued
+// from inline assembly, so the compiler does not track it: the caller waits for it
+// (wait_lds_loads) before the barrier that publishes the stage.
+__device__ __forceinline__ void load_lds16(const float *base, uint32_t off, float *lds)
 {
-    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(base)
+                 : "memory", "m0");
 }
+__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // WHOLE: every slab of every tile is whole (M, N, K multiples of the tile and slab, 16-byte
 // loads allowed), so staging runs on advancing pointers with no bound checks.
@@ -75,37 +81,13 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // unpadded (see the layouts at the direct loads below).
     constexpr bool kDirect = WHOLE && !TB;
     constexpr int LDA = kDirect ? BM : Cfg::LDA, LDB = kDirect ? BN : Cfg::LDB;
-    // Two stages are indexed at run time, three at compile time. With direct loads each of the
-    // three stages is an LDS object of its own, so the compiler can tell a direct load into one
-    // stage from the reads of another (with one array it waits for the load before every read).
+    // Two stages are indexed at run time, three at compile time.
     __shared__ __align__(16) float As[2][BK][LDA];
     __shared__ __align__(16) float Bs[2][BK][LDB];
     __shared__ __align__(16) float As3[3][BK][LDA];
     __shared__ __align__(16) float Bs3[3][BK][LDB];
-    __shared__ __align__(16) float A0[BK][LDA], A1[BK][LDA], A2[BK][LDA];
-    __shared__ __align__(16) float B0[BK][LDB], B1[BK][LDB], B2[BK][LDB];
-    auto sa = [&](auto st_c) -> float(*)[LDA] {
-        constexpr int st = decltype(st_c)::value;
-        if constexpr (!kDirect)
-            return As3[st];
-        else if constexpr (st == 0)
-            return A0;
-        else if constexpr (st == 1)
-            return A1;
-        else
-            return A2;
-    };
-    auto sb = [&](auto st_c) -> float(*)[LDB] {
-        constexpr int st = decltype(st_c)::value;
-        if constexpr (!kDirect)
-            return Bs3[st];
-        else if constexpr (st == 0)
-            return B0;
-        else if constexpr (st == 1)
-            return B1;
-        else
-            return B2;
-    };
+    auto sa = [&](auto st_c) -> float(*)[LDA] { return As3[decltype(st_c)::value]; };
+    auto sb = [&](auto st_c) -> float(*)[LDB] { return Bs3[decltype(st_c)::value]; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
@@ -182,22 +164,26 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         //    rows 64 (w % 2) to 64 (w % 2) + 63.
         const int wv = __builtin_amdgcn_readfirstlane(wave);
         const int rot = half ? (col + 8) & 31 : col; // the 16-byte run a lane of row 2w + half moves
-        const float *ga = nullptr, *gb = nullptr;
+        const float *ga = nullptr, *gb = nullptr; // wave-uniform bases
+        uint32_t lo_a = 0, lo_b = 0;              // the lane's byte offsets from them
         size_t da = 0, db = 0;
         int la = 0, lb = 0, a_off = 0, b_off = 0;
         if constexpr (kDirect) {
             if (!TA) {
-                ga = A + (size_t)(m0 + 64 * (wv & 1) + lane) * K + 4 * (wv >> 1);
+                ga = A + (size_t)(m0 + 64 * (wv & 1)) * K + 4 * (wv >> 1);
+                lo_a = (uint32_t)lane * (uint32_t)K * 4u;
                 da = BK;
                 la = 512 * (wv >> 1) + 256 * (wv & 1);
                 a_off = 4 * (wm + col) + half;
             } else {
-                ga = A + (size_t)(2 * wv + half) * M + m0 + 4 * rot;
+                ga = A + (size_t)(2 * wv) * M + m0;
+                lo_a = ((uint32_t)half * (uint32_t)M + 4u * rot) * 4u;
                 da = (size_t)BK * M;
                 la = 256 * wv;
                 a_off = half ? 128 + ((wm + col - 32) & 127) : wm + col;
             }
-            gb = B + (size_t)(2 * wv + half) * N + n0 + 4 * rot;
+            gb = B + (size_t)(2 * wv) * N + n0;
+            lo_b = ((uint32_t)half * (uint32_t)N + 4u * rot) * 4u;
             db = (size_t)BK * N;
             lb = 256 * wv;
             b_off = half ? 128 + ((wn + 2 * col - 32) & 127) : wn + 2 * col;
@@ -206,8 +192,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // to LDS follows at the end of the slab).
         auto load_slab = [&](auto st_c) {
             if constexpr (kDirect) {
-                load_lds16(ga, &sa(st_c)[0][0] + la);
-                load_lds16(gb, &sb(st_c)[0][0] + lb);
+                load_lds16(ga, lo_a, &sa(st_c)[0][0] + la);
+                load_lds16(gb, lo_b, &sb(st_c)[0][0] + lb);
                 ga += da;
                 gb += db;
             } else {
@@ -226,6 +212,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             load_slab(std::integral_constant<int, 1>{});
             stash_slab(std::integral_constant<int, 1>{});
         }
+        if constexpr (kDirect)
+            wait_lds_loads();
         __syncthreads();
         // Software pipeline over the slab, unrolled: each MFMA is issued, then the products of
         // the one before it are folded. sched_barrier pins that order (left to the scheduler,
@@ -280,6 +268,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             }
             if (kt + 2 < ktiles)
                 stash_slab(nn_c);
+            if constexpr (kDirect)
+                wait_lds_loads();
             __syncthreads();
         };
         for (int kt = 0; kt < ktiles; kt += 3) {
@@ -409,9 +399,13 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    // Whole tiles store C two floats at a time.
+    // Whole tiles store C two floats at a time. With op(B) untransposed they load directly, and
+    // a lane's byte offset from its wave's base must fit 32 bits: at most 63 rows of op(A)
+    // untransposed, else at most one row and 128 floats (of op(A) transposed, or of op(B)).
+    const uint64_t span_a = TA ? (uint64_t)M + 128 : 64 * (uint64_t)K, span_b = (uint64_t)N + 128;
+    const bool offsets32 = TB || (4 * span_a <= UINT32_MAX && 4 * span_b <= UINT32_MAX);
     const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
-                       ((uintptr_t)C & 7u) == 0;
+                       ((uintptr_t)C & 7u) == 0 && offsets32;
     if (whole)
         hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
     else if (va && vb)
