@@ -109,10 +109,13 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 #pragma unroll
     for (int r = 0; r < 32; r++)
         zero[r] = 0.0f;
-    // With two stages, raising the wave's priority around each MFMA issue measured about
-    // 0.8% faster at 4096^3 when op(A) and op(B) are staged alike (both transposed or
-    // neither) and about 0.4% slower otherwise, so it is used only there. With three stages
-    // it measured 1.7-4% slower in every layout.
+    // Wave priority. With three stages, a wave raises its priority while it folds (1.8-1.9%
+    // faster at 4096^3): a wave in the middle of its adds keeps issuing them, paired with
+    // another wave's, rather than giving way to a wave ready to issue its MFMA. With two
+    // stages, raising it around each MFMA issue measured about 0.8% faster at 4096^3 when
+    // op(A) and op(B) are staged alike (both transposed or neither) and about 0.4% slower
+    // otherwise, so it is used only there.
+    constexpr bool kFoldPrio = WHOLE;
     constexpr bool kIssuePrio = !WHOLE && TA == TB;
     auto mma = [&](float a, float b) {
         if (kIssuePrio)
@@ -126,6 +129,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // then its k+1 product (register 16 + r). The sixteen k sums go first, so no add waits
     // on the add just before it (measured 2-3% faster with a transposed operand).
     auto fold = [&](float (&c)[16], const v32f &p) {
+        if (kFoldPrio)
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[r];
@@ -136,6 +141,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
                      "+v"(c[6]), "+v"(c[7]), "+v"(c[8]), "+v"(c[9]), "+v"(c[10]), "+v"(c[11]),
                      "+v"(c[12]), "+v"(c[13]), "+v"(c[14]), "+v"(c[15]));
+        if (kFoldPrio)
+            __builtin_amdgcn_s_setprio(0);
     };
 
     const int ktiles = (K + BK - 1) / BK;
