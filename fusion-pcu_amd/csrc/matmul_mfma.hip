@@ -76,11 +76,12 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // Whole tiles run three LDS stages (see the slab loop); tiles with bound checks keep two,
     // since their staging needs more registers and three spill there.
     constexpr int kStages = WHOLE ? 3 : 2;
-    // Whole tiles with op(B) untransposed load both operands from global memory straight into
-    // LDS (global_load_lds_dwordx4: no staging registers, no LDS stores); their stages are
-    // unpadded (see the layouts at the direct loads below).
-    constexpr bool kDirect = WHOLE && !TB;
-    constexpr int LDA = kDirect ? BM : Cfg::LDA, LDB = kDirect ? BN : Cfg::LDB;
+    // Whole tiles load op(A), and op(B) when untransposed, from global memory straight into
+    // LDS (global_load_lds_dwordx4: no staging registers, no LDS stores); those stages are
+    // unpadded (see the layouts at the direct loads below). A transposed op(B) goes through
+    // registers, which turn its k-contiguous runs into k-major rows.
+    constexpr bool kDirectA = WHOLE, kDirectB = WHOLE && !TB;
+    constexpr int LDA = kDirectA ? BM : Cfg::LDA, LDB = kDirectB ? BN : Cfg::LDB;
     // Two stages are indexed at run time, three at compile time.
     __shared__ __align__(16) float As[2][BK][LDA];
     __shared__ __align__(16) float Bs[2][BK][LDB];
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         uint32_t lo_a = 0, lo_b = 0;              // the lane's byte offsets from them
         size_t da = 0, db = 0;
         int la = 0, lb = 0, a_off = 0, b_off = 0;
-        if constexpr (kDirect) {
+        if constexpr (kDirectA) {
             if (!TA) {
                 ga = A + (size_t)(m0 + 64 * (wv & 1)) * K + 4 * (wv >> 1);
                 lo_a = (uint32_t)lane * (uint32_t)K * 4u;
@@ -189,6 +190,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 la = 256 * wv;
                 a_off = half ? 128 + ((wm + col - 32) & 127) : wm + col;
             }
+        }
+        if constexpr (kDirectB) {
             gb = B + (size_t)(2 * wv) * N + n0;
             lo_b = ((uint32_t)half * (uint32_t)N + 4u * rot) * 4u;
             db = (size_t)BK * N;
@@ -198,18 +201,20 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // Stage the next slab into stage ST: direct loads, or global -> registers (the stash
         // to LDS follows at the end of the slab).
         auto load_slab = [&](auto st_c) {
-            if constexpr (kDirect) {
+            if constexpr (kDirectA) {
                 load_lds16(ga, lo_a, &sa(st_c)[0][0] + la);
-                load_lds16(gb, lo_b, &sb(st_c)[0][0] + lb);
                 ga += da;
+            }
+            if constexpr (kDirectB) {
+                load_lds16(gb, lo_b, &sb(st_c)[0][0] + lb);
                 gb += db;
             } else {
-                stage.fetch_whole();
+                stage.fetch_whole_b();
             }
         };
         auto stash_slab = [&](auto st_c) {
-            if constexpr (!kDirect)
-                stage.stash(sa(st_c), sb(st_c), tid);
+            if constexpr (!kDirectB)
+                stage.stash_b(sb(st_c), tid);
         };
         if (ktiles > 0) {
             load_slab(std::integral_constant<int, 0>{});
@@ -219,8 +224,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             load_slab(std::integral_constant<int, 1>{});
             stash_slab(std::integral_constant<int, 1>{});
         }
-        if constexpr (kDirect)
-            wait_lds_loads();
+        wait_lds_loads();
         __syncthreads();
         // Software pipeline over the slab, unrolled: each MFMA is issued, then the products of
         // the one before it are folded. sched_barrier pins that order (left to the scheduler,
@@ -232,14 +236,14 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         float oa[2], ob[2][2];
         auto rd = [&](auto st_c, int j) {
             float2 v;
-            if constexpr (kDirect) {
-                const float *as = &sa(st_c)[0][0], *bs = &sb(st_c)[0][0];
-                oa[j & 1] = as[a_off + (TA ? 256 * j : 512 * (j >> 1) + 2 * (j & 1))];
-                v = *reinterpret_cast<const float2 *>(bs + b_off + 256 * j);
-            } else {
+            if constexpr (kDirectA)
+                oa[j & 1] = (&sa(st_c)[0][0])[a_off + (TA ? 256 * j : 512 * (j >> 1) + 2 * (j & 1))];
+            else
                 oa[j & 1] = sa(st_c)[2 * j + half][wm + col];
+            if constexpr (kDirectB)
+                v = *reinterpret_cast<const float2 *>(&sb(st_c)[0][0] + b_off + 256 * j);
+            else
                 v = *reinterpret_cast<const float2 *>(&sb(st_c)[2 * j + half][wn + 2 * col]);
-            }
             ob[j & 1][0] = v.x;
             ob[j & 1][1] = v.y;
         };
@@ -275,8 +279,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             }
             if (kt + 2 < ktiles)
                 stash_slab(nn_c);
-            if constexpr (kDirect)
-                wait_lds_loads();
+            wait_lds_loads();
             __syncthreads();
         };
         for (int kt = 0; kt < ktiles; kt += 3) {
@@ -406,11 +409,11 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    // Whole tiles store C two floats at a time. With op(B) untransposed they load directly, and
-    // a lane's byte offset from its wave's base must fit 32 bits: at most 63 rows of op(A)
-    // untransposed, else at most one row and 128 floats (of op(A) transposed, or of op(B)).
+    // Whole tiles store C two floats at a time and load op(A), and op(B) when untransposed,
+    // directly: a lane's byte offset from its wave's base must fit 32 bits (at most 63 rows of
+    // op(A) untransposed, else at most one row and 128 floats).
     const uint64_t span_a = TA ? (uint64_t)M + 128 : 64 * (uint64_t)K, span_b = (uint64_t)N + 128;
-    const bool offsets32 = TB || (4 * span_a <= UINT32_MAX && 4 * span_b <= UINT32_MAX);
+    const bool offsets32 = 4 * span_a <= UINT32_MAX && (TB || 4 * span_b <= UINT32_MAX);
     const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
                        ((uintptr_t)C & 7u) == 0 && offsets32;
     if (whole)

@@ -155,6 +155,29 @@ template <typename T, class Cfg, bool TA, bool TB, bool VA, bool VB> struct Slab
         }
     }
 
+    // op(B) alone, for kernels that move op(A) straight to LDS.
+    __device__ __forceinline__ void fetch_whole_b()
+    {
+        if constexpr (kRunsB)
+            load_runs<T, EB, RSB, true>(pb, BN, rb);
+        else
+            load_run<T, EB, true>(pb, EB, rb);
+        pb += sb;
+    }
+    __device__ __forceinline__ void stash_b(T (*Bs)[Cfg::LDB], int tid) const
+    {
+        static_assert(!kRunsB, "op(B) alone is stashed as one run a thread");
+        if (!TB) {
+            const int k = tid / TPRB, n = (tid % TPRB) * WB;
+            store_run<T, EB>(&Bs[k][n], rb);
+        } else {
+            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
+                Bs[k + i][n] = rb[i];
+        }
+    }
+
     __device__ __forceinline__ void fetch(const T *__restrict__ A, const T *__restrict__ B, int M,
                                           int N, int K, int m0, int n0, int k0, int tid)
     {
