@@ -211,17 +211,31 @@ template <typename T> __host__ __device__ inline uint64_t exp_blocks(const ExpJo
 // Both jobs of a MatMul in one launch: blocks [0, na) run job a, the rest job b. A block's
 // branches are uniform, so the columns job's barrier is reached by all of its threads. The
 // launch also clears the MatMul's first-suspect word.
+// Block 0 of a program's first kernel opens the program (see ProgramOpen).
+__device__ __forceinline__ void program_open_block(const ProgramOpen &o)
+{
+    if (!o.words)
+        return;
+    for (uint64_t i = threadIdx.x; i < o.n; i += blockDim.x)
+        o.words[i] = o.value;
+    if (threadIdx.x == 0)
+        *o.gate = 0xffffffffu;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, uint64_t na,
                                                     uint32_t gen, unsigned long long *suspect,
-                                                    NodeGate gate)
+                                                    NodeGate gate, ProgramOpen open)
 {
     __shared__ int part[4][64 * 16 / sizeof(T)];
     if (block_gate_closed(gate))
         return;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        suspect[0] = kNoFault; // first suspect cell
-        suspect[1] = kNoFault; // first row with a cell the tiny scan flags
+    if (blockIdx.x == 0) {
+        program_open_block(open);
+        if (threadIdx.x == 0) {
+            suspect[0] = kNoFault; // first suspect cell
+            suspect[1] = kNoFault; // first row with a cell the tiny scan flags
+        }
     }
     const bool first = blockIdx.x < na;
     const ExpJob<T> &j = first ? a : b;
@@ -236,6 +250,16 @@ __global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, ui
             exp_cols_block<T, true>(j, bid, gen, part);
         else
             exp_cols_block<T, false>(j, bid, gen, part);
+    }
+}
+
+// The screen's place when there is nothing to screen: the suspect words, and the program.
+__global__ void k_matmul_open(unsigned long long *suspect, ProgramOpen open)
+{
+    program_open_block(open);
+    if (threadIdx.x == 0) {
+        suspect[0] = kNoFault;
+        suspect[1] = kNoFault;
     }
 }
 
@@ -1038,12 +1062,12 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; 
 // The exponent screen of op(A) rows and op(B) columns, both jobs in one launch.
 template <typename T>
 static void prefilter(hipStream_t s, ExpJob<T> ja, ExpJob<T> jb, uint32_t gen,
-                      unsigned long long *suspect, NodeGate gate)
+                      unsigned long long *suspect, NodeGate gate, ProgramOpen open)
 {
     for (ExpJob<T> *j : {&ja, &jb})
         j->vec = j->C % (16 / sizeof(T)) == 0 && aligned16(j->X);
     const uint64_t na = exp_blocks(ja), nb = exp_blocks(jb);
-    hipLaunchKernelGGL(k_exp_screen<T>, dim3((unsigned)(na + nb)), dim3(256), 0, s, ja, jb, na, gen, suspect, gate);
+    hipLaunchKernelGGL(k_exp_screen<T>, dim3((unsigned)(na + nb)), dim3(256), 0, s, ja, jb, na, gen, suspect, gate, open);
 }
 
 template <typename T, bool TA, bool TB>
@@ -1109,7 +1133,7 @@ template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault, NodeGate gate,
-                                  hipEvent_t *ev, int engine)
+                                  hipEvent_t *ev, int engine, ProgramOpen open)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -1127,10 +1151,10 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         // column c is stored column c (B is K x N) or stored row c (B is N x K).
         const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp};
         const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp};
-        prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate);
+        prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate, open);
     } else {
         risk = 0; // AllowGradual, or an empty reduction: no underflow screen
-        hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(64), 0, s, sc.suspect, (uint64_t)2, (unsigned long long)kNoFault);
+        hipLaunchKernelGGL(k_matmul_open, dim3(1), dim3(256), 0, s, sc.suspect, open);
     }
     dim3 grid((unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN)));
     const int m = (int)M, n = (int)N, k = (int)K;
@@ -1221,17 +1245,17 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
-                                hipEvent_t *ev, int engine)
+                                hipEvent_t *ev, int engine, ProgramOpen open)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (dtype == 0)
         return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                       (const float *)a, (const float *)b, (float *)c, policy,
-                                      scratch, fault, gate, ev, engine);
+                                      scratch, fault, gate, ev, engine, open);
     return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                    (const double *)a, (const double *)b, (double *)c, policy,
-                                   scratch, fault, gate, ev, kEngineValu);
+                                   scratch, fault, gate, ev, kEngineValu, open);
 }
 
 } // namespace pcu

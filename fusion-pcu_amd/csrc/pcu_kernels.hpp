@@ -73,11 +73,22 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
 // faulted (that earlier fault is reported).
 // `ev` (optional, 4 events) is recorded before the prefilter, before and after the main
 // kernel, and after the replay.
+// The opening of a program (its fault words set to `value`, its stage gate opened) can be
+// done by the first kernel of the program's first node instead of a launch of its own: a
+// first node is never gated, so that kernel may open the gate while it runs. `open` asks the
+// MatMul's first kernel to do it (rows and cols must then be nonzero); words == nullptr: no.
+struct ProgramOpen {
+    unsigned long long *words = nullptr;
+    uint64_t n = 0;
+    unsigned long long value = 0;
+    unsigned int *gate = nullptr;
+};
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
-                                hipEvent_t *ev = nullptr, int engine = kEngineAuto);
+                                hipEvent_t *ev = nullptr, int engine = kEngineAuto,
+                                ProgramOpen open = {});
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,

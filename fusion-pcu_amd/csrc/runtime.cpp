@@ -707,15 +707,22 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     if (timed)
         for (auto &x : ev)
             x = take_event();
-    if ((st = open_words()))
+    // As the program's first node, the MatMul's first kernel opens the program (one launch
+    // fewer; a first node is never gated, so nothing waits on the gate it opens).
+    ProgramOpen open;
+    if (words_pending && nodes.size() == 1) {
+        words_pending = false;
+        open = {fault_words, kMaxNodes, kNoFaultWord, gate_word()};
+    } else if ((st = open_words())) {
         return st;
+    }
     if (clear_words &&
         (st = hip(launch_fill_u64(stream, (unsigned long long *)sc, clear_words, 0),
                   "clear MatMul screen words")))
         return st;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
-                                        timed ? ev : nullptr, matmul_engine);
+                                        timed ? ev : nullptr, matmul_engine, open);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
     if (timed) {

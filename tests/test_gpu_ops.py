@@ -674,6 +674,36 @@ def test_program_stage_gate_skips_nodes_after_a_fault(ctx, pcu_pkg, engine_name)
         ctx.set_matmul_engine("auto")
 
 
+@pytest.mark.parametrize("policy", list(POLICY), ids=list(POLICY))
+def test_program_opened_by_its_first_matmul(ctx, pcu_pkg, policy):
+    """A MatMul that is a program's first node opens the program from its own first kernel
+    (the screen, or its stand-in when there is nothing to screen): after a program whose
+    node 0 faulted, the next program's fault words and stage gate must read as fresh, so
+    its node 1 still runs and is the node reported."""
+    pol = POLICY[policy]
+    rng = np.random.default_rng(21)
+    a = rng.uniform(-1, 1, (128, 64)).astype(np.float32)
+    b = rng.uniform(-1, 1, (64, 96)).astype(np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    dnan = ctx.upload(np.array([1.0, np.nan], np.float32))
+    ref, _ = oracle.matmul(a, b, policy=pol)
+    for _ in range(2):
+        with pytest.raises(pcu_pkg.PcuExecutionError) as e:
+            with ctx.program():
+                ctx.checked_relu(dnan)
+        assert e.value.tensor_fault.node == 0
+        with pytest.raises(pcu_pkg.PcuExecutionError) as e:
+            with ctx.program():
+                out = ctx.strict_matmul(da, db, False, False, pol)
+                ctx.checked_relu(dnan)
+        f = e.value.tensor_fault
+        assert (f.node, f.element_index, int(f.kind)) == (1, 1, 5)
+        np.testing.assert_array_equal(_bits(out.numpy()), _bits(ref))
+        got = ctx.strict_matmul(da, db, False, False, pol).numpy()
+        np.testing.assert_array_equal(_bits(got), _bits(ref))
+        assert ctx.last_fault() is None
+
+
 # ------------------------------------------------------------ output aliasing
 
 
