@@ -486,6 +486,37 @@ def test_matmul_random_fault_placement_fuzz(ctx, pcu_pkg, dtype, engine):
             np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_whole_tile_fuzz(ctx, pcu_pkg, dtype, engine):
+    """The same first-fault fuzz over whole tiles only (M and N multiples of 128, K of 16),
+    where the main kernels load operands straight into LDS in per-layout arrangements and run
+    three slabs a trip: 12 seeded cases over every layout and policy, a third of them clean
+    (bits compared) and the rest with up to five special operands, so faults land in
+    different slabs and stages; the GPU must give the oracle's first fault or, without one,
+    its bits."""
+    rng = np.random.default_rng(31 if dtype == np.float32 else 32)
+    info = np.finfo(dtype)
+    specials = np.array([np.nan, np.inf, -np.inf, info.max, -info.max,
+                         info.tiny * dtype(2.0 ** 20), -info.tiny * dtype(3.0),
+                         info.smallest_subnormal * dtype(3.0)], dtype=dtype)
+    for case in range(12):
+        m, n = (128 * int(v) for v in rng.integers(1, 4, size=2))
+        k = 16 * int(rng.integers(1, 25))
+        tl, tr = case % 2 == 1, (case // 2) % 2 == 1
+        policy = int(rng.integers(3))
+        a = rng.uniform(-1, 1, (k, m) if tl else (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (n, k) if tr else (k, n)).astype(dtype)
+        for x in (a, b):
+            cnt = int(rng.integers(0, 6)) if case % 3 else 0
+            if cnt:
+                x.reshape(-1)[rng.choice(x.size, cnt, replace=False)] = rng.choice(specials, size=cnt)
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(a), ctx.upload(b), tl, tr, policy).numpy())
+        ref, rf = oracle.matmul(a, b, tl, tr, policy=policy)
+        assert gf == _ofault(rf), (case, m, k, n, tl, tr, policy, gf, rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
 @pytest.mark.parametrize("policy", [0, 1, 2])
 def test_matmul_signed_zero_and_subnormal_products(ctx, pcu_pkg, policy, engine):
     """Operands whose products are exact zeros of either sign, subnormal, or straddle the
