@@ -157,46 +157,59 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         // and issues its first MFMA before the barrier that ends slab kt: the MFMA runs while
         // the wave waits there, and no slab starts from an empty pipeline.
         //
-        // Lane col of the wave's subtile j owns tile column wn + 2 col + j, so its
-        // two B operands of a k row sit side by side and one 8-byte LDS read, at an immediate
-        // offset from the lane's base, fetches both.
-        static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
+        // With two subtiles a wave (SN = 2), lane col of subtile j owns tile column
+        // wn + 2 col + j, so its two B operands of a k row sit side by side and one 8-byte LDS
+        // read, at an immediate offset from the lane's base, fetches both. With one (SN = 1) it
+        // owns column wn + col.
+        static_assert(SM == 1 && (SN == 1 || SN == 2), "the pipeline below is written for one or two subtiles a wave");
         //
         // Direct loads: each wave moves 1 KiB of op(A) and 1 KiB of op(B) per slab, lane l's 16
         // bytes landing at the wave's LDS base + 16 l. Stage layouts (floats):
-        //  * op(B), and op(A) when transposed: k-major rows of 128; wave w fills rows 2w (lanes
-        //    0-31) and 2w + 1 (lanes 32-63), and odd rows are rotated by 32 (element x at
-        //    (x - 32) mod 128), so the two half-waves of an operand read fall on different banks;
-        //  * op(A) untransposed: k quads, element (k, m) at 512 (k / 4) + 4 m + k % 4, so each
-        //    lane's 16 bytes (four consecutive k of one row) land whole; wave w fills quad w / 2,
-        //    rows 64 (w % 2) to 64 (w % 2) + 63.
+        //  * op(B), and op(A) when transposed: k-major rows of R = BN (BM) floats; wave w fills
+        //    256 / R consecutive rows from row 256 w / R, and odd rows are rotated by 32
+        //    (element x at (x - 32) mod R), so the two half-waves of an operand read (rows 2j
+        //    and 2j + 1) fall on different banks;
+        //  * op(A) untransposed: k quads, element (k, m) at 4 BM (k / 4) + 4 m + k % 4, so each
+        //    lane's 16 bytes (four consecutive k of one row) land whole; BM / 64 waves fill a
+        //    quad, 64 rows each.
+        constexpr int W = Cfg::kThreads / 64;
+        static_assert(BM == 16 * W && BN == 16 * W, "each wave moves 1 KiB of each operand a slab");
         const int wv = __builtin_amdgcn_readfirstlane(wave);
-        const int rot = half ? (col + 8) & 31 : col; // the 16-byte run a lane of row 2w + half moves
+        // Rows layout of R floats: the run (16 bytes) lane l moves, and its offset in floats
+        // from the wave's first row; `stride` is the stored row pitch.
+        auto row_run = [&](int R, uint64_t stride) {
+            const int rr = lane / (R / 4), p = lane % (R / 4);
+            const int c = (rr & 1) ? (p + 8) % (R / 4) : p;
+            return (uint32_t)(((uint64_t)rr * stride + 4 * c) * 4);
+        };
+        // Element x of k row 2j + half, from the lane's base: 2 R j + off.
+        auto row_off = [&](int R, int x) { return half ? R + ((x - 32) & (R - 1)) : x; };
         const float *ga = nullptr, *gb = nullptr; // wave-uniform bases
         uint32_t lo_a = 0, lo_b = 0;              // the lane's byte offsets from them
         size_t da = 0, db = 0;
         int la = 0, lb = 0, a_off = 0, b_off = 0;
         if constexpr (kDirectA) {
             if (!TA) {
-                ga = A + (size_t)(m0 + 64 * (wv & 1)) * K + 4 * (wv >> 1);
+                constexpr int WQ = BM / 64; // waves a quad
+                ga = A + (size_t)(m0 + 64 * (wv % WQ)) * K + 4 * (wv / WQ);
                 lo_a = (uint32_t)lane * (uint32_t)K * 4u;
                 da = BK;
-                la = 512 * (wv >> 1) + 256 * (wv & 1);
+                la = 4 * BM * (wv / WQ) + 256 * (wv % WQ);
                 a_off = 4 * (wm + col) + half;
             } else {
-                ga = A + (size_t)(2 * wv) * M + m0;
-                lo_a = ((uint32_t)half * (uint32_t)M + 4u * rot) * 4u;
+                ga = A + (size_t)(256 / BM * wv) * M + m0;
+                lo_a = row_run(BM, (uint64_t)M);
                 da = (size_t)BK * M;
                 la = 256 * wv;
-                a_off = half ? 128 + ((wm + col - 32) & 127) : wm + col;
+                a_off = row_off(BM, wm + col);
             }
         }
         if constexpr (kDirectB) {
-            gb = B + (size_t)(2 * wv) * N + n0;
-            lo_b = ((uint32_t)half * (uint32_t)N + 4u * rot) * 4u;
+            gb = B + (size_t)(256 / BN * wv) * N + n0;
+            lo_b = row_run(BN, (uint64_t)N);
             db = (size_t)BK * N;
             lb = 256 * wv;
-            b_off = half ? 128 + ((wn + 2 * col - 32) & 127) : wn + 2 * col;
+            b_off = row_off(BN, SN == 2 ? wn + 2 * col : wn + col);
         }
         // Stage the next slab into stage ST: direct loads, or global -> registers (the stash
         // to LDS follows at the end of the slab).
@@ -228,28 +241,41 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         __syncthreads();
         // Software pipeline over the slab, unrolled: each MFMA is issued, then the products of
         // the one before it are folded. sched_barrier pins that order (left to the scheduler,
-        // the same sequence measured about 8% slower), and each k-pair's operands are read from
-        // LDS one pair ahead into the other of two register slots. Lanes 0-31 carry k = 2j,
-        // lanes 32-63 carry k = 2j + 1 (the MFMA's two blocks).
+        // the same sequence measured about 8% slower). Each k-pair's operands are read from
+        // LDS ahead into register slots used in turn: one pair ahead into two slots with two
+        // subtiles (their MFMAs alternate within a pair), two pairs ahead into three slots
+        // with one (each pair's MFMA is issued before the previous pair is folded). Lanes
+        // 0-31 carry k = 2j, lanes 32-63 carry k = 2j + 1 (the MFMA's two blocks).
         constexpr int NP = BK / 2;
-        static_assert(NP % 2 == 0, "a slab's first pair takes register slot 0");
-        float oa[2], ob[2][2];
-        auto rd = [&](auto st_c, int j) {
-            float2 v;
+        constexpr int kSlots = SN == 2 ? 2 : 3, D = kSlots - 1;
+        static_assert((3 * NP) % kSlots == 0, "a trip of three slabs ends on slot 0");
+        // Register slot of pair j of the trip's slab c (j may run into the next slab).
+        auto slot = [](int c, int j) { return (c * NP + j) % kSlots; };
+        float oa[kSlots], ob[kSlots][SN];
+        auto rd = [&](auto st_c, int g, int j) {
             if constexpr (kDirectA)
-                oa[j & 1] = (&sa(st_c)[0][0])[a_off + (TA ? 256 * j : 512 * (j >> 1) + 2 * (j & 1))];
+                oa[g] = (&sa(st_c)[0][0])[a_off + (TA ? 2 * BM * j : 4 * BM * (j >> 1) + 2 * (j & 1))];
             else
-                oa[j & 1] = sa(st_c)[2 * j + half][wm + col];
-            if constexpr (kDirectB)
-                v = *reinterpret_cast<const float2 *>(&sb(st_c)[0][0] + b_off + 256 * j);
-            else
-                v = *reinterpret_cast<const float2 *>(&sb(st_c)[2 * j + half][wn + 2 * col]);
-            ob[j & 1][0] = v.x;
-            ob[j & 1][1] = v.y;
+                oa[g] = sa(st_c)[2 * j + half][wm + col];
+            if constexpr (SN == 2) {
+                float2 v;
+                if constexpr (kDirectB)
+                    v = *reinterpret_cast<const float2 *>(&sb(st_c)[0][0] + b_off + 2 * BN * j);
+                else
+                    v = *reinterpret_cast<const float2 *>(&sb(st_c)[2 * j + half][wn + 2 * col]);
+                ob[g][0] = v.x;
+                ob[g][SN - 1] = v.y;
+            } else if constexpr (kDirectB) {
+                ob[g][0] = (&sb(st_c)[0][0])[b_off + 2 * BN * j];
+            } else {
+                ob[g][0] = sb(st_c)[2 * j + half][wn + col];
+            }
         };
         v32f p;
         if (ktiles > 0) {
-            rd(std::integral_constant<int, 0>{}, 0);
+#pragma unroll
+            for (int j = 0; j < D; j++)
+                rd(std::integral_constant<int, 0>{}, slot(0, j), j);
             p = mma(oa[0], ob[0][0]);
         }
         // One slab computed from stage CUR; the loop below runs three slabs per trip, so every
@@ -263,19 +289,32 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 load_slab(nn_c);
 #pragma unroll
             for (int j = 0; j < NP; j++) {
-                if (j + 1 < NP)
-                    rd(cur_c, j + 1);
+                if (j + D < NP)
+                    rd(cur_c, slot(cur, j + D), j + D);
                 else if (has_next)
-                    rd(nxt_c, 0);
-                const v32f q = mma(oa[j & 1], ob[j & 1][1]);
-                __builtin_amdgcn_sched_barrier(0);
-                fold(acc[0], p);
-                __builtin_amdgcn_sched_barrier(0);
-                if (j + 1 < NP || has_next)
-                    p = mma(oa[(j + 1) & 1], ob[(j + 1) & 1][0]);
-                __builtin_amdgcn_sched_barrier(0);
-                fold(acc[1], q);
-                __builtin_amdgcn_sched_barrier(0);
+                    rd(nxt_c, slot(cur, j + D), j + D - NP);
+                const int g = slot(cur, j), g1 = slot(cur, j + 1);
+                if constexpr (SN == 2) {
+                    const v32f q = mma(oa[g], ob[g][SN - 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[0], p);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j + 1 < NP || has_next)
+                        p = mma(oa[g1], ob[g1][0]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[SN - 1], q);
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    v32f q;
+                    const bool more = j + 1 < NP || has_next;
+                    if (more)
+                        q = mma(oa[g1], ob[g1][0]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[0], p);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (more)
+                        p = q;
+                }
             }
             if (kt + 2 < ktiles)
                 stash_slab(nn_c);
@@ -346,10 +385,27 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     }
 
     // Epilogue: for subtile (i, j) the lane owns rows m0+wm+32i+8(r/4)+4*half+(r%4) of column
-    // n0+wn+2col+j (three stages: both columns in one 8-byte store, every cell inside M x N)
-    // or n0+wn+32j+col.
+    // n0+wn+2col+j (three stages, two subtiles: both columns in one 8-byte store, every cell
+    // inside M x N) or n0+wn+32j+col.
     uint64_t key = kNoFault;
-    if constexpr (kStages == 3) {
+    if constexpr (kStages == 3 && SN == 1) {
+        const int c = n0 + wn + col;
+        const int cexp = check_risk ? exp_of(col_exp[c]) : 0;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
+            const float v = acc[0][r];
+            C[(size_t)row * N + c] = v;
+            bool bad = !finite_bits(v);
+            if (check_risk)
+                bad |= exp_of(row_exp[row]) + cexp < thr;
+            const uint64_t cell = (uint64_t)row * N + c;
+            if (bad)
+                key = cell < key ? cell : key;
+        }
+        wave_record_fault(key, suspect);
+        return;
+    } else if constexpr (kStages == 3) {
         const int c = n0 + wn + 2 * col;
         const int cexp0 = check_risk ? exp_of(col_exp[c]) : 0;
         const int cexp1 = check_risk ? exp_of(col_exp[c + 1]) : 0;
@@ -445,6 +501,29 @@ static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, co
 // 32 x 32, a 256 x 128 tile, 4-wave tiles of 128 x 64 and 64 x 64, and BK = 32 (which
 // spills with the pinned slab).
 using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
+// Outputs of fewer 128 x 128 tiles than CUs: 64 x 64 tiles of four 32 x 32 waves spread the
+// same work over four times the workgroups (one wave a SIMD on more CUs rather than two on
+// fewer). Whole tiles only.
+using SmallCfg = MfmaCfg<2, 2, 1, 1, 16, 4>;
+
+template <class Cfg>
+static bool small_whole(int M, int N, int K, bool ta, bool tb, const float *A, const float *B)
+{
+    const bool va = (ta ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
+    const bool vb = (tb ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
+    const uint64_t span_a = ta ? (uint64_t)M + 128 : 64 * (uint64_t)K, span_b = (uint64_t)N + 128;
+    const bool offsets32 = 4 * span_a <= UINT32_MAX && (tb || 4 * span_b <= UINT32_MAX);
+    return va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 && offsets32;
+}
+
+template <class Cfg, bool TA, bool TB>
+static void whole_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
+                           int K, const unsigned long long *re, const unsigned long long *ce,
+                           int thr, int risk, unsigned long long *suspect, NodeGate gate)
+{
+    const dim3 grid((unsigned)((M / Cfg::BM) * (N / Cfg::BN)));
+    hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, dim3(Cfg::kThreads), 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+}
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C,
@@ -452,7 +531,16 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 const unsigned long long *col_exp, int thr, int risk,
                                 unsigned long long *suspect, NodeGate gate)
 {
-    mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
+    const uint64_t big_tiles = (uint64_t)((M + GemmCfg::BM - 1) / GemmCfg::BM) * ((N + GemmCfg::BN - 1) / GemmCfg::BN);
+    if (big_tiles < 256 && small_whole<SmallCfg>(M, N, K, ta, tb, A, B)) {
+        const unsigned long long *re = row_exp, *ce = col_exp;
+        if (!ta && !tb) whole_dispatch<SmallCfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        else if (!ta && tb) whole_dispatch<SmallCfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        else if (ta && !tb) whole_dispatch<SmallCfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        else whole_dispatch<SmallCfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    } else {
+        mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
+    }
     return hipGetLastError();
 }
 

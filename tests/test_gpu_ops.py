@@ -486,22 +486,29 @@ def test_matmul_random_fault_placement_fuzz(ctx, pcu_pkg, dtype, engine):
             np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("grid", ["small", "full"])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
-def test_matmul_whole_tile_fuzz(ctx, pcu_pkg, dtype, engine):
+def test_matmul_whole_tile_fuzz(ctx, pcu_pkg, dtype, engine, grid):
     """The same first-fault fuzz over whole tiles only (M and N multiples of 128, K of 16),
     where the main kernels load operands straight into LDS in per-layout arrangements and run
-    three slabs a trip: 12 seeded cases over every layout and policy, a third of them clean
-    (bits compared) and the rest with up to five special operands, so faults land in
-    different slabs and stages; the GPU must give the oracle's first fault or, without one,
-    its bits."""
-    rng = np.random.default_rng(31 if dtype == np.float32 else 32)
+    three slabs a trip. "small" outputs have fewer 128 x 128 tiles than the GPU has CUs (F32
+    runs 64 x 64 tiles, F64 its narrow tile); "full" ones have at least as many (the 128 x
+    128 kernels). 12 seeded cases over every layout and policy, a third clean (bits
+    compared) and the rest with up to five special operands, so faults land in different
+    slabs and stages; the GPU must give the oracle's first fault or, without one, its bits."""
+    rng = np.random.default_rng((31 if dtype == np.float32 else 32) + (grid == "full") * 10)
     info = np.finfo(dtype)
     specials = np.array([np.nan, np.inf, -np.inf, info.max, -info.max,
                          info.tiny * dtype(2.0 ** 20), -info.tiny * dtype(3.0),
                          info.smallest_subnormal * dtype(3.0)], dtype=dtype)
+    full_shapes = [(2048, 2048), (4096, 1024), (1024, 4096), (2048, 2560)]
     for case in range(12):
-        m, n = (128 * int(v) for v in rng.integers(1, 4, size=2))
-        k = 16 * int(rng.integers(1, 25))
+        if grid == "small":
+            m, n = (128 * int(v) for v in rng.integers(1, 4, size=2))
+            k = 16 * int(rng.integers(1, 25))
+        else:
+            m, n = full_shapes[int(rng.integers(len(full_shapes)))]
+            k = 16 * int(rng.integers(1, 9))
         tl, tr = case % 2 == 1, (case // 2) % 2 == 1
         policy = int(rng.integers(3))
         a = rng.uniform(-1, 1, (k, m) if tl else (m, k)).astype(dtype)
