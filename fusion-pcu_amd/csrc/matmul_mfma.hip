@@ -559,8 +559,13 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_ge
     typedef float v16f __attribute__((ext_vector_type(16)));
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, SM = Cfg::SM, SN = Cfg::SN;
     constexpr int S = SM * SN;
-    __shared__ __align__(16) float As[2][BK][Cfg::LDA];
-    __shared__ __align__(16) float Bs[2][BK][Cfg::LDB];
+    // Whole tiles load op(A), and op(B) when untransposed, straight into LDS, in the strict
+    // kernel's layouts (k-major rows with odd rows rotated by 32 floats; op(A) untransposed
+    // in k quads), unpadded; a transposed op(B) goes through registers.
+    constexpr bool kDirectA = WHOLE, kDirectB = WHOLE && !TB;
+    constexpr int LDA = kDirectA ? BM : Cfg::LDA, LDB = kDirectB ? BN : Cfg::LDB;
+    __shared__ __align__(16) float As[2][BK][LDA];
+    __shared__ __align__(16) float Bs[2][BK][LDB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave / Cfg::WN) * SM * 32, wn = (wave % Cfg::WN) * SN * 32;
@@ -580,39 +585,132 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_native_ge
     const int ktiles = (K + BK - 1) / BK;
     if (WHOLE)
         stage.begin_whole(A, B, M, N, K, m0, n0, tid);
-    if (ktiles > 0) {
-        if (WHOLE)
-            stage.fetch_whole();
-        else
-            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
-        stage.stash(As[0], Bs[0], tid);
-    }
-    __syncthreads();
     const int half = lane >> 5, col = lane & 31;
-    for (int kt = 0; kt < ktiles; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) {
-            if (WHOLE)
-                stage.fetch_whole();
-            else
-                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+    if constexpr (WHOLE) {
+        // Wave w moves IPW 1 KiB runs of each directly loaded operand a slab: runs
+        // q = IPW w .. IPW w + IPW - 1, run q landing at 256 q floats of the stage. In rows of
+        // 128 floats run q is rows 2q (lanes 0-31) and 2q + 1 (lanes 32-63); in k quads it
+        // is quad q / 2, rows 64 (q % 2) + lane.
+        constexpr int W = Cfg::kThreads / 64, IPW = BM * BK / 256 / W;
+        static_assert(BM == 128 && BN == 128 && IPW * W * 256 == BM * BK && IPW % 2 == 0,
+                      "the runs below are laid out for 128 x 128 tiles");
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        const int rot = half ? (col + 8) & 31 : col;
+        const float *ga = nullptr, *gb = nullptr;
+        uint32_t lo_a = 0, lo_b = 0;
+        size_t da = 0, db = 0, ra = 0, rb = 0; // slab advance, and run r's base offset / r
+        if constexpr (!TA) {
+            // run q = IPW w + r: quad IPW w / 2 + r / 2, rows 64 (r % 2) + lane
+            ga = A + (size_t)m0 * K + 4 * (IPW / 2 * wv);
+            lo_a = (uint32_t)lane * (uint32_t)K * 4u;
+            da = BK;
+        } else {
+            ga = A + (size_t)(2 * IPW * wv) * M + m0;
+            lo_a = ((uint32_t)half * (uint32_t)M + 4u * rot) * 4u;
+            da = (size_t)BK * M;
+            ra = (size_t)2 * M;
         }
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            float a[SM], b[SN];
-#pragma unroll
-            for (int i = 0; i < SM; i++)
-                a[i] = As[cur][kk + half][wm + 32 * i + col];
-#pragma unroll
-            for (int j = 0; j < SN; j++)
-                b[j] = Bs[cur][kk + half][wn + 32 * j + col];
-#pragma unroll
-            for (int t = 0; t < S; t++)
-                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t / SN], b[t % SN], acc[t], 0, 0, 0);
+        if constexpr (kDirectB) {
+            gb = B + (size_t)(2 * IPW * wv) * N + n0;
+            lo_b = ((uint32_t)half * (uint32_t)N + 4u * rot) * 4u;
+            db = (size_t)BK * N;
+            rb = (size_t)2 * N;
         }
-        if (kt + 1 < ktiles)
-            stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+        auto run_a = [&](int r) {
+            return TA ? ga + r * ra : ga + (size_t)(64 * (r & 1)) * K + 4 * (r >> 1);
+        };
+        auto load_slab = [&](auto st_c) {
+            constexpr int st = decltype(st_c)::value;
+#pragma unroll
+            for (int r = 0; r < IPW; r++)
+                load_lds16(run_a(r), lo_a, &As[st][0][0] + 256 * (IPW * wv + r));
+            ga += da;
+            if constexpr (kDirectB) {
+#pragma unroll
+                for (int r = 0; r < IPW; r++)
+                    load_lds16(gb + r * rb, lo_b, &Bs[st][0][0] + 256 * (IPW * wv + r));
+                gb += db;
+            } else {
+                stage.fetch_whole_b();
+            }
+        };
+        auto stash_slab = [&](auto st_c) {
+            if constexpr (!kDirectB)
+                stage.stash_b(Bs[decltype(st_c)::value], tid);
+        };
+        // Operand offsets of k pair kk (k = kk + half) from the stage base.
+        auto a_at = [&](int kk, int i) {
+            const int m = wm + 32 * i + col;
+            return TA ? 128 * kk + (half ? 128 + ((m - 32) & 127) : m)
+                      : 512 * (kk >> 2) + (kk & 3) + 4 * m + half;
+        };
+        auto b_at = [&](int kk, int j) {
+            const int n = wn + 32 * j + col;
+            return kDirectB ? 128 * kk + (half ? 128 + ((n - 32) & 127) : n) : (kk + half) * LDB + n;
+        };
+        if (ktiles > 0) {
+            load_slab(std::integral_constant<int, 0>{});
+            stash_slab(std::integral_constant<int, 0>{});
+        }
+        wait_lds_loads();
         __syncthreads();
+        // Two slabs a trip, so each stage index is fixed at compile time.
+        auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+            constexpr int cur = decltype(cur_c)::value;
+            const std::integral_constant<int, cur ^ 1> nxt_c;
+            if (kt + 1 < ktiles)
+                load_slab(nxt_c);
+            const float *as = &As[cur][0][0], *bs = &Bs[cur][0][0];
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 2) {
+                float a[SM], b[SN];
+#pragma unroll
+                for (int i = 0; i < SM; i++)
+                    a[i] = as[a_at(kk, i)];
+#pragma unroll
+                for (int j = 0; j < SN; j++)
+                    b[j] = bs[b_at(kk, j)];
+#pragma unroll
+                for (int t = 0; t < S; t++)
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t / SN], b[t % SN], acc[t], 0, 0, 0);
+            }
+            if (kt + 1 < ktiles)
+                stash_slab(nxt_c);
+            wait_lds_loads();
+            __syncthreads();
+        };
+        for (int kt = 0; kt < ktiles; kt += 2) {
+            slab(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < ktiles)
+                slab(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    } else {
+        if (ktiles > 0) {
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+            stage.stash(As[0], Bs[0], tid);
+        }
+        __syncthreads();
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int cur = kt & 1;
+            if (kt + 1 < ktiles)
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 2) {
+                float a[SM], b[SN];
+#pragma unroll
+                for (int i = 0; i < SM; i++)
+                    a[i] = As[cur][kk + half][wm + 32 * i + col];
+#pragma unroll
+                for (int j = 0; j < SN; j++)
+                    b[j] = Bs[cur][kk + half][wn + 32 * j + col];
+#pragma unroll
+                for (int t = 0; t < S; t++)
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t / SN], b[t % SN], acc[t], 0, 0, 0);
+            }
+            if (kt + 1 < ktiles)
+                stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+            __syncthreads();
+        }
     }
 #pragma unroll
     for (int t = 0; t < S; t++) {
@@ -636,7 +734,10 @@ static void native_dispatch(hipStream_t s, const float *A, const float *B, float
     const dim3 block(Cfg::kThreads);
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0;
+    // Whole tiles load directly: a lane's byte offset from its run's base must fit 32 bits.
+    const uint64_t span_a = TA ? (uint64_t)M + 128 : 64 * (uint64_t)K, span_b = (uint64_t)N + 128;
+    const bool offsets32 = 4 * span_a <= UINT32_MAX && (TB || 4 * span_b <= UINT32_MAX);
+    const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 && offsets32;
     if (whole)
         hipLaunchKernelGGL((k_native_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, gate);
     else if (va && vb)

@@ -45,7 +45,9 @@ def _op(x, t):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 @pytest.mark.parametrize("shape", [(1, 1, 1), (65, 3, 17), (128, 256, 128), (300, 257, 130),
-                                   (200, 100, 260), (512, 1024, 384)])
+                                   (200, 100, 260), (512, 1024, 384),
+                                   # whole tiles with one and with three slabs of 32
+                                   (128, 32, 256), (256, 96, 384)])
 def test_native_matmul_within_the_dot_product_bound(ctx, dtype, shape):
     m, k, n = shape
     rng = np.random.default_rng(m + 3 * k + 7 * n)
