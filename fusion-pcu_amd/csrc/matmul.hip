@@ -422,7 +422,9 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-#pragma unroll(sizeof(T) == 4 ? BK : 2)
+            // Binary64 unrolls four k rows (220 VGPRs): two measured up to 6% slower by box
+            // and shape, a whole slab spills.
+#pragma unroll(sizeof(T) == 4 ? BK : 4)
             for (int k = 0; k < BK; k++) {
                 T a[8], b[8];
 #pragma unroll
