@@ -524,6 +524,26 @@ def test_matmul_whole_tile_fuzz(ctx, pcu_pkg, dtype, engine, grid):
             np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("shape", [(128, 0, 128), (2048, 0, 2048), (65, 0, 17), (0, 5, 7), (6, 5, 0)],
+                         ids=["small-grid", "full-grid", "ragged", "no-rows", "no-cols"])
+def test_matmul_empty_reduction_and_empty_output(ctx, pcu_pkg, dtype, shape, engine):
+    """An empty reduction (K = 0) leaves every cell at the +0 it starts from
+    (strict_matmul.rs:22-73), on whole tiles of either grid and on ragged ones, in every
+    layout and policy; an empty output launches nothing and is no fault."""
+    m, k, n = shape
+    for tl in (False, True):
+        for tr in (False, True):
+            a = np.zeros((k, m) if tl else (m, k), dtype)
+            b = np.zeros((n, k) if tr else (k, n), dtype)
+            for policy in (0, 1, 2):
+                got = ctx.strict_matmul(ctx.upload(a), ctx.upload(b), tl, tr, policy).numpy()
+                ref, rf = oracle.matmul(a, b, tl, tr, policy=policy)
+                assert rf is None and got.shape == (m, n)
+                np.testing.assert_array_equal(_bits(got), _bits(ref))
+                assert not _bits(got).any()
+
+
 @pytest.mark.parametrize("policy", [0, 1, 2])
 def test_matmul_signed_zero_and_subnormal_products(ctx, pcu_pkg, policy, engine):
     """Operands whose products are exact zeros of either sign, subnormal, or straddle the
