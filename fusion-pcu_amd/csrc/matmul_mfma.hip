@@ -360,22 +360,43 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 for (int jj = 0; jj < SN; jj++)
                     ob[j][jj] = Bs[cur][2 * j + half][wn + 32 * jj + col];
             };
-            static_assert(SM == 1 && SN == 2, "the pipeline below is written for two subtiles a wave");
-            rd(0);
-            v32f p = mma(oa[0][0], ob[0][0]);
+            static_assert(SM == 1 && (SN == 1 || SN == 2), "the pipeline below is written for one or two subtiles a wave");
+            if constexpr (SN == 2) {
+                rd(0);
+                v32f p = mma(oa[0][0], ob[0][0]);
 #pragma unroll
-            for (int j = 0; j < NP; j++) {
-                if (j + 1 < NP)
-                    rd(j + 1);
-                const v32f q = mma(oa[j][0], ob[j][1]);
-                __builtin_amdgcn_sched_barrier(0);
-                fold(acc[0], p);
-                __builtin_amdgcn_sched_barrier(0);
-                if (j + 1 < NP)
-                    p = mma(oa[j + 1][0], ob[j + 1][0]);
-                __builtin_amdgcn_sched_barrier(0);
-                fold(acc[1], q);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < NP; j++) {
+                    if (j + 1 < NP)
+                        rd(j + 1);
+                    const v32f q = mma(oa[j][0], ob[j][SN - 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[0], p);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j + 1 < NP)
+                        p = mma(oa[j + 1][0], ob[j + 1][0]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[SN - 1], q);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                // One subtile: each pair's MFMA is issued before the previous pair is folded,
+                // operands read two pairs ahead.
+                rd(0);
+                rd(1);
+                v32f p = mma(oa[0][0], ob[0][0]);
+#pragma unroll
+                for (int j = 0; j < NP; j++) {
+                    if (j + 2 < NP)
+                        rd(j + 2);
+                    v32f q;
+                    if (j + 1 < NP)
+                        q = mma(oa[j + 1][0], ob[j + 1][0]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fold(acc[0], p);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j + 1 < NP)
+                        p = q;
+                }
             }
             if (kt + 1 < ktiles)
                 stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
@@ -503,27 +524,8 @@ static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, co
 using GemmCfg = MfmaCfg<4, 2, 1, 2, 16, 4>;
 // Outputs of fewer 128 x 128 tiles than CUs: 64 x 64 tiles of four 32 x 32 waves spread the
 // same work over four times the workgroups (one wave a SIMD on more CUs rather than two on
-// fewer). Whole tiles only.
+// fewer).
 using SmallCfg = MfmaCfg<2, 2, 1, 1, 16, 4>;
-
-template <class Cfg>
-static bool small_whole(int M, int N, int K, bool ta, bool tb, const float *A, const float *B)
-{
-    const bool va = (ta ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
-    const bool vb = (tb ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
-    const uint64_t span_a = ta ? (uint64_t)M + 128 : 64 * (uint64_t)K, span_b = (uint64_t)N + 128;
-    const bool offsets32 = 4 * span_a <= UINT32_MAX && (tb || 4 * span_b <= UINT32_MAX);
-    return va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 && offsets32;
-}
-
-template <class Cfg, bool TA, bool TB>
-static void whole_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
-                           int K, const unsigned long long *re, const unsigned long long *ce,
-                           int thr, int risk, unsigned long long *suspect, NodeGate gate)
-{
-    const dim3 grid((unsigned)((M / Cfg::BM) * (N / Cfg::BN)));
-    hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, dim3(Cfg::kThreads), 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-}
 
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C,
@@ -532,15 +534,10 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 unsigned long long *suspect, NodeGate gate)
 {
     const uint64_t big_tiles = (uint64_t)((M + GemmCfg::BM - 1) / GemmCfg::BM) * ((N + GemmCfg::BN - 1) / GemmCfg::BN);
-    if (big_tiles < 256 && small_whole<SmallCfg>(M, N, K, ta, tb, A, B)) {
-        const unsigned long long *re = row_exp, *ce = col_exp;
-        if (!ta && !tb) whole_dispatch<SmallCfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-        else if (!ta && tb) whole_dispatch<SmallCfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-        else if (ta && !tb) whole_dispatch<SmallCfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-        else whole_dispatch<SmallCfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-    } else {
+    if (big_tiles < 256)
+        mfma_launch<SmallCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
+    else
         mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
-    }
     return hipGetLastError();
 }
 
