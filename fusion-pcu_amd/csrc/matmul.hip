@@ -838,13 +838,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
 
 // --------------------------------------------------------------- exact replay
 
-// First fault of one output cell, found by a whole wave (every lane returns the same). The
-// K products are classified 64 at a time in k order, which gives the first faulting
-// Multiply k_m. When `walk_adds` is set (a non-finite result, where a sum can overflow, or
-// RejectSubnormal, where a subnormal sum faults), the ordered sums before k_m are then
-// formed exactly as the contract orders them: the lanes form 64 products at a time and
-// every lane folds them in k order with the exact add classifier. Returns kNoFault or the
-// packed fault word.
+// Lane l's value of v, on every lane (l uniform across the wave).
+__device__ __forceinline__ float lane_value(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double lane_value(double v, int l)
+{
+    const uint64_t x = bits_of(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// First fault of one output cell, found by a whole wave (every lane returns the same). One
+// pass over k in chunks of 64, the next chunk's operands loaded while the current one is
+// classified: the lanes form the chunk's products and classify them, which gives the
+// chunk's first faulting Multiply. When `walk_adds` is set (a non-finite result, where a sum
+// can overflow, or RejectSubnormal, where a subnormal sum faults), every lane then folds the
+// chunk's products before that Multiply in k order, as the contract orders the sums. Those
+// products are finite, so a sum there can only fault by overflowing (the running sum turns,
+// and stays, infinite) or, under RejectSubnormal, by being subnormal: the chunk is folded
+// with plain adds and that check, and only a chunk that trips it is folded again with the
+// exact add classifier to name the step. A Multiply at k comes before the Add at k. Returns
+// kNoFault or the packed fault word.
 template <typename T>
 __device__ __forceinline__ uint64_t cell_first_fault(const T *__restrict__ A, const T *__restrict__ B,
                                                      uint64_t M, uint64_t N, uint64_t K, int ta,
@@ -853,47 +870,63 @@ __device__ __forceinline__ uint64_t cell_first_fault(const T *__restrict__ A, co
 {
     const int lane = threadIdx.x & 63;
     const uint64_t r = cell / N, c = cell % N;
-    auto a_at = [&](uint64_t k) { return ta ? A[k * M + r] : A[r * K + k]; };
-    auto b_at = [&](uint64_t k) { return tb ? B[c * K + k] : B[k * N + c]; };
-    uint64_t k_m = K;
-    uint32_t kind_m = kOk;
-    for (uint64_t k0 = 0; k0 < K; k0 += 64) {
+    auto load = [&](uint64_t k0, T &a, T &b) {
         const uint64_t k = k0 + lane;
-        uint32_t kind = kOk;
+        a = (T)0;
+        b = (T)0;
         if (k < K) {
-            const T a = a_at(k), b = b_at(k);
-            kind = classify_mul(a, b, a * b, policy);
+            a = ta ? A[k * M + r] : A[r * K + k];
+            b = tb ? B[c * K + k] : B[k * N + c];
         }
+    };
+    const bool reject_sub = policy == kPolicyRejectSubnormal;
+    T total = (T)0;
+    T a, b;
+    load(0, a, b);
+    for (uint64_t k0 = 0; k0 < K; k0 += 64) {
+        T na = (T)0, nb = (T)0;
+        if (k0 + 64 < K)
+            load(k0 + 64, na, nb);
+        const T p = a * b;
+        uint32_t kind = kOk;
+        if (k0 + lane < K)
+            kind = classify_mul(a, b, p, policy);
         const uint64_t mask = __ballot(kind != kOk);
-        if (mask) {
-            const int l = __ffsll((long long)mask) - 1;
-            k_m = k0 + l;
-            kind_m = __shfl(kind, l, 64);
-            break;
-        }
-    }
-    if (walk_adds) {
-        T total = (T)0;
-        for (uint64_t k0 = 0; k0 < k_m; k0 += 64) {
-            const uint64_t k = k0 + lane;
-            T p = (T)0;
-            if (k < k_m) {
-                const T a = a_at(k), b = b_at(k);
-                p = a * b;
+        const int l_m = mask ? __ffsll((long long)mask) - 1 : 64;
+        if (walk_adds) {
+            const int in_k = K - k0 < 64 ? (int)(K - k0) : 64;
+            const int here = l_m < in_k ? l_m : in_k; // products summed before any fault
+            T t = total;
+            bool sub = false;
+            if (here == 64) {
+#pragma unroll
+                for (int j = 0; j < 64; j++) {
+                    t = t + lane_value(p, j);
+                    sub |= reject_sub && subnormal(t);
+                }
+            } else {
+                for (int j = 0; j < here; j++) {
+                    t = t + lane_value(p, j);
+                    sub |= reject_sub && subnormal(t);
+                }
             }
-            const int here = k_m - k0 < 64 ? (int)(k_m - k0) : 64;
-            for (int j = 0; j < here; j++) {
-                const T pj = __shfl(p, j, 64);
-                const T nxt = total + pj;
-                const uint32_t kind = classify_add(total, pj, nxt, policy);
-                if (kind != kOk)
-                    return pack_fault((cell * K + k0 + j) * 2 + 1, kind);
-                total = nxt;
+            if (!finite_bits(t) || sub) {
+                for (int j = 0; j < here; j++) {
+                    const T pj = lane_value(p, j);
+                    const T nxt = total + pj;
+                    const uint32_t k_add = classify_add(total, pj, nxt, policy);
+                    if (k_add != kOk)
+                        return pack_fault((cell * K + k0 + j) * 2 + 1, k_add);
+                    total = nxt;
+                }
             }
+            total = t;
         }
+        if (mask)
+            return pack_fault((cell * K + k0 + l_m) * 2, __shfl(kind, l_m, 64));
+        a = na;
+        b = nb;
     }
-    if (k_m < K)
-        return pack_fault((cell * K + k_m) * 2, kind_m);
     return kNoFault;
 }
 
@@ -945,6 +978,17 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
     const int lane = threadIdx.x & 63;
     const uint64_t waves = (uint64_t)gridDim.x * (blockDim.x / 64);
     const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    // The first suspect cell holds a fault when its result is not finite (an invalid operand,
+    // or an overflow, leaves Inf or NaN for good), and no earlier cell can hold one (none is
+    // marked or non-finite): that cell's first fault is the MatMul's, and one wave finds it.
+    if (!finite_bits(C[first])) {
+        if (wave == 0) {
+            const uint64_t w = cell_first_fault(A, B, M, N, K, ta, tb, first, policy, true);
+            if (w != kNoFault)
+                record(w);
+        }
+        return;
+    }
     for (uint64_t c0 = (first / 64 + wave) * 64; c0 < cells; c0 += waves * 64) {
         if (best_cell() < c0)
             break; // this wave's blocks only grow

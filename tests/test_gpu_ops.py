@@ -808,6 +808,65 @@ def test_output_overlapping_an_operand_is_rejected(ctx, pcu_pkg):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_first_fault_late_in_a_long_reduction(ctx, pcu_pkg, dtype, engine):
+    """The replay's walk of one cell over K = 1000 (sixteen chunks of 64, the last one
+    partial), every layout and policy, against the oracle: (a) cell (2, 3) overflows in the
+    Add at k 700, its first non-finite cell; (b) the same with a NaN at k 650 of column 3,
+    so cell (0, 3)'s Multiply at k 650 is first; (c) the overflow moved into the partial
+    last chunk (k 990); (d) the k 700 overflow with a NaN and an infinity in later rows, whose
+    cells are all non-finite; (e) row 1 zero but for two normal products at k 400 and 500
+    whose sum is subnormal: finite cells the screen marks, where RejectSubnormal faults in
+    the Add at k 500 of cell (1, 0) and the other policies have no fault."""
+    m, k, n = 5, 1000, 7
+    f32 = dtype == np.float32
+    rng = np.random.default_rng(77 if f32 else 78)
+    huge = dtype(3.0e38) if f32 else dtype(1.7e308)
+
+    def base(k1, k2):
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        a[2, k1] = a[2, k2] = huge
+        b[k1, :] = b[k2, :] = dtype(0.25)  # the other columns of row 2 stay finite
+        b[k1, 3] = b[k2, 3] = dtype(1.0)
+        return a, b
+
+    cases = [("add-overflow-k700", *base(100, 700))]
+    a, b = base(100, 700)
+    b[650, 3] = np.nan
+    cases.append(("mul-invalid-k650", a, b))
+    cases.append(("add-overflow-k990", *base(30, 990)))
+    a, b = base(100, 700)
+    a[3, 900], a[4, 10] = np.nan, np.inf
+    cases.append(("overflow-before-later-nan", a, b))
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    e = -125 if f32 else -1021
+    a[1, :] = 0
+    a[1, 400], a[1, 500] = dtype(2.0 ** e), dtype(-1.25 * 2.0 ** e)
+    b[400, :] = b[500, :] = dtype(1.0)
+    cases.append(("subnormal-sum-k500", a, b))
+    want = {"add-overflow-k700": (2 * n + 3, 700), "mul-invalid-k650": (3, 650),
+            "add-overflow-k990": (2 * n + 3, 990), "overflow-before-later-nan": (2 * n + 3, 700)}
+    for name, a, b in cases:
+        for tl in (False, True):
+            for tr in (False, True):
+                aa = np.ascontiguousarray(a.T) if tl else a
+                bb = np.ascontiguousarray(b.T) if tr else b
+                for policy in (0, 1, 2):
+                    got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), tl, tr, policy).numpy())
+                    ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+                    assert gf == _ofault(rf), (name, tl, tr, policy, gf, rf)
+                    if rf is None:
+                        np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{name} {tl} {tr} {policy}")
+                    if name in want:
+                        assert _ofault(rf)[:2] == want[name], (name, policy, rf)
+                    elif policy == 1:
+                        assert _ofault(rf)[:2] == (n, 500), rf
+                    else:
+                        assert rf is None, (name, policy, rf)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 def test_matmul_replay_paths_for_marked_cells(ctx, pcu_pkg, dtype, engine):
     """The replay's two passes under the IEEE policy, every layout, against the oracle:
     (a) every cell marked by the exponent screen, no tiny product, no fault (the tiled tiny
