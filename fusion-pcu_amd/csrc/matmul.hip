@@ -14,9 +14,10 @@
 //                 invalid operand or an overflow leaves) or when the two exponents allow a
 //                 product small enough to be tiny (the only way an underflow can arise),
 //                 and keeps the first suspect cell with one atomicMin per wave.
-//  3. tiny scan   (IEEE policy, only when a cell is marked) a tiled pass like the main
-//                 kernel over the tiles the screen marks, finding the cells that have a
-//                 product at most the smallest normal; see k_gemm_tiny_scan.
+//  3. tiny scan   (IEEE policy, only when a cell is marked) a tiled pass over the tiles
+//                 the screen marks, finding the cells that can have a tiny product from the
+//                 smallest exponent sum over k (16-bit exponents, packed); see
+//                 k_gemm_tiny_scan.
 //  4. replay      exact ordered re-execution in row-major order from the first suspect:
 //                 non-finite cells walked serially, per-op classified; cells the scan
 //                 flagged have their K products classified in parallel by a wave. Both stop
@@ -711,19 +712,38 @@ __global__ __launch_bounds__(256, 3) void k_strict_gemm_f64n(
 // ------------------------------------------------------------------ tiny scan
 // IEEE policy. A cell whose result is finite met no invalid operand and no overflow (both
 // leave Inf or NaN for good), and a sum is never tiny-inexact, so its first fault can only
-// be a Multiply whose product is tiny and inexact. This tiled pass finds the cells that have
-// any product at most the smallest normal from a nonzero, finite pair of operands: per cell
-// the smallest |a * b| over k, two vector instructions per (cell, k) like the strict kernel.
-// Zero and non-finite operands are staged as 2^64, whose products are never that small (a
-// non-finite operand makes its whole row or column non-finite, which the serial replay
-// walks). For each output row it keeps the first such column, and the first such row
-// overall. It runs only when the screen marked a cell, and skips every tile whose row and
-// column exponents rule out a tiny product.
-template <typename T> __device__ __forceinline__ T tiny_scan_operand(T x)
+// be a Multiply whose product is tiny and inexact. This tiled pass narrows the screen's marks
+// to the cells that can have one, for the replay to classify exactly. A tiny product a * b
+// (|a b| < 2^emin before rounding, emin the smallest normal exponent) has
+// floor(log2|a|) + floor(log2|b|) < emin, since |a b| >= 2^(ea + eb). So per cell the pass
+// takes the smallest exponent sum over k, a (min, +) product of 16-bit exponents, two cells
+// per packed add and packed min (one instruction per (cell, k)), and flags the cell when
+// that sum is below emin: every cell with a tiny product, and a few whose smallest products
+// lie in [2^emin, 2^(emin + 1)). Zero and non-finite operands carry exponent 16000, so
+// their sums never flag (a non-finite operand makes its whole row or column non-finite,
+// which the serial replay walks). For each output row it keeps the first flagged column,
+// and the first flagged row overall. It runs only when the screen marked a cell, skips
+// every tile whose row and column exponents rule out a tiny product, and within a tile
+// every k slab whose smallest A exponent and smallest B exponent (over the tile's rows and
+// columns) do.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+constexpr short kScanExpNone = 16000; // exponent of zero and non-finite operands
+
+template <typename T> __device__ __forceinline__ short scan_exp(T x)
 {
-    const T stand_in = (T)18446744073709551616.0; // 2^64
-    return (x == (T)0 || !finite_bits(x)) ? stand_in : x;
+    const int e = ilog2_abs(x);
+    return (short)(e == kExpNone ? kScanExpNone : e);
 }
+
+// Tile of the scan: 128 x 128 cells per 256-thread workgroup, thread (tx, ty) owning rows
+// 8 ty .. 8 ty + 7 and columns 8 tx .. 8 tx + 7, so each k row of a stage gives it its eight
+// A exponents and eight B exponents as one 16-byte LDS read each. Slabs of 16 k.
+template <typename T> struct ScanCfg {
+    static constexpr int BM = 128, BN = 128, BK = 16, kThreads = 256;
+    static constexpr int LDA = BM, LDB = BN; // (the exponent stages below have their own)
+    static constexpr int EA = BM * BK / kThreads, EB = BN * BK / kThreads;
+    template <bool TA> static constexpr bool kSplitRunsB = false;
+};
 
 template <typename T, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
@@ -736,11 +756,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
         return;
     if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault)
         return; // no cell marked: nothing to scan (the same word for every thread)
-    using Cfg = ValuCfg<T>;
-    constexpr int BK = Cfg::BK;
-    __shared__ __align__(16) T As[2][BK][Cfg::LDA];
-    __shared__ __align__(16) T Bs[2][BK][Cfg::LDB];
+    using Cfg = ScanCfg<T>;
+    constexpr int BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
+    // k-major exponent stages; rows padded by 8 exponents (16 bytes) so the scattered
+    // exponent stores of a transposing stash spread over the banks.
+    constexpr int LA = BM + 8, LB = BN + 8;
+    __shared__ __align__(16) short Ae[2][BK][LA];
+    __shared__ __align__(16) short Be[2][BK][LB];
     __shared__ int tile_min[2];
+    __shared__ int slab_min[2][2][4]; // stage, operand, wave
 
     const int tid = threadIdx.x;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -767,67 +791,115 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
         return;
 
     const int tx = tid % 16, ty = tid / 16;
-    constexpr int RUN = 16 / sizeof(T), RUNS = 8 / RUN, RUN_STRIDE = BN / RUNS;
-    auto col_of = [&](int j) { return (j / RUN) * RUN_STRIDE + tx * RUN + (j % RUN); };
-    T mn[8][8];
+    s16x2 mn[8][4]; // row i, columns 2 jp and 2 jp + 1
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            mn[i][j] = (T)INFINITY;
+        for (int jp = 0; jp < 4; jp++)
+            mn[i][jp] = (s16x2){kScanExpNone, kScanExpNone};
 
+    // Global -> registers with the MatMul kernels' staging (elements outside the matrices
+    // stage as +0, exponent 16000); registers -> LDS as exponents.
     SlabStager<T, Cfg, TA, TB, VA, VB> stage;
-    auto stage_mapped = [&](int buf) {
+    // Also folds the slab's smallest A and B exponents, one word per wave.
+    auto stash = [&](int buf) {
+        short ea[EA], eb[EB];
+        int amin = kScanExpNone, bmin = kScanExpNone;
 #pragma unroll
-        for (int i = 0; i < Cfg::EA; i++)
-            stage.ra[i] = tiny_scan_operand(stage.ra[i]);
+        for (int i = 0; i < EA; i++) {
+            ea[i] = scan_exp(stage.ra[i]);
+            amin = ea[i] < amin ? ea[i] : amin;
+        }
 #pragma unroll
-        for (int i = 0; i < Cfg::EB; i++)
-            stage.rb[i] = tiny_scan_operand(stage.rb[i]);
-        stage.stash(As[buf], Bs[buf], tid);
+        for (int i = 0; i < EB; i++) {
+            eb[i] = scan_exp(stage.rb[i]);
+            bmin = eb[i] < bmin ? eb[i] : bmin;
+        }
+        if (!TA) { // thread: row m, k run of EA
+            const int m = tid / (BK / EA), k = (tid % (BK / EA)) * EA;
+#pragma unroll
+            for (int i = 0; i < EA; i++)
+                Ae[buf][k + i][m] = ea[i];
+        } else {   // thread: k row, m run of EA
+            const int k = tid / (BM / EA), m = (tid % (BM / EA)) * EA;
+#pragma unroll
+            for (int i = 0; i < EA; i++)
+                Ae[buf][k][m + i] = ea[i];
+        }
+        if (!TB) { // thread: k row, n run of EB
+            const int k = tid / (BN / EB), n = (tid % (BN / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
+                Be[buf][k][n + i] = eb[i];
+        } else {   // thread: column n, k run of EB
+            const int n = tid / (BK / EB), k = (tid % (BK / EB)) * EB;
+#pragma unroll
+            for (int i = 0; i < EB; i++)
+                Be[buf][k + i][n] = eb[i];
+        }
+        amin = wave_min_i32(amin);
+        bmin = wave_min_i32(bmin);
+        if ((tid & 63) == 0) {
+            slab_min[buf][0][tid >> 6] = amin;
+            slab_min[buf][1][tid >> 6] = bmin;
+        }
     };
     const int ktiles = (K + BK - 1) / BK;
     if (ktiles > 0) {
         stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
-        stage_mapped(0);
+        stash(0);
     }
     __syncthreads();
     for (int kt = 0; kt < ktiles; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < ktiles)
             stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
-#pragma unroll(sizeof(T) == 4 ? BK : 2)
-        for (int k = 0; k < BK; k++) {
-            T a[8], b[8];
+        int amin = slab_min[cur][0][0], bmin = slab_min[cur][1][0];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                a[i] = As[cur][k][ty * 4 + i];
-                a[4 + i] = As[cur][k][64 + ty * 4 + i];
+        for (int w = 1; w < 4; w++) {
+            amin = slab_min[cur][0][w] < amin ? slab_min[cur][0][w] : amin;
+            bmin = slab_min[cur][1][w] < bmin ? slab_min[cur][1][w] : bmin;
+        }
+        // Every sum of this slab is at least amin + bmin (the same value on every thread).
+        if (amin + bmin < thr) {
+#pragma unroll 4
+            for (int k = 0; k < BK; k++) {
+                const uint4 av = *reinterpret_cast<const uint4 *>(&Ae[cur][k][8 * ty]);
+                const uint4 bv = *reinterpret_cast<const uint4 *>(&Be[cur][k][8 * tx]);
+                const short *a = reinterpret_cast<const short *>(&av);
+                const s16x2 *b = reinterpret_cast<const s16x2 *>(&bv);
+                // The k row's 32 packed sums first, then the 32 packed minima: no minimum
+                // waits on the sum just before it.
+                s16x2 t[8][4];
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int jp = 0; jp < 4; jp++)
+                        t[i][jp] = (s16x2){a[i], a[i]} + b[jp];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int jp = 0; jp < 4; jp++)
+                        mn[i][jp] = __builtin_elementwise_min(mn[i][jp], t[i][jp]);
+                __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                b[j] = Bs[cur][k][col_of(j)];
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    mn[i][j] = fmin(mn[i][j], fabs(a[i] * b[j]));
         }
         if (kt + 1 < ktiles)
-            stage_mapped(cur ^ 1);
+            stash(cur ^ 1);
         __syncthreads();
     }
-    // Past the edges the operands stage as +0, mapped to 2^64: those cells never flag.
-    const T min_normal = sizeof(T) == 4 ? (T)1.17549435082228750797e-38 : (T)2.2250738585072014e-308;
+    // Past the edges the operands stage as +0 (exponent 16000): those cells never flag.
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int r = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+        const int r = m0 + 8 * ty + i;
         uint32_t first = 0xffffffffu;
 #pragma unroll
         for (int j = 7; j >= 0; j--) {
-            const int c = n0 + col_of(j);
-            if (c < N && mn[i][j] <= min_normal)
-                first = (uint32_t)c < first ? (uint32_t)c : first;
+            const int c = n0 + 8 * tx + j;
+            const int e = (j & 1) ? mn[i][j >> 1].y : mn[i][j >> 1].x;
+            if (c < N && e < thr)
+                first = (uint32_t)c;
         }
         if (r < M && first != 0xffffffffu) {
             atomicMax(&row_flag[r], ((unsigned long long)gen << 32) | (0xffffffffu - first));
