@@ -1297,6 +1297,116 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
     }
 }
 
+// Small inputs (n <= kMseSerialMax), one workgroup. Its four waves form every difference and
+// square in parallel into LDS and find the first faulting Subtract or Multiply; then one wave
+// folds the squares before that element into the total in order, 64 at a time, each lane
+// holding the chunk's squares in registers. The squares folded are finite, so a sum can only
+// fault by overflowing (the total turns, and stays, infinite) or, under RejectSubnormal, by
+// being subnormal: a chunk is folded with plain adds (under RejectSubnormal each partial
+// total is kept and checked after), and folded again with the exact add classifier only when
+// that trips. The same results and first fault as the pipeline above, in one launch and no
+// scratch.
+template <typename T, bool REJECT_SUB>
+__global__ __launch_bounds__(256) void k_mse_serial(const T *__restrict__ p, const T *__restrict__ t,
+                                                    uint64_t n, T count, int policy,
+                                                    T *__restrict__ out, unsigned long long *fault,
+                                                    NodeGate gate)
+{
+    if (block_gate_closed(gate))
+        return;
+    constexpr int P = 16 / sizeof(T); // squares per 16-byte LDS read
+    __shared__ __align__(16) T sq[kMseSerialMax];
+    __shared__ unsigned long long first_sm; // earliest Subtract or Multiply fault word
+    const int tid = threadIdx.x;
+    if (tid == 0)
+        first_sm = kNoFault;
+    __syncthreads();
+    uint64_t key = kNoFault;
+    for (uint64_t i = tid; i < n; i += 256) {
+        const T pv = p[i], tv = t[i];
+        const T d = pv - tv;
+        const T s = d * d;
+        sq[i] = s;
+        if (key == kNoFault) {
+            const uint32_t ks = classify_add(pv, tv, d, policy);
+            if (ks != kOk) {
+                key = pack_fault(3 * i, ks);
+            } else {
+                const uint32_t km = classify_mul(d, d, s, policy);
+                if (km != kOk)
+                    key = pack_fault(3 * i + 1, km);
+            }
+        }
+    }
+    if (key != kNoFault)
+        atomicMin(&first_sm, (unsigned long long)key);
+    __syncthreads();
+    if (tid >= 64)
+        return;
+    const unsigned long long fsm = first_sm;
+    const uint64_t limit = fsm == kNoFault ? n : ((fsm >> 3) / 3); // elements summed
+    auto record = [&](uint64_t w) {
+        if (tid == 0) {
+            atomicMin(fault, (unsigned long long)w);
+            gate_record(gate);
+        }
+    };
+    T total = (T)0;
+    for (uint64_t i0 = 0; i0 < limit; i0 += 64) {
+        const int here = limit - i0 < 64 ? (int)(limit - i0) : 64;
+        T sum = total;
+        bool trip = false;
+        if (here == 64) {
+            T v[64];
+#pragma unroll
+            for (int q = 0; q < 64 / P; q++)
+                *reinterpret_cast<uint4 *>(&v[P * q]) = *reinterpret_cast<const uint4 *>(&sq[i0 + P * q]);
+            if constexpr (!REJECT_SUB) {
+#pragma unroll
+                for (int j = 0; j < 64; j++)
+                    sum = sum + v[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 64; j++) {
+                    sum = sum + v[j];
+                    v[j] = sum;
+                }
+#pragma unroll
+                for (int j = 0; j < 64; j++)
+                    trip |= subnormal(v[j]);
+            }
+        } else {
+            for (int j = 0; j < here; j++) {
+                sum = sum + sq[i0 + j];
+                trip |= REJECT_SUB && subnormal(sum);
+            }
+        }
+        if (!finite_bits(sum) || trip) {
+            for (int j = 0; j < here; j++) {
+                const T sj = sq[i0 + j];
+                const T nxt = total + sj;
+                const uint32_t k_add = classify_add(total, sj, nxt, policy);
+                if (k_add != kOk) {
+                    record(pack_fault(3 * (i0 + j) + 2, k_add));
+                    return;
+                }
+                total = nxt;
+            }
+        }
+        total = sum;
+    }
+    if (fsm != kNoFault) {
+        record(fsm);
+        return;
+    }
+    const T r = total / count;
+    const uint32_t kind = classify_div(total, count, r, policy);
+    if (kind != kOk)
+        record(pack_fault(3 * n, kind));
+    else if (tid == 0)
+        *out = r;
+}
+
 // ------------------------------------------------------------- native compounds
 // Explicitly permitted native compound arithmetic (Boundary + BackendDefined): no fault is
 // classified; special values and subnormals flow through as the hardware produces them.
@@ -1628,6 +1738,24 @@ hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, 
         return hipErrorInvalidValue;
     return dtype == 0 ? mse_walk_t<float>(s, n, scratch, (float)count, out, policy, fault, gate)
                       : mse_walk_t<double>(s, n, scratch, count, out, policy, fault, gate);
+}
+
+hipError_t launch_mse_serial(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                             double count, void *out, int policy, unsigned long long *fault,
+                             NodeGate gate)
+{
+    if (n == 0 || n > kMseSerialMax)
+        return hipErrorInvalidValue;
+    const bool rs = policy == kPolicyRejectSubnormal;
+    if (dtype == 0 && rs)
+        hipLaunchKernelGGL((k_mse_serial<float, true>), dim3(1), dim3(256), 0, s, (const float *)p, (const float *)t, n, (float)count, policy, (float *)out, fault, gate);
+    else if (dtype == 0)
+        hipLaunchKernelGGL((k_mse_serial<float, false>), dim3(1), dim3(256), 0, s, (const float *)p, (const float *)t, n, (float)count, policy, (float *)out, fault, gate);
+    else if (rs)
+        hipLaunchKernelGGL((k_mse_serial<double, true>), dim3(1), dim3(256), 0, s, (const double *)p, (const double *)t, n, count, policy, (double *)out, fault, gate);
+    else
+        hipLaunchKernelGGL((k_mse_serial<double, false>), dim3(1), dim3(256), 0, s, (const double *)p, (const double *)t, n, count, policy, (double *)out, fault, gate);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------ native launchers

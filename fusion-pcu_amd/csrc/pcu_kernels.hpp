@@ -40,6 +40,11 @@ hipError_t launch_mse_prepare(hipStream_t s, int dtype, uint64_t n, const void *
                               void *scratch, int policy, unsigned long long *fault, NodeGate gate);
 hipError_t launch_mse_walk(hipStream_t s, int dtype, uint64_t n, void *scratch, double count,
                            void *out, int policy, unsigned long long *fault, NodeGate gate);
+// Strict MSE of at most kMseSerialMax elements in one launch of one workgroup, no scratch.
+constexpr uint64_t kMseSerialMax = 4096;
+hipError_t launch_mse_serial(hipStream_t s, int dtype, uint64_t n, const void *p, const void *t,
+                             double count, void *out, int policy, unsigned long long *fault,
+                             NodeGate gate);
 
 // Strict MatMul scratch. Exponent words (generation << 32 | bias - minimum exponent) of
 // op(A) rows and op(B) columns; per output row, the first column whose cell has a product

@@ -906,6 +906,27 @@ pcu_status Ctx::op_mse(int dtype, uint64_t n, const void *p, const void *t, void
     pcu_status st = add_node(NodeInfo{Prim::Mse, n, 0}, &word);
     if (st)
         return st;
+    if (n <= kMseSerialMax) {
+        // One wave folds a small input in order; it overlaps the following work on the side
+        // stream as the walk does.
+        if ((st = open_words()))
+            return st;
+        hipStream_t s = stream;
+        if (on_side) {
+            if ((st = hip(hipEventRecord(main_ready, stream), "hipEventRecord")))
+                return st;
+            if ((st = hip(hipStreamWaitEvent(side, main_ready, 0), "hipStreamWaitEvent")))
+                return st;
+            s = side;
+            side_pending = true;
+        }
+        hipEvent_t t1 = timer_start(s);
+        if ((st = hip(launch_mse_serial(s, dtype, n, p, t, count_as(dtype, n), out, policy, word,
+                                        gate_for(word)), "strict_mse launch")))
+            return st;
+        timer_stop(PCU_KERNEL_MSE, t1, s);
+        return PCU_OK;
+    }
     void *sq = nullptr;
     if ((st = scratch(mse_scratch, mse_scratch_bytes(dtype, n), true, &sq)))
         return st;

@@ -242,9 +242,12 @@ def test_mse_parity(ctx, pcu_pkg, dtype, n):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
-def test_mse_faults_parity(ctx, pcu_pkg, dtype):
+@pytest.mark.parametrize("n", [1000, 30_000], ids=["one-workgroup", "pipeline"])
+def test_mse_faults_parity(ctx, pcu_pkg, dtype, n):
+    """Invalid, Multiply overflow, Add overflow, tiny squares and a lone tiny square under
+    every policy, at a size the one-workgroup kernel takes (at most 4096 elements) and at one
+    the parallel pipeline takes."""
     rng = np.random.default_rng(77)
-    n = 30_000
     big = np.finfo(dtype).max
     cases = []
     p = rng.uniform(-1, 1, n).astype(dtype); t = rng.uniform(-1, 1, n).astype(dtype)
