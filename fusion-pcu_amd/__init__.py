@@ -218,8 +218,10 @@ class Context:
         self.check(self._lib.pcu_fault_reset(self.handle))
 
     def set_matmul_engine(self, engine: str) -> None:
-        """Main-kernel engine of the strict F32 MatMul ("auto", "valu", "mfma_products");
-        every engine gives the same bits."""
+        """Engine of the strict MatMul ("auto", "valu", "mfma_products"); every engine gives
+        the same bits and first fault. "auto" runs small outputs (at most 256 x 256 cells for
+        F32, 512 x 512 for F64) as one fused launch and larger F32 ones with matrix-core
+        products; "valu" and "mfma_products" always take the screened tile kernels."""
         self.check(self._lib.pcu_ctx_set_matmul_engine(self.handle, self.MATMUL_ENGINES[engine]))
 
     @property

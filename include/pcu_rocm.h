@@ -115,13 +115,16 @@ int pcu_abi_version(void);
 void *pcu_ctx_stream(pcu_ctx *ctx);
 pcu_status pcu_ctx_synchronize(pcu_ctx *ctx);
 
-/* Engine of the strict F32 MatMul's main kernel. Both give the same bits.
- *  PCU_MATMUL_VALU: each product is a v_mul_f32 and each sum a v_add_f32.
- *  PCU_MATMUL_MFMA_PRODUCTS: the matrix cores act as a multiplier array only
+/* Engine of the strict MatMul. Every engine gives the same bits and the same first fault.
+ *  PCU_MATMUL_VALU: each product is a v_mul and each sum a v_add (F32 and F64).
+ *  PCU_MATMUL_MFMA_PRODUCTS: for F32 the matrix cores act as a multiplier array only
  *   (v_mfma_f32_32x32x1_2b_f32, K = 1, +0 accumulator input): every element is one
  *   product rounded once. The ordered sums stay separate v_add_f32 in k order, and no
- *   sum is formed in the matrix core.
- *  PCU_MATMUL_AUTO (default): MFMA products for F32; F64 always uses the vector unit.
+ *   sum is formed in the matrix core. F64 uses the vector unit.
+ *  PCU_MATMUL_AUTO (default): outputs of at most 256 x 256 cells (F32) or 512 x 512 (F64)
+ *   run as one fused launch on the vector unit (screen, products and sums, and the exact
+ *   first-fault search per 16 x 16 block); larger ones as PCU_MATMUL_MFMA_PRODUCTS.
+ *   Choosing VALU or MFMA_PRODUCTS always takes the screened tile kernels.
  * No counterpart in the reference, whose strict MatMul is one integer-emulated thread
  * per cell (backends/rocm/tensor/strict_matmul/strict_matmul.rs:187-239). */
 typedef enum pcu_matmul_engine {

@@ -360,13 +360,15 @@ def test_mse_ordered_sum_uneven_chunks(ctx, pcu_pkg, dtype):
 # ------------------------------------------------------------------- MatMul
 
 
-ENGINES = ["valu", "mfma_products"]
+ENGINES = ["auto", "valu", "mfma_products"]
 
 
 @pytest.fixture(params=ENGINES)
 def engine(request, ctx):
-    """Runs a MatMul test once per main-kernel engine of the F32 MatMul (F64 always uses
-    the vector unit); every engine must give the oracle's bits."""
+    """Runs a MatMul test once per engine; every engine must give the oracle's bits and
+    first fault. "auto" runs outputs of at most 256 x 256 cells (F32) or 512 x 512 (F64) as
+    one fused launch; "valu" and "mfma_products" always take the screened tile kernels
+    (F64 uses the vector unit under both)."""
     ctx.set_matmul_engine(request.param)
     yield request.param
     ctx.set_matmul_engine("auto")
