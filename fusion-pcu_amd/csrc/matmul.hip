@@ -23,6 +23,9 @@
 //                 flagged have their K products classified in parallel by a wave. Both stop
 //                 once the earliest fault found lies before the cells still to visit. The
 //                 fault-free path returns at once.
+// Small outputs (engine auto) take one fused launch instead, k_strict_gemm_fused: each
+// 16 x 16 block screens its own rows and columns, computes its cells and searches its
+// suspect cells exactly.
 #include "pcu_device.hpp"
 #include "pcu_gemm_stage.hpp"
 #include "pcu_kernels.hpp"
