@@ -382,7 +382,9 @@ def engine(request, ctx):
                                    (128, 16, 128), (256, 32, 384), (256, 48, 130), (130, 64, 256),
                                    # whole, with 3, 4 and 6 slabs (every trip count of the
                                    # three-stage slab loop)
-                                   (128, 48, 128), (256, 64, 128), (128, 96, 256)])
+                                   (128, 48, 128), (256, 64, 128), (128, 96, 256),
+                                   # whole 64 x 64 tiles of 16 x 16 waves: 1, 5 and 17 slabs
+                                   (64, 16, 64), (192, 80, 320), (448, 272, 512)])
 def test_matmul_parity_all_transposes(ctx, pcu_pkg, dtype, shape, engine):
     m, k, n = shape
     rng = np.random.default_rng(m * 7 + k * 3 + n)
