@@ -430,7 +430,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             if (bad)
                 key = cell < key ? cell : key;
         }
-        wave_record_fault(key, suspect);
+        block_record_min<Cfg::kThreads / 64>(key, suspect);
         return;
     } else if constexpr (kStages == 3) {
         const int c = n0 + wn + 2 * col;
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             else if (bad1)
                 key = cell + 1 < key ? cell + 1 : key;
         }
-        wave_record_fault(key, suspect);
+        block_record_min<Cfg::kThreads / 64>(key, suspect);
         return;
     }
 #pragma unroll
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             }
         }
     }
-    wave_record_fault(key, suspect);
+    block_record_min<Cfg::kThreads / 64>(key, suspect);
 }
 
 // ------------------------------------------------------- 16 x 16 waves, whole tiles
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
         if (bad)
             key = cell < key ? cell : key;
     }
-    wave_record_fault(key, suspect);
+    block_record_min<16>(key, suspect);
 }
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
