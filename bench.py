@@ -174,7 +174,7 @@ def bench_c3(pkg, ctx, steps):
             "work": "strict F64 MatMul 4096^3 + checked bias add + ReLU, one prepared program"}
 
 
-def bench_c1(pkg, ctx, steps=10):
+def bench_c1(pkg, ctx, steps=100):
     """C1: the strict F32 single-layer training step (X 64x128, W 128x64, b 64x64, Y 64x64,
     seeds 1..4, lr 0.01) with W and b resident and fed back: microseconds per step."""
     from fusion_pcu_amd import graph as G
@@ -184,7 +184,7 @@ def bench_c1(pkg, ctx, steps=10):
     b = G.PcuTensor(ctx.upload(syn.uniform(3, (64, 64), np.float32)))
     y = G.PcuTensor(ctx.upload(syn.uniform(4, (64, 64), np.float32)))
     step = G.c1_training_step(0.01)
-    for _ in range(5):
+    for _ in range(20):
         w, b, loss = step(x, w, b, y)
     ctx.synchronize()
     t0 = time.perf_counter()
