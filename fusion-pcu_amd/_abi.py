@@ -155,7 +155,7 @@ GRAPH_OPS = ["Input", "Uniform", "Add", "Sub", "Mul", "Div", "SgdUpdate", "MatMu
 KERNEL_IDS = {
     "strict_gemm": 0, "gemm_prefilter": 1, "gemm_replay": 2, "sgd": 3, "binary": 4,
     "relu": 5, "relu_backward": 6, "add_relu": 7, "mse": 8,
-    "native_gemm": 9, "native_sgd": 10, "native_mse": 11,
+    "native_gemm": 9, "native_sgd": 10, "native_mse": 11, "elementwise_chain": 12,
 }
 
 _lib = None

@@ -291,6 +291,142 @@ __global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a
     wave_record_fault(key_relu, fault_relu, NodeGate{gate.word, gate.node + 1});
 }
 
+// ---------------------------------------------------------- fused chains
+// Consecutive elementwise nodes of a prepared program, each an operand of the next, in one
+// pass over the elements: the values between steps stay in registers, and only the values
+// another node reads are stored. Each step's faults go to its own node's word and every
+// step is classified as its own kernel classifies it, so the node-major first fault is the
+// one the nodes give one after another (a step may also record a fault on a value a
+// faulting earlier step produced: the earlier node's fault is the one reported).
+template <typename T> __device__ __forceinline__ T chain_uniform(uint64_t bits)
+{
+    if constexpr (sizeof(T) == 4)
+        return __builtin_bit_cast(float, (uint32_t)bits);
+    else
+        return __builtin_bit_cast(double, bits);
+}
+
+template <typename T> __device__ __forceinline__ T chain_binary(int op, T a, T b)
+{
+    switch (op) {
+    case kOpAdd: return a + b;
+    case kOpSub: return a - b;
+    case kOpMul: return a * b;
+    default: return a / b;
+    }
+}
+
+template <typename T> __device__ __forceinline__ bool chain_suspect(int op, T a, T b, T r, int policy)
+{
+    if (op == kOpAdd || op == kOpSub) return add_suspect(a, b, r, policy);
+    if (op == kOpMul) return mul_suspect(a, b, r, policy);
+    return div_suspect(a, b, r, policy);
+}
+
+template <typename T> __device__ __forceinline__ uint32_t chain_classify(int op, T a, T b, T r, int policy)
+{
+    if (op == kOpAdd || op == kOpSub) return classify_add(a, b, r, policy);
+    if (op == kOpMul) return classify_mul(a, b, r, policy);
+    return classify_div(a, b, r, policy);
+}
+
+// Step S of a chain on the lanes [base, base + W): v holds the value the step takes and is
+// replaced by the step's result; key keeps the step's first fault in this thread.
+template <typename T, bool VEC, int S>
+__device__ __forceinline__ void chain_step(const ChainLaunch &c, uint64_t base, uint64_t n,
+                                           T (&v)[Lanes<T, VEC>::W], uint64_t &key)
+{
+    constexpr int W = Lanes<T, VEC>::W;
+    const ChainStep &st = c.step[S];
+    const int op = st.op, policy = st.policy;
+    const bool right = st.chain_right != 0;
+    T o[W], r[W];
+    if (op != kStepRelu) {
+        if (st.other) {
+            load_lanes<T, VEC>((const T *)st.other, base, n, o);
+        } else {
+            const T u = chain_uniform<T>(st.other_bits);
+#pragma unroll
+            for (int j = 0; j < W; j++)
+                o[j] = u;
+        }
+    }
+    bool any = false;
+    if (op == kStepRelu) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            r[j] = relu_select(v[j]);
+            any |= base + j < n && (!finite_bits(v[j]) || (policy == kPolicyRejectSubnormal && subnormal(r[j])));
+        }
+    } else if (op == kStepReluBackward) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T x = right ? o[j] : v[j], u = right ? v[j] : o[j];
+            r[j] = strictly_positive(x) ? u : (T)0;
+            any |= base + j < n && (!finite_bits(x) || !finite_bits(u) ||
+                                    (policy == kPolicyRejectSubnormal && subnormal(r[j])));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T a = right ? o[j] : v[j], b = right ? v[j] : o[j];
+            r[j] = chain_binary(op, a, b);
+            any |= base + j < n && chain_suspect(op, a, b, r[j], policy);
+        }
+    }
+    if (st.out)
+        store_lanes<T, VEC>((T *)st.out, base, n, r);
+    if (any && key == kNoFault) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            if (base + j >= n || key != kNoFault)
+                continue;
+            uint32_t kind;
+            if (op == kStepRelu) {
+                kind = classify_relu(v[j], r[j], policy);
+            } else {
+                const T a = right ? o[j] : v[j], b = right ? v[j] : o[j];
+                kind = op == kStepReluBackward ? classify_relu_backward(a, b, r[j], policy)
+                                               : chain_classify(op, a, b, r[j], policy);
+            }
+            if (kind != kOk)
+                key = pack_fault(base + j, kind);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < W; j++)
+        v[j] = r[j];
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n, NodeGate gate)
+{
+    static_assert(kChainMaxSteps == 4, "one chain_step call per step below");
+    if (wave_gate_closed(gate))
+        return;
+    constexpr int W = Lanes<T, VEC>::W;
+    uint64_t k0 = kNoFault, k1 = kNoFault, k2 = kNoFault, k3 = kNoFault;
+    PCU_EW_LOOP(W)
+    {
+        T v[W];
+        load_lanes<T, VEC>((const T *)c.head, base, n, v);
+        chain_step<T, VEC, 0>(c, base, n, v, k0);
+        if (c.steps > 1)
+            chain_step<T, VEC, 1>(c, base, n, v, k1);
+        if (c.steps > 2)
+            chain_step<T, VEC, 2>(c, base, n, v, k2);
+        if (c.steps > 3)
+            chain_step<T, VEC, 3>(c, base, n, v, k3);
+    }
+    wave_record_fault(k0, c.step[0].fault, gate);
+    if (c.steps > 1)
+        wave_record_fault(k1, c.step[1].fault, NodeGate{gate.word, gate.node + 1});
+    if (c.steps > 2)
+        wave_record_fault(k2, c.step[2].fault, NodeGate{gate.word, gate.node + 2});
+    if (c.steps > 3)
+        wave_record_fault(k3, c.step[3].fault, NodeGate{gate.word, gate.node + 3});
+}
+
 // -------------------------------------------------------------------- SGD
 // core/dialect/tensor/reference/strict_sgd/strict_sgd.rs:20-46: p = rate (x) g, then
 // w' = w (-) p; ordinal 2i (Multiply) and 2i+1 (Subtract).
@@ -1568,6 +1704,28 @@ static hipError_t relu_t(hipStream_t s, uint64_t n, const void *x, void *out, in
     else
         hipLaunchKernelGGL((k_relu<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)x, (T *)out, n, policy, fault, gate);
     return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t chain_t(hipStream_t s, uint64_t n, const ChainLaunch &c, NodeGate gate)
+{
+    constexpr int Wd = Vec<T>::width;
+    bool vec = aligned16(c.head);
+    for (int i = 0; i < c.steps; i++)
+        vec = vec && aligned16(c.step[i].other) && aligned16(c.step[i].out);
+    const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
+    if (vec)
+        hipLaunchKernelGGL((k_chain<T, true>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+    else
+        hipLaunchKernelGGL((k_chain<T, false>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+    return hipGetLastError();
+}
+
+hipError_t launch_chain(hipStream_t s, int dtype, uint64_t n, const ChainLaunch &c, NodeGate gate)
+{
+    if (n == 0 || c.steps <= 0)
+        return hipSuccess;
+    return dtype == 0 ? chain_t<float>(s, n, c, gate) : chain_t<double>(s, n, c, gate);
 }
 
 hipError_t launch_relu(hipStream_t s, int dtype, uint64_t n, const void *x, void *out,

@@ -729,6 +729,73 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
                 fused_into[a] = (int)i;
         }
     }
+    // Chains: consecutive launching elementwise nodes (checked binary, ReLU, ReLU backward)
+    // of one dtype and shape, each an operand of the next, run as one kernel with one fault
+    // word per node (launch order and fault order unchanged; the values between them stay
+    // in registers). A later step may not read an earlier step's stored value as its other
+    // operand, so every value a step reads was written before the launch.
+    chain_next.assign(n, UINT32_MAX);
+    chain_len.assign(n, 0);
+    chain_member.assign(n, 0);
+    chain_store.assign(n, 1);
+    {
+        auto launches = [&](uint32_t i) {
+            const Op op = graph.nodes[i].op;
+            return op != Op::Input && op != Op::Constant && op != Op::Uniform && fused_into[i] < 0;
+        };
+        auto chainable = [&](uint32_t i) {
+            const Node &nd = graph.nodes[i];
+            const bool elementwise = nd.op == Op::Add || nd.op == Op::Sub || nd.op == Op::Mul ||
+                                     nd.op == Op::Div || nd.op == Op::Relu || nd.op == Op::ReluBackward;
+            // A ReLU that has absorbed its Add already runs as one kernel.
+            return elementwise && !(nd.op == Op::Relu && fused_into[nd.a] == (int)i);
+        };
+        auto binary = [&](uint32_t i) {
+            const Op op = graph.nodes[i].op;
+            return op == Op::Add || op == Op::Sub || op == Op::Mul || op == Op::Div;
+        };
+        std::vector<uint32_t> run;
+        for (uint32_t i : order)
+            if (launches(i))
+                run.push_back(i);
+        for (size_t k = 0; k < run.size();) {
+            const uint32_t h = run[k];
+            const Node &hn = graph.nodes[h];
+            // The head's chain operand must be dense: a binary node takes its dense side.
+            bool ok = chainable(h) && !(binary(h) && graph.nodes[hn.a].op == Op::Uniform &&
+                                        graph.nodes[hn.b].op == Op::Uniform);
+            std::vector<uint32_t> members{h};
+            while (ok && k + members.size() < run.size() && (int)members.size() < kChainMaxSteps) {
+                const uint32_t x = members.back(), y = run[k + members.size()];
+                const Node &yn = graph.nodes[y];
+                if (!chainable(y) || yn.dtype != hn.dtype || graph.nodes[y].shape != hn.shape)
+                    break;
+                if (yn.op == Op::Relu) {
+                    if (yn.a != x)
+                        break;
+                } else {
+                    if ((yn.a == x) == (yn.b == x))
+                        break; // x is not an operand, or is both
+                    const uint32_t other = yn.a == x ? yn.b : yn.a;
+                    if (std::find(members.begin(), members.end(), other) != members.end())
+                        break;
+                }
+                members.push_back(y);
+            }
+            if (members.size() > 1) {
+                chain_len[h] = (int)members.size();
+                for (size_t j = 0; j < members.size(); j++) {
+                    const uint32_t m = members[j];
+                    if (j + 1 < members.size())
+                        chain_next[m] = members[j + 1];
+                    if (j > 0)
+                        chain_member[m] = 1;
+                    chain_store[m] = j + 1 == members.size() || is_output[m] || uses[m] > 1;
+                }
+            }
+            k += members.size();
+        }
+    }
     // The ordered MSE sum runs on the side stream when nothing in the plan consumes its
     // value (the training-loss case): it then overlaps the backward pass.
     for (uint32_t i : order)
@@ -748,7 +815,7 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
                 return st;
             continue;
         }
-        if (nd.op == Op::Input || nd.op == Op::Uniform || fused_into[i] >= 0)
+        if (nd.op == Op::Input || nd.op == Op::Uniform || fused_into[i] >= 0 || !chain_store[i])
             continue;
         size_t bytes = graph.elements(i) * dsize(nd.dtype);
         for (int b = 0; b < (is_output[i] ? 2 : 1); b++)
@@ -773,6 +840,48 @@ void *Prepared::value_ptr(uint32_t id, const std::vector<const void *> &in, int 
     if (nd.op == Op::Constant)
         return constant_buf[id];
     return buf[is_output[id] ? bank : 0][id];
+}
+
+ChainLaunch Prepared::chain_launch(uint32_t head, const std::vector<const void *> &in, int bank_w) const
+{
+    ChainLaunch c;
+    // A Uniform operand that was not materialized goes in as its bits.
+    auto dense = [&](uint32_t id) {
+        return graph.nodes[id].op != Op::Uniform || dense_uniform[id] != nullptr;
+    };
+    auto set_other = [&](ChainStep &st, uint32_t id, int dtype) {
+        if (dense(id)) {
+            st.other = value_ptr(id, in, bank_w);
+        } else {
+            const uint64_t bits = graph.nodes[id].value_bits;
+            st.other_bits = dtype == 0 ? (uint32_t)bits : bits;
+        }
+    };
+    uint32_t prev = UINT32_MAX;
+    for (uint32_t m = head; m != UINT32_MAX; m = chain_next[m]) {
+        const Node &nd = graph.nodes[m];
+        ChainStep &st = c.step[c.steps++];
+        st.policy = nd.policy < 0 ? 0 : nd.policy;
+        st.out = chain_store[m] ? value_ptr(m, in, bank_w) : nullptr;
+        st.op = nd.op == Op::Add ? kOpAdd : nd.op == Op::Sub ? kOpSub : nd.op == Op::Mul ? kOpMul
+              : nd.op == Op::Div ? kOpDiv : nd.op == Op::Relu ? kStepRelu : kStepReluBackward;
+        if (nd.op == Op::Relu) {
+            if (prev == UINT32_MAX)
+                c.head = value_ptr(nd.a, in, bank_w);
+        } else if (prev == UINT32_MAX) {
+            // The head reads its dense left operand, or its right one when the left is an
+            // unmaterialized Uniform.
+            const bool left = dense(nd.a);
+            c.head = value_ptr(left ? nd.a : nd.b, in, bank_w);
+            st.chain_right = left ? 0 : 1;
+            set_other(st, left ? nd.b : nd.a, nd.dtype);
+        } else {
+            st.chain_right = nd.b == prev ? 1 : 0;
+            set_other(st, nd.b == prev ? nd.a : nd.b, nd.dtype);
+        }
+        prev = m;
+    }
+    return c;
 }
 
 pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fault)
@@ -817,10 +926,23 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     auto ptr = [&](uint32_t id) { return value_ptr(id, in, bank_w); };
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
-        if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0)
+        if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0 ||
+            chain_member[i])
             continue;
         uint64_t n = graph.elements(i);
         int policy = nd.policy < 0 ? 0 : nd.policy;
+        if (chain_len[i] > 1) {
+            st = ctx->op_chain(nd.dtype, n, chain_launch(i, in, bank_w));
+            for (uint32_t m = i; m != UINT32_MAX; m = chain_next[m])
+                prog_to_graph.push_back(m);
+            if (st) {
+                pcu_fault ignore;
+                (void)ctx->end_program(&ignore);
+                error = ctx->error;
+                return st;
+            }
+            continue;
+        }
         switch (nd.op) {
         case Op::Add:
         case Op::Sub:

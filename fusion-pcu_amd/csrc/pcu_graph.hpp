@@ -93,6 +93,13 @@ struct Prepared {
     std::vector<int> is_output;     // per node
     std::vector<int> fused_into;    // Add fused into the ReLU at this id (or -1)
     std::vector<int> mse_side;      // MSE runs on the side stream
+    // Fused elementwise chains: chain_next links a chain's nodes in order (UINT32_MAX at its
+    // end); chain_len is the step count at its head, 0 elsewhere; chain_member marks the
+    // nodes after the head (launched with it); chain_store marks the nodes whose value is
+    // stored (the last step, outputs and values other nodes read).
+    std::vector<uint32_t> chain_next;
+    std::vector<int> chain_len;
+    std::vector<char> chain_member, chain_store;
     std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
     std::vector<void *> constant_buf; // resident copy of each planned Constant, uploaded at build
@@ -105,6 +112,8 @@ struct Prepared {
     pcu_status build(Ctx *c, const Graph &g, const std::vector<uint32_t> &outs);
     pcu_status execute(const std::vector<const void *> &device_inputs, pcu_fault *fault);
     void *value_ptr(uint32_t id, const std::vector<const void *> &in, int bank) const;
+    // The launch of the chain that starts at `head`.
+    ChainLaunch chain_launch(uint32_t head, const std::vector<const void *> &in, int bank_w) const;
 };
 
 } // namespace pcu

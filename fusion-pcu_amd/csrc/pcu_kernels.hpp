@@ -31,6 +31,28 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                            unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
                       double rate, void *out, int policy, unsigned long long *fault, NodeGate gate);
+
+// A chain of elementwise nodes (checked binary, ReLU, ReLU backward) evaluated in one pass:
+// each step takes the value of the step before it (the first takes `head`) and, for a binary
+// op or ReLU backward, one more operand. Every step has its own policy and fault word, and
+// step s is program node gate.node + s.
+enum : int { kStepRelu = 4, kStepReluBackward = 5 };
+constexpr int kChainMaxSteps = 4;
+struct ChainStep {
+    int op;              // kOpAdd..kOpDiv, kStepRelu or kStepReluBackward
+    int chain_right;     // the chain's value is the right operand (ReLU backward: the upstream)
+    int policy;
+    const void *other;   // the other operand, or nullptr for the uniform `other_bits`
+    uint64_t other_bits; // the uniform operand's bits (dtype-sized)
+    void *out;           // the step's value is stored here, or nullptr (read by the next step only)
+    unsigned long long *fault;
+};
+struct ChainLaunch {
+    int steps = 0;
+    const void *head = nullptr;
+    ChainStep step[kChainMaxSteps] = {};
+};
+hipError_t launch_chain(hipStream_t s, int dtype, uint64_t n, const ChainLaunch &c, NodeGate gate);
 // Strict MSE in two launches on one scratch of mse_scratch_bytes(dtype, n) bytes: the
 // parallel part (squares, chunk estimates and summaries), then the one-workgroup ordered
 // walk and the division, which may run on another stream once the first is done. `count`

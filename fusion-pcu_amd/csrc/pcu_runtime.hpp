@@ -143,6 +143,9 @@ struct Ctx {
                                 int policy);
     pcu_status op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
                            const void *b_value, void *out, int policy);
+    // Consecutive elementwise nodes as one launch: one program node per step, in order
+    // (each step's fault word is filled in here).
+    pcu_status op_chain(int dtype, uint64_t n, ChainLaunch chain);
     pcu_status op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate, void *out,
                       int policy);
     pcu_status op_mse(int dtype, uint64_t n, const void *p, const void *t, void *out, int policy,

@@ -779,6 +779,51 @@ pcu_status Ctx::op_relu(int dtype, uint64_t n, const void *x, void *out, int pol
     return st;
 }
 
+pcu_status Ctx::op_chain(int dtype, uint64_t n, ChainLaunch c)
+{
+    if (!valid_dtype(dtype) || c.steps < 1 || c.steps > kChainMaxSteps || (n && !c.head)) {
+        fail("elementwise chain: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    const uint64_t bytes = n * dsize(dtype);
+    for (int i = 0; i < c.steps; i++) {
+        const ChainStep &st = c.step[i];
+        if (!valid_policy(st.policy) || st.op < kOpAdd || st.op > kStepReluBackward ||
+            (i == c.steps - 1 && n && !st.out)) {
+            fail("elementwise chain: invalid step %d", i);
+            return PCU_ERR_ARGUMENT;
+        }
+        // A stored value may alias an operand exactly (each element is read before it is
+        // written, by the same thread) but not in part.
+        for (int j = 0; j < c.steps; j++)
+            if (partial_overlap(st.out, c.step[j].other, bytes)) {
+                fail("elementwise chain: a step's output partly overlaps an operand");
+                return PCU_ERR_ARGUMENT;
+            }
+        if (partial_overlap(st.out, c.head, bytes)) {
+            fail("elementwise chain: a step's output partly overlaps an operand");
+            return PCU_ERR_ARGUMENT;
+        }
+    }
+    unsigned long long *first = nullptr;
+    for (int i = 0; i < c.steps; i++) {
+        unsigned long long *word;
+        pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
+        if (st)
+            return st;
+        c.step[i].fault = word;
+        if (!first)
+            first = word;
+    }
+    pcu_status st = open_words();
+    if (st)
+        return st;
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_chain(stream, dtype, n, c, gate_for(first)), "elementwise chain launch");
+    timer_stop(PCU_KERNEL_ELEMENTWISE_CHAIN, t, stream);
+    return st;
+}
+
 pcu_status Ctx::op_relu_backward(int dtype, uint64_t n, const void *x, const void *up, void *out,
                                  int policy)
 {

@@ -271,7 +271,8 @@ typedef enum pcu_kernel_id {
     PCU_KERNEL_NATIVE_GEMM = 9,     /* native (BackendDefined) MatMul */
     PCU_KERNEL_NATIVE_SGD = 10,
     PCU_KERNEL_NATIVE_MSE = 11,
-    PCU_KERNEL_COUNT = 12
+    PCU_KERNEL_ELEMENTWISE_CHAIN = 12, /* a prepared program's fused elementwise nodes */
+    PCU_KERNEL_COUNT = 13
 } pcu_kernel_id;
 pcu_status pcu_profile_enable(pcu_ctx *ctx, int on);
 pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t *launches);
@@ -391,8 +392,10 @@ pcu_status pcu_graph_plan(const pcu_graph *graph, uint32_t n_outputs, const uint
  *                                                    -> the native kernels above;
  *  anything else                                     -> PCU_ERR_UNSUPPORTED (the reference
  *    rejects checked result-boundary MatMul: backends/rocm/tensor.rs:9053-9058).
- * Prepare once (plan, fusion of single-use Add->ReLU, device storage with two banks per
- * output), execute many times. Inputs are device pointers in the order of the graph's Input
+ * Prepare once (plan; fusion of a single-use Add->ReLU, and of runs of up to four
+ * consecutive elementwise nodes of one shape, each an operand of the next, into one kernel
+ * that keeps one fault word per node; device storage with two banks per output), execute
+ * many times. Inputs are device pointers in the order of the graph's Input
  * nodes that the plan uses (pcu_prepared_input_id). An execution that faults publishes
  * nothing and returns the first fault with `node` = its graph node id; the previous
  * outputs stay published, so a resident weight fed back as an input is never lost. */
