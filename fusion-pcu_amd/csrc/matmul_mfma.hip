@@ -17,10 +17,12 @@
 //    both terms are), and x + (+0) = x + (-0) for every x != -0.
 // The two blocks of one MFMA carry k and k+1 for the same 32x32 output tile, so one
 // instruction yields 2048 products and a lane adds its 16 cells' k-product, then their
-// (k+1)-product.
+// (k+1)-product. Small grids of whole 64x64 tiles use v_mfma_f32_16x16x1_4b_f32 the same
+// way (k_strict_gemm_mfma16): its four blocks carry k..k+3 for one 16x16 output tile.
 //
 // Fault screening (non-finite result, exponent prefilter) and the exact replay of suspect
-// cells are shared with the VALU kernel.
+// cells are shared with the VALU kernel; these kernels record a workgroup's first suspect
+// cell with one atomic.
 #include "pcu_device.hpp"
 #include "pcu_gemm_stage.hpp"
 #include "pcu_kernels.hpp"
