@@ -136,7 +136,11 @@ __device__ __forceinline__ void exp_rows_block(const ExpJob<T> &j, uint64_t bid,
 // Columns job, block `bid` = (column block cb, 64-row group rg): 64 column-runs (16 bytes
 // each) by 4 row groups of 16 rows; the row groups meet in LDS and the block folds its
 // minimum into out with one atomicMax per column. Fewer rows per block measured slower: the
-// atomics on one column then contend.
+// atomics on one column then contend. More measured slower too (128 or 256 rows: 4096^3 NN
+// 28.1 -> 29.6 / 28.7 us, K = 1024 12.5 -> 14.0 / 18.7 us, binary64 48.0 -> 51.1 / 49.8 us),
+// except when both jobs are column jobs (op(A) transposed: 34.7 -> 30.3 us).
+constexpr uint64_t kColRows = 64; // rows of a columns-job block
+
 template <typename T, bool VEC>
 __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen,
                                                int (*part)[64 * 16 / sizeof(T)])
@@ -146,8 +150,8 @@ __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid,
     const uint64_t cb = bid % ncb, rg = bid / ncb;
     const int cx = threadIdx.x % 64, ry = threadIdx.x / 64;
     const uint64_t c0 = (cb * 64 + cx) * P;
-    const uint64_t r0 = rg * 64;
-    const uint64_t r1 = r0 + 64 < R ? r0 + 64 : R;
+    const uint64_t r0 = rg * kColRows;
+    const uint64_t r1 = r0 + kColRows < R ? r0 + kColRows : R;
     const T *X = j.X;
     int m[P];
 #pragma unroll
@@ -209,7 +213,7 @@ template <typename T> __host__ __device__ inline uint64_t exp_blocks(const ExpJo
     if (j.rows)
         return (j.R + 3) / 4;
     const uint64_t P = j.vec ? 16 / sizeof(T) : 1;
-    return ((j.C + 64 * P - 1) / (64 * P)) * ((j.R + 63) / 64);
+    return ((j.C + 64 * P - 1) / (64 * P)) * ((j.R + kColRows - 1) / kColRows);
 }
 
 // Both jobs of a MatMul in one launch: blocks [0, na) run job a, the rest job b. A block's
