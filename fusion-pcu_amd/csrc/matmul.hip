@@ -759,10 +759,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
     int thr, const unsigned long long *suspect, unsigned long long *row_flag,
     unsigned long long *flag_first, uint32_t gen, NodeGate gate)
 {
+    // No cell marked: nothing to scan (the same word for every thread). Most launches end
+    // here, before the gate's block-wide read and its barrier.
+    if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault)
+        return;
     if (block_gate_closed(gate))
         return;
-    if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault)
-        return; // no cell marked: nothing to scan (the same word for every thread)
     using Cfg = ScanCfg<T>;
     constexpr int BK = Cfg::BK, EA = Cfg::EA, EB = Cfg::EB;
     // k-major exponent stages; rows padded by 8 exponents (16 bytes) so the scattered
@@ -1035,11 +1037,13 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
     int policy, const unsigned long long *suspect, const unsigned long long *row_flag,
     const unsigned long long *flag_first, uint32_t gen, unsigned long long *fault, NodeGate gate)
 {
-    if (block_gate_closed(gate))
-        return; // an earlier node faulted: that fault is the one reported
+    // No suspect cell: nothing to replay, whatever the gate says. Most launches end here,
+    // before the gate's block-wide read and its barrier.
     const uint64_t first = *suspect;
     if (first == kNoFault || K == 0)
         return;
+    if (block_gate_closed(gate))
+        return; // an earlier node faulted: that fault is the one reported
     const uint64_t cells = M * N;
     // The cell of a packed MatMul fault: ordinal = 2 (cell K + k) + step.
     auto cell_of = [&](uint64_t w) { return ((w >> 3) / 2) / K; };
