@@ -2,9 +2,10 @@
 // operand), ReLU, ReLU-backward, fused Add->ReLU, strict SGD and strict MSE.
 //
 // Layout: dense row-major tensors in HBM. One thread moves one 16-byte vector per operand
-// (4 floats or 2 doubles) and the grid covers the whole tensor in 128-thread blocks, with
-// non-temporal loads and stores: on MI355X this streams at about 85% of the 8 TB/s HBM
-// peak, ahead of every grid-stride shape tried. The last vector may be partial (scalar
+// (4 floats or 2 doubles) and the grid covers the whole tensor in 256-thread blocks, with
+// non-temporal loads and stores: on MI355X this streams at about 83% of the 8 TB/s HBM
+// peak, ahead of every grid-stride shape tried (2^28 f32 SGD: 6.55-6.64 TB/s, against
+// 6.32-6.52 with 128-thread blocks and 6.43 / 6.34 with 512 / 1024). The last vector may be partial (scalar
 // accesses for its in-range elements). Faults are screened per lane, resolved exactly
 // only on flagged lanes, and reduced with one ballot per wave and one atomicMin per
 // faulting wave into the op's 64-bit fault word.
@@ -17,7 +18,7 @@
 
 namespace pcu {
 
-constexpr int kEwThreads = 128;
+constexpr int kEwThreads = 256;
 
 template <typename T> struct Vec;
 template <> struct Vec<float> {
