@@ -1319,6 +1319,61 @@ hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t 
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// A stored R x C float matrix copied into C x R (R and C multiples of 4, both pointers
+// 16-byte aligned): 64 x 64 tiles through LDS, 16-byte loads and stores, rows of the tile
+// padded by one float so that both phases meet at most two lanes a bank. Used for a
+// transposed op(B) of the matrix-core engine: the copy holds the same values, so every
+// product, sum and fault of the MatMul is unchanged.
+__global__ __launch_bounds__(256) void k_transpose_f32(const float *__restrict__ X,
+                                                      float *__restrict__ Y, int R, int C,
+                                                      NodeGate gate)
+{
+    if (block_gate_closed(gate))
+        return;
+    __shared__ float t[64][65];
+    const int tiles_c = (C + 63) / 64;
+    const int r0 = (int)(blockIdx.x / tiles_c) * 64, c0 = (int)(blockIdx.x % tiles_c) * 64;
+    const int q = threadIdx.x & 15, row = threadIdx.x >> 4; // 16 runs of 4 floats x 16 rows
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int i = row + 16 * p, r = r0 + i, c = c0 + 4 * q;
+        if (r < R && c < C) {
+            const float4 v = *reinterpret_cast<const float4 *>(X + (size_t)r * C + c);
+            t[i][4 * q] = v.x;
+            t[i][4 * q + 1] = v.y;
+            t[i][4 * q + 2] = v.z;
+            t[i][4 * q + 3] = v.w;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int j = row + 16 * p, c = c0 + j, r = r0 + 4 * q;
+        if (c < C && r < R)
+            *reinterpret_cast<float4 *>(Y + (size_t)c * R + r) =
+                make_float4(t[4 * q][j], t[4 * q + 1][j], t[4 * q + 2][j], t[4 * q + 3][j]);
+    }
+}
+
+// Largest op(B) copied out for the matrix-core engine (1 GiB of floats); larger ones are
+// read in place.
+constexpr uint64_t kBtMaxElems = 1ull << 28;
+
+bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tr,
+                      int engine)
+{
+    if (dtype != 0 || !tr || engine == kEngineValu || inner == 0 || inner % 16 != 0)
+        return false;
+    if (engine == kEngineAuto && rows * cols <= fused_cells<float>())
+        return false; // the fused small-output launch reads B in place
+    // Whole 128 x 128 tiles filling at least one workgroup a CU: the copy measured 2-2.5%
+    // faster there (NT 4096^3 1973 against 2021 us, 4096 x 1024 x 4096 510 against 521, TT
+    // 4096^3 -2%), and 4.5-7% slower on the 64 x 64 tiles of smaller grids (1024^3 NT 57.1
+    // against 54.6 us).
+    return rows % 128 == 0 && cols % 128 == 0 && (rows / 128) * (cols / 128) >= 256 &&
+           inner * cols <= kBtMaxElems;
+}
+
 // The exponent screen of op(A) rows and op(B) columns, both jobs in one launch.
 template <typename T>
 static void prefilter(hipStream_t s, ExpJob<T> ja, ExpJob<T> jb, uint32_t gen,
@@ -1439,8 +1494,19 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (ev)
         (void)hipEventRecord(ev[1], s);
     if (f32 && engine != kEngineValu) {
-        (void)launch_gemm_mfma_f32(s, m, n, k, ta, tb, (const float *)A, (const float *)B,
-                                   (float *)C, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        // A transposed op(B) (stored N x K) goes to the tile kernel as its K x N copy, which
+        // it loads straight into LDS; the screen, tiny scan and replay read B in place.
+        const float *Bt = (const float *)B;
+        bool tbt = tb;
+        if (tb && sc.bt && aligned16(B)) {
+            const unsigned tiles = (unsigned)(((N + 63) / 64) * ((K + 63) / 64));
+            hipLaunchKernelGGL(k_transpose_f32, dim3(tiles), dim3(256), 0, s, (const float *)B,
+                               sc.bt, n, k, gate);
+            Bt = sc.bt;
+            tbt = false;
+        }
+        (void)launch_gemm_mfma_f32(s, m, n, k, ta, tbt, (const float *)A, Bt, (float *)C,
+                                   sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
     } else if (!f32 && (uint64_t)grid.x < 256) {
         const double *dA = (const double *)A, *dB = (const double *)B;
         double *dC = (double *)C;

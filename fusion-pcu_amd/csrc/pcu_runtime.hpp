@@ -96,7 +96,7 @@ struct Ctx {
         void *p = nullptr;
         size_t cap = 0;
     };
-    Scratch matmul_scratch, mse_scratch;
+    Scratch matmul_scratch, mse_scratch, bt_scratch;
     uint32_t screen_gen = 0; // generation of the latest MatMul exponent screen
     // Buffers released by the caller are kept for reuse by an allocation of the same size
     // (a training step frees its previous weights and takes as many new ones of the same
