@@ -46,6 +46,10 @@ CASES = [  # (rows, inner, cols, transposes, dtype, policy, planted special or N
     (512, 128, 384, (False, False), np.float32, 0, ("a", 7777, np.nan)),
     (200, 90, 100, (False, False), np.float32, 0, ("b", 4321, 1e-30)),
     (96, 40, 33, (True, False), np.float64, 0, ("a", 99, np.inf)),
+    # Full F32 grids with op(B) transposed: the allocating entry point copies op(B) out as
+    # K x N for its tile kernel, the no-allocation one reads B in place.
+    (2048, 48, 2048, (False, True), np.float32, 0, ("b", 50000, np.inf)),
+    (2048, 64, 2048, (True, True), np.float32, 1, None),
 ]
 
 
