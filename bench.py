@@ -49,32 +49,36 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _abi_matmul(ctx, da, db, dc, m, k, n, policy=0):
-    """One strict MatMul call straight through the C ABI; returns its status (a fault
-    variant returns PCU_ARITHMETIC_FAULT without a Python exception in the timed loop)."""
+def _abi_matmul_call(ctx, da, db, dc, m, k, n, policy=0):
+    """A zero-argument callable making one complete strict MatMul call straight through the
+    C ABI (launches and fault readback); it returns the call's status, so a fault variant
+    returns PCU_ARITHMETIC_FAULT without a Python exception in the timed loop. The argument
+    list and the fault record are built once, so the loop times the call itself."""
     import ctypes
     from fusion_pcu_amd import _abi
     f = _abi.Fault()
     code = _abi.PCU_F32 if da.dtype == np.float32 else _abi.PCU_F64
-    return ctx._lib.pcu_strict_matmul(ctx.handle, code, m, k, n, 0, 0, da.ptr, db.ptr, dc.ptr,
-                                      policy, ctypes.byref(f))
+    fn = ctx._lib.pcu_strict_matmul
+    args = (ctx.handle, code, m, k, n, 0, 0, da.ptr, db.ptr, dc.ptr, policy, ctypes.byref(f))
+    return lambda: fn(*args)
 
 
 def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0):
     """ms per complete call, timed with per-kernel timing off, then the kernel breakdown
     (prefilter, main tile kernel, replay including the tiny scan) from a second timed
     pass of the same number of calls."""
+    call = _abi_matmul_call(ctx, da, db, dc, m, k, n)
     for _ in range(warmup):
-        assert _abi_matmul(ctx, da, db, dc, m, k, n) == expect
+        assert call() == expect
     ctx.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        _abi_matmul(ctx, da, db, dc, m, k, n)
+        call()
     ctx.synchronize()
     t1 = time.perf_counter()
     ctx.profile(True)
     for _ in range(steps):
-        _abi_matmul(ctx, da, db, dc, m, k, n)
+        call()
     ctx.synchronize()
     gemm_ms, gemm_n = ctx.kernel_time("strict_gemm")
     pre_ms, _ = ctx.kernel_time("gemm_prefilter")
@@ -207,11 +211,12 @@ def bench_small_calls(pkg, ctx, reps=200):
         da = ctx.upload(syn.uniform(5, (64, 256), dtype))
         db = ctx.upload(syn.uniform(6, (256, 64), dtype))
         dc = ctx.empty((64, 64), dtype)
+        call = _abi_matmul_call(ctx, da, db, dc, 64, 256, 64)
         for _ in range(20):
-            _abi_matmul(ctx, da, db, dc, 64, 256, 64)
+            call()
         t0 = time.perf_counter()
         for _ in range(reps):
-            _abi_matmul(ctx, da, db, dc, 64, 256, 64)
+            call()
         t1 = time.perf_counter()
         out[f"matmul_64x256x64_{tag}_us"] = (t1 - t0) * 1e6 / reps
         out[f"matmul_64x256x64_{tag}_reference_us"] = ref
