@@ -1319,18 +1319,22 @@ hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t 
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// A stored R x C float matrix copied into C x R (R and C multiples of 4, both pointers
-// 16-byte aligned): 64 x 64 tiles through LDS, 16-byte loads and stores, rows of the tile
-// padded by one float so that both phases meet at most two lanes a bank. Used for a
-// transposed op(B) of the matrix-core engine: the copy holds the same values, so every
+// A stored R x C matrix copied into C x R (R and C multiples of 4, both pointers 16-byte
+// aligned): 64 x 64 tiles through LDS, runs of four elements (one or two 16-byte loads and
+// stores), rows of the tile padded by one element. Used for a transposed op(B) that the
+// tile kernel then loads as an untransposed one: the copy holds the same values, so every
 // product, sum and fault of the MatMul is unchanged.
-__global__ __launch_bounds__(256) void k_transpose_f32(const float *__restrict__ X,
-                                                      float *__restrict__ Y, int R, int C,
-                                                      NodeGate gate)
+template <typename T> struct alignas(16) Run4 {
+    T v[4];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose(const T *__restrict__ X, T *__restrict__ Y,
+                                                   int R, int C, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
-    __shared__ float t[64][65];
+    __shared__ T t[64][65];
     const int tiles_c = (C + 63) / 64;
     const int r0 = (int)(blockIdx.x / tiles_c) * 64, c0 = (int)(blockIdx.x % tiles_c) * 64;
     const int q = threadIdx.x & 15, row = threadIdx.x >> 4; // 16 runs of 4 floats x 16 rows
@@ -1338,31 +1342,37 @@ __global__ __launch_bounds__(256) void k_transpose_f32(const float *__restrict__
     for (int p = 0; p < 4; p++) {
         const int i = row + 16 * p, r = r0 + i, c = c0 + 4 * q;
         if (r < R && c < C) {
-            const float4 v = *reinterpret_cast<const float4 *>(X + (size_t)r * C + c);
-            t[i][4 * q] = v.x;
-            t[i][4 * q + 1] = v.y;
-            t[i][4 * q + 2] = v.z;
-            t[i][4 * q + 3] = v.w;
+            const Run4<T> v = *reinterpret_cast<const Run4<T> *>(X + (size_t)r * C + c);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                t[i][4 * q + e] = v.v[e];
         }
     }
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < 4; p++) {
         const int j = row + 16 * p, c = c0 + j, r = r0 + 4 * q;
-        if (c < C && r < R)
-            *reinterpret_cast<float4 *>(Y + (size_t)c * R + r) =
-                make_float4(t[4 * q][j], t[4 * q + 1][j], t[4 * q + 2][j], t[4 * q + 3][j]);
+        if (c < C && r < R) {
+            Run4<T> v;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v.v[e] = t[4 * q + e][j];
+            *reinterpret_cast<Run4<T> *>(Y + (size_t)c * R + r) = v;
+        }
     }
 }
 
-// Largest op(B) copied out for the matrix-core engine (1 GiB of floats); larger ones are
-// read in place.
+// Largest op(B) copied out (2^28 elements); larger ones are read in place.
 constexpr uint64_t kBtMaxElems = 1ull << 28;
 
-bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tr,
-                      int engine)
+bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tl,
+                      bool tr, int engine)
 {
-    if (dtype != 0 || !tr || engine == kEngineValu || inner == 0 || inner % 16 != 0)
+    if (!tr || (dtype == 0 && engine == kEngineValu) || inner == 0 || inner % 16 != 0)
+        return false;
+    // Binary64: NT 4096^3 4507 against 4692 us, 2048^3 610 against 674; TT measured no
+    // faster (4563 against 4523), its op(A) read-ahead path already hides the staging.
+    if (dtype != 0 && tl)
         return false;
     if (engine == kEngineAuto && rows * cols <= fused_cells<float>())
         return false; // the fused small-output launch reads B in place
@@ -1500,9 +1510,9 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         bool tbt = tb;
         if (tb && sc.bt && aligned16(B)) {
             const unsigned tiles = (unsigned)(((N + 63) / 64) * ((K + 63) / 64));
-            hipLaunchKernelGGL(k_transpose_f32, dim3(tiles), dim3(256), 0, s, (const float *)B,
-                               sc.bt, n, k, gate);
-            Bt = sc.bt;
+            hipLaunchKernelGGL(k_transpose<float>, dim3(tiles), dim3(256), 0, s, (const float *)B,
+                               (float *)sc.bt, n, k, gate);
+            Bt = (const float *)sc.bt;
             tbt = false;
         }
         (void)launch_gemm_mfma_f32(s, m, n, k, ta, tbt, (const float *)A, Bt, (float *)C,
@@ -1514,10 +1524,22 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         else if (!ta && tb) f64n_dispatch<false, true>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
         else if (ta && !tb) f64n_dispatch<true, false>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
         else f64n_dispatch<true, true>(s, dA, dB, dC, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-    } else if (!ta && !tb) gemm_dispatch<T, false, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-    else if (!ta && tb) gemm_dispatch<T, false, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-    else if (ta && !tb) gemm_dispatch<T, true, false>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-    else gemm_dispatch<T, true, true>(s, grid, A, B, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    } else {
+        // A transposed binary64 op(B) on a full grid goes to the tile kernel as its K x N
+        // copy, as for the matrix-core engine above.
+        const T *Bk = B;
+        bool tbk = tb;
+        if (!f32 && tb && sc.bt && aligned16(B)) {
+            const unsigned tiles = (unsigned)(((N + 63) / 64) * ((K + 63) / 64));
+            hipLaunchKernelGGL(k_transpose<T>, dim3(tiles), dim3(256), 0, s, B, (T *)sc.bt, n, k, gate);
+            Bk = (const T *)sc.bt;
+            tbk = false;
+        }
+        if (!ta && !tbk) gemm_dispatch<T, false, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else if (!ta && tbk) gemm_dispatch<T, false, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else if (ta && !tbk) gemm_dispatch<T, true, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        else gemm_dispatch<T, true, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;

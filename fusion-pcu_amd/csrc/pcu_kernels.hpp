@@ -80,16 +80,16 @@ struct MatmulScratch {
     unsigned long long *suspect;    // first suspect cell (kNoFault when none)
     unsigned long long *flag_first; // first row with a flagged cell (kNoFault when none)
     uint32_t gen = 1;
-    // K x N floats for a transposed F32 op(B) copied out for the matrix-core engine, or
-    // null (the tile kernel then reads B in place). See matmul_bt_wanted.
-    float *bt = nullptr;
+    // K x N elements for a transposed op(B) copied out for the tile kernel, or null (the
+    // tile kernel then reads B in place). See matmul_bt_wanted.
+    void *bt = nullptr;
 };
-// Whether a strict F32 MatMul on the matrix-core engine runs its tile kernel on a copy of a
-// transposed op(B) stored K x N (grids of whole 128 x 128 tiles, K a multiple of 16): the tile
-// kernels load an untransposed op(B) straight into LDS but stage a transposed one through
-// registers.
-bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tr,
-                      int engine);
+// Whether a strict MatMul (F32 on the matrix-core engine, or F64) runs its tile kernel on a
+// copy of a transposed op(B) stored K x N (grids of whole 128 x 128 tiles, K a multiple of
+// 16): the tile kernels load an untransposed op(B) straight into LDS but stage a transposed
+// one through registers.
+bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tl,
+                      bool tr, int engine);
 size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);
 MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
 

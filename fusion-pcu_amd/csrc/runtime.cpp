@@ -699,13 +699,13 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     }
     MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
     s.gen = gen;
-    // The copy of a transposed F32 op(B) for the matrix-core tile kernel; the no-allocation
-    // call reads B in place.
-    if (!noalloc && matmul_bt_wanted(dtype, rows, inner, cols, tr != 0, matmul_engine)) {
+    // The copy of a transposed op(B) for the tile kernel; the no-allocation call reads B in
+    // place.
+    if (!noalloc && matmul_bt_wanted(dtype, rows, inner, cols, tl != 0, tr != 0, matmul_engine)) {
         void *bt = nullptr;
-        if ((st = scratch(bt_scratch, (size_t)(inner * cols * sizeof(float)), false, &bt)))
+        if ((st = scratch(bt_scratch, (size_t)(inner * cols * dsize(dtype)), false, &bt)))
             return st;
-        s.bt = (float *)bt;
+        s.bt = bt;
     }
 
     // Per-kernel timing takes events from a pool that may grow, so the no-allocation call
