@@ -118,9 +118,12 @@ pcu_status pcu_ctx_synchronize(pcu_ctx *ctx);
 /* Engine of the strict MatMul. Every engine gives the same bits and the same first fault.
  *  PCU_MATMUL_VALU: each product is a v_mul and each sum a v_add (F32 and F64).
  *  PCU_MATMUL_MFMA_PRODUCTS: for F32 the matrix cores act as a multiplier array only
- *   (v_mfma_f32_32x32x1_2b_f32, K = 1, +0 accumulator input): every element is one
- *   product rounded once. The ordered sums stay separate v_add_f32 in k order, and no
- *   sum is formed in the matrix core. F64 uses the vector unit.
+ *   (K = 1, +0 accumulator input): every element is one product rounded once. Outputs of
+ *   fewer 128 x 128 tiles than CUs made of at most 512 whole 64 x 64 tiles, with K a
+ *   multiple of 16, use v_mfma_f32_16x16x1_4b_f32 (four blocks, k0 .. k0 + 3); all other
+ *   outputs use v_mfma_f32_32x32x1_2b_f32 (two blocks, k and k + 1). The ordered sums stay
+ *   separate v_add_f32 in k order, and no sum is formed in the matrix core. F64 uses the
+ *   vector unit.
  *  PCU_MATMUL_AUTO (default): outputs of at most 256 x 256 cells (F32) or 512 x 512 (F64)
  *   run as one fused launch on the vector unit (screen, products and sums, and the exact
  *   first-fault search per 16 x 16 block); larger ones as PCU_MATMUL_MFMA_PRODUCTS.

@@ -147,3 +147,143 @@ def test_mfma_products_fault_coordinates(ctx, pcu_pkg, k):
             for engine in ("mfma_products", "valu"):
                 _, gf = _run(ctx, pcu_pkg, aa, bb, policy, engine)
                 assert gf == _of(rf), (name, policy, engine, gf, rf)
+
+
+# ------------------------------------------------- the four-block 16 x 16 product form
+# Outputs of fewer 128 x 128 tiles than CUs made of at most 512 whole 64 x 64 tiles, with K a
+# multiple of 16 (C2's 1024^3 among them), go to k_strict_gemm_mfma16, which forms its
+# products with v_mfma_f32_16x16x1_4b_f32: four blocks of 16 x 16 products, one k each
+# (k0 .. k0 + 3), published straight from the matrix core. 1024 x K x 1024 with K = 16 or
+# 32 is such a shape (64 tiles of 128 x 128, 256 of 64 x 64).
+M16 = 1024
+LAYOUTS = [(False, False), (False, True), (True, False), (True, True)]
+LAYOUT_IDS = ["nn", "nt", "tn", "tt"]
+
+
+def _stored(a, b, ta, tb):
+    """The stored operands of a layout: op(A) = a, op(B) = b."""
+    return (np.ascontiguousarray(a.T) if ta else a), (np.ascontiguousarray(b.T) if tb else b)
+
+
+def _run_layout(ctx, pcu_pkg, a, b, policy, engine, ta, tb):
+    ctx.set_matmul_engine(engine)
+    sa, sb = _stored(a, b, ta, tb)
+    da, db = ctx.upload(sa), ctx.upload(sb)
+    try:
+        out = ctx.strict_matmul(da, db, ta, tb, policy)
+        got = out.numpy()
+        out.free()
+        return got, None
+    except pcu_pkg.PcuExecutionError as e:
+        f = e.tensor_fault
+        return None, (f.element_index, f.reduction_index, int(f.step), int(f.kind))
+    finally:
+        da.free()
+        db.free()
+
+
+@pytest.fixture(scope="module")
+def pools():
+    rng = np.random.default_rng(4242)
+    return _pool(rng, "a"), _pool(rng, "b")
+
+
+def _single_products(pools, i, j, k, seed):
+    """op(A) (M16 x k) whose row r holds one nonzero, A-pool segment i's value r, at k = r % k;
+    op(B) (k x M16) whose every row is a permutation of B-pool segment j. Cell (r, c) is
+    then ((+0 + 0 b) + ...) + a_r B[r % k, c] + ...: the one product rounded once (zero
+    products leave a +0 or nonzero sum unchanged), so every A value of segment i meets every
+    B value of segment j, and every block of every MFMA (k0 .. k0 + 3 for each k0) publishes
+    products. The 16 (i, j) segment pairs meet all 4096 x 4096 pool pairs."""
+    pa, pb = pools
+    rng = np.random.default_rng(seed)
+    a = np.zeros((M16, k), np.float32)
+    a[np.arange(M16), np.arange(M16) % k] = rng.permutation(pa[i * SEG:(i + 1) * SEG])
+    b = np.stack([rng.permutation(pb[j * SEG:(j + 1) * SEG]) for _ in range(k)])
+    return a, b
+
+
+@pytest.mark.parametrize("k", [16, 32])
+def test_mfma16_single_products_bit_exact(ctx, pcu_pkg, pools, k):
+    """Every pool pair once, as a published single product, in all four layouts and both
+    engines under AllowGradual; the first fault under IEEE and RejectSubnormal."""
+    tiny = np.finfo(np.float32).tiny
+    n_sub = n_ties = 0
+    for i in range(4):
+        for j in range(4):
+            a, b = _single_products(pools, i, j, k, 100 * k + 4 * i + j)
+            for policy in (2, 0, 1):
+                ref, rf = oracle.matmul(a, b, policy=policy)
+                layouts = LAYOUTS if policy == 2 else LAYOUTS[:1]
+                for ta, tb in layouts:
+                    for engine in ("mfma_products", "valu"):
+                        got, gf = _run_layout(ctx, pcu_pkg, a, b, policy, engine, ta, tb)
+                        assert gf == _of(rf), (i, j, policy, ta, tb, engine, gf, rf)
+                        if rf is None:
+                            np.testing.assert_array_equal(
+                                _bits(got), _bits(ref), err_msg=f"{i}{j} {ta}{tb} {engine}")
+                if policy == 2:
+                    p = np.abs(ref.astype(np.float64))
+                    n_sub += np.count_nonzero((p > 0) & (p < tiny))
+                    if i == 0 and j == 0:
+                        # ties x ties: exact binary64 products halfway between two floats
+                        nz = a[np.arange(M16), np.arange(M16) % k].astype(np.float64)
+                        ex = nz[:, None] * b[np.arange(M16) % k].astype(np.float64)
+                        lo = ex.astype(np.float32)
+                        up = np.nextafter(lo, np.float32(np.inf) * np.sign(lo))
+                        mid = (lo.astype(np.float64) + up.astype(np.float64)) / 2
+                        n_ties += np.count_nonzero(mid == ex)
+    # The sweep reaches the cases it is meant for.
+    assert n_sub > 200_000
+    assert n_ties > 50_000
+
+
+def _dense(pools, k, seed):
+    """Dense op(A) (M16 x k) and op(B) (k x M16) from the pools: column c of A and row r of
+    B are permutations of a pool's first M16 entries of a random segment mix."""
+    pa, pb = pools
+    rng = np.random.default_rng(seed)
+    a = np.stack([rng.permutation(pa)[:M16] for _ in range(k)], 1)
+    b = np.stack([rng.permutation(pb)[:M16] for _ in range(k)], 0)
+    return np.ascontiguousarray(a), np.ascontiguousarray(b)
+
+
+@pytest.mark.parametrize("k", [16, 48, 80])
+def test_mfma16_dense_sums_bit_exact(ctx, pcu_pkg, pools, k):
+    """Dense reductions over one, three and five slabs (the three-stage rotation and its
+    tail): every output bit and first fault against the oracle, all layouts and policies."""
+    a, b = _dense(pools, k, 7000 + k)
+    for policy in (2, 0, 1):
+        ref, rf = oracle.matmul(a, b, policy=policy)
+        for ta, tb in LAYOUTS:
+            for engine in ("mfma_products", "valu"):
+                got, gf = _run_layout(ctx, pcu_pkg, a, b, policy, engine, ta, tb)
+                assert gf == _of(rf), (policy, ta, tb, engine, gf, rf)
+                if rf is None:
+                    np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{ta}{tb} {engine}")
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=LAYOUT_IDS)
+def test_mfma16_fault_coordinates(ctx, pcu_pkg, pools, layout):
+    """Overflowing and non-finite operands planted in the dense K = 16 sweep: both engines
+    report the oracle's first (cell, k, step, kind) under every policy."""
+    ta, tb = layout
+    a, b = _dense(pools, 16, 8016)
+    rng = np.random.default_rng(77)
+    cases = [
+        ("overflow", lambda a, b: (a.__setitem__((700, 9), np.float32(3.0e38)),
+                                   b.__setitem__((9, 300), np.float32(2.0e10)))),
+        ("nan", lambda a, b: b.__setitem__((int(rng.integers(16)), int(rng.integers(M16))),
+                                           np.float32(np.nan))),
+        ("inf", lambda a, b: a.__setitem__((int(rng.integers(M16)), int(rng.integers(16))),
+                                           np.float32(-np.inf))),
+    ]
+    for name, plant in cases:
+        aa, bb = a.copy(), b.copy()
+        plant(aa, bb)
+        for policy in (0, 1, 2):
+            _, rf = oracle.matmul(aa, bb, policy=policy)
+            assert rf is not None
+            for engine in ("mfma_products", "valu"):
+                _, gf = _run_layout(ctx, pcu_pkg, aa, bb, policy, engine, ta, tb)
+                assert gf == _of(rf), (name, policy, engine, gf, rf)
