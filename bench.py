@@ -63,11 +63,11 @@ def _abi_matmul_call(ctx, da, db, dc, m, k, n, policy=0):
     return lambda: fn(*args)
 
 
-def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0):
+def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0, policy=0):
     """ms per complete call, timed with per-kernel timing off, then the kernel breakdown
     (prefilter, main tile kernel, replay including the tiny scan) from a second timed
     pass of the same number of calls."""
-    call = _abi_matmul_call(ctx, da, db, dc, m, k, n)
+    call = _abi_matmul_call(ctx, da, db, dc, m, k, n, policy)
     for _ in range(warmup):
         assert call() == expect
     ctx.synchronize()
@@ -93,6 +93,30 @@ def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0):
         "prefilter_avg_ms": pre_ms / max(gemm_n, 1),
         "replay_avg_ms": rep_ms / max(gemm_n, 1),
     }
+
+
+def settle_clock(ctx, ms):
+    """Bring the GPU out of its idle clock before the first leg. A cold MI355X runs the first
+    ~15 strict 4096^3 launches (about 30 ms of load) up to 25% slower while its clock ramps
+    (2291 -> 1890 us a launch in one trace), which a short warm-up leaves inside the timed
+    steps. This runs a different workload, the native (BackendDefined) F32 MatMul 4096^3,
+    for about `ms` milliseconds; no leg's timed region includes it."""
+    from fusion_pcu_amd import synthetic as syn
+    if ms <= 0:
+        return 0
+    da = ctx.upload(syn.uniform(91, (4096, 4096), np.float32))
+    db = ctx.upload(syn.uniform(92, (4096, 4096), np.float32))
+    dc = ctx.empty((4096, 4096), np.float32)
+    calls = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            ctx.native_matmul(da, db, out=dc)
+        ctx.synchronize()
+        calls += 8
+    for x in (da, db, dc):
+        x.free()
+    return calls
 
 
 def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
@@ -146,6 +170,37 @@ def bench_c2_variants(pkg, ctx, steps):
     r = time_matmul(ctx, da, db, dc, M, M, M, max(3, steps // 4), 2)
     r["input"] = "A col 0 = +-2^-120, B row 0 in +-[0.5, 1), rest uniform[-1,1]: every cell marked, none faults"
     out["suspect_heavy_clean_4096"] = r
+    for x in (da, db, dc):
+        x.free()
+    return out
+
+
+def bench_policies(pkg, ctx, steps):
+    """The strict F32 MatMul 4096^3 under the two other underflow policies
+    (core/scalar_float_underflow.rs:61-73), clean, and the suspect-heavy input (A column 0
+    at +-2^-120, so every cell meets a product below 2^-103 and the exponent screen marks
+    all of them) under RejectSubnormal, where a subnormal partial sum faults too: the tile
+    kernel checks the partial sums of every marked tile, so the replay walks only cells whose
+    lane met a subnormal sum (none here)."""
+    from fusion_pcu_amd import synthetic as syn
+    M = 4096
+    a = syn.uniform(11, (M, M), np.float32)
+    b = syn.uniform(12, (M, M), np.float32)
+    out = {}
+    dc = ctx.empty((M, M), np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    for name, policy in (("reject_subnormal_clean", 1), ("allow_gradual_clean", 2), ("ieee_clean", 0)):
+        out[name] = time_matmul(ctx, da, db, dc, M, M, M, steps, 3, policy=policy)
+    da.free()
+    db.free()
+    sign = np.where(np.random.default_rng(3).random(M) < 0.5, -1.0, 1.0)
+    a[:, 0] = (2.0 ** -120 * sign).astype(np.float32)
+    b[0, :] = (np.random.default_rng(4).uniform(0.5, 1.0, M) * sign[::-1]).astype(np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    r = time_matmul(ctx, da, db, dc, M, M, M, steps, 3, policy=1)
+    r["input"] = "A col 0 = +-2^-120, B row 0 in +-[0.5, 1), rest uniform[-1,1]: every cell marked, none faults"
+    out["reject_subnormal_suspect_heavy"] = r
+    out["suspect_heavy_reject_over_clean_ieee"] = r["ms_per_step"] / out["ieee_clean"]["ms_per_step"]
     for x in (da, db, dc):
         x.free()
     return out
@@ -466,6 +521,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=32)
+    ap.add_argument("--settle-ms", type=float, default=60.0,
+                    help="native MatMul load before the first leg, so the clock has left idle")
     ap.add_argument("--probe", action="store_true",
                     help="run each profiled kernel once (for rocprofv3 --pmc passes) and exit")
     args = ap.parse_args()
@@ -482,6 +539,8 @@ def main() -> int:
     G.configure(0)
     ctx = G.default_context()
     if True:
+        log(f"clock settle: native F32 MatMul for {args.settle_ms:.0f} ms")
+        settle_calls = settle_clock(ctx, args.settle_ms)
         log("strict F32 MatMul 4096^3")
         mm = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup)
         extra = {}
@@ -514,6 +573,8 @@ def main() -> int:
             extra["sgd_f32_2p28"] = bench_sgd(pkg, ctx, 1 << 28, max(5, args.steps), 2)
             log("C2 1024^3 clean and fault variants; a fully screen-marked clean 4096^3")
             extra["c2_and_replay"] = bench_c2_variants(pkg, ctx, max(10, args.steps))
+            log("F32 MatMul 4096^3 under RejectSubnormal and AllowGradual; suspect-heavy RejectSubnormal")
+            extra["policies_4096"] = bench_policies(pkg, ctx, 10)
             log("C3 F64 MatMul + bias + ReLU program")
             extra["c3_f64_program"] = bench_c3(pkg, ctx, max(2, args.steps // 3), args.warmup)
             log("C1 training-step latency")
@@ -561,7 +622,9 @@ def main() -> int:
                                "prefilter + tile kernel + replay check + fault readback; timed "
                                "with per-kernel timing off (the roofline's kernel duration comes "
                                "from a second, timed pass)",
-                   "m": M, "k": K, "n": N},
+                   "m": M, "k": K, "n": N,
+                   "clock_settle": f"{settle_calls} native F32 MatMul 4096^3 calls (~{args.settle_ms:.0f} ms) "
+                                   f"before the first leg, outside every timed region"},
         "pct_fp32_vector_peak": round(100.0 * mm["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 3),
         "mlp_train_steps_per_s": (round(extra["mlp_c5"]["steps_per_s"], 3)
                                   if "mlp_c5" in extra else None),

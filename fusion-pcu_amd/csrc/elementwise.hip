@@ -37,7 +37,7 @@ template <typename T, bool VEC> struct Lanes {
 // Elements [base, base + W) of p that lie below n (the rest read as +0 and must be masked
 // by the caller). A whole vector is one non-temporal 16-byte load.
 template <typename T, bool VEC>
-__device__ __forceinline__ void load_lanes(const T *__restrict__ p, uint64_t base, uint64_t n,
+__device__ __forceinline__ void load_lanes(const T *p, uint64_t base, uint64_t n,
                                            T (&v)[Lanes<T, VEC>::W])
 {
     constexpr int W = Lanes<T, VEC>::W;
@@ -55,7 +55,7 @@ __device__ __forceinline__ void load_lanes(const T *__restrict__ p, uint64_t bas
 }
 
 template <typename T, bool VEC, bool NT = true>
-__device__ __forceinline__ void store_lanes(T *__restrict__ p, uint64_t base, uint64_t n,
+__device__ __forceinline__ void store_lanes(T *p, uint64_t base, uint64_t n,
                                             const T (&v)[Lanes<T, VEC>::W])
 {
     constexpr int W = Lanes<T, VEC>::W;
@@ -114,11 +114,14 @@ __device__ __forceinline__ uint32_t classify(T a, T b, T r, int policy)
 }
 
 // ------------------------------------------------------------ checked binary
+// The checked elementwise and SGD kernels may run in place (out equal to an operand), so
+// none of their pointers is __restrict__: a fault is classified from register values after
+// the store, and the compiler may not reload an operand from memory the store overwrote.
 
 template <typename T, int OP, bool UNIFORM, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
-                                                       const T *__restrict__ b, T b_value,
-                                                       T *__restrict__ out, uint64_t n,
+__global__ __launch_bounds__(kEwThreads) void k_binary(const T *a,
+                                                       const T *b, T b_value,
+                                                       T *out, uint64_t n,
                                                        int policy, unsigned long long *fault, NodeGate gate)
 {
     if (wave_gate_closed(gate))
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kEwThreads) void k_binary(const T *__restrict__ a,
 // -------------------------------------------------------------------- relu
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T *__restrict__ out,
+__global__ __launch_bounds__(kEwThreads) void k_relu(const T *x, T *out,
                                                      uint64_t n, int policy,
                                                      unsigned long long *fault, NodeGate gate)
 {
@@ -197,9 +200,9 @@ __global__ __launch_bounds__(kEwThreads) void k_relu(const T *__restrict__ x, T 
 // ---------------------------------------------------------- relu backward
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restrict__ x,
-                                                              const T *__restrict__ up,
-                                                              T *__restrict__ out, uint64_t n,
+__global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *x,
+                                                              const T *up,
+                                                              T *out, uint64_t n,
                                                               int policy,
                                                               unsigned long long *fault, NodeGate gate)
 {
@@ -240,9 +243,9 @@ __global__ __launch_bounds__(kEwThreads) void k_relu_backward(const T *__restric
 // (a ReLU of a successful, hence finite, sum can only fault under RejectSubnormal).
 
 template <typename T, bool UNIFORM, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *__restrict__ a,
-                                                         const T *__restrict__ b, T b_value,
-                                                         T *__restrict__ out, uint64_t n,
+__global__ __launch_bounds__(kEwThreads) void k_add_relu(const T *a,
+                                                         const T *b, T b_value,
+                                                         T *out, uint64_t n,
                                                          int policy,
                                                          unsigned long long *fault_add,
                                                          unsigned long long *fault_relu, NodeGate gate)
@@ -433,9 +436,9 @@ __global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n,
 // w' = w (-) p; ordinal 2i (Multiply) and 2i+1 (Subtract).
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_sgd(const T *__restrict__ w,
-                                                    const T *__restrict__ g, T rate,
-                                                    T *__restrict__ out, uint64_t n, int policy,
+__global__ __launch_bounds__(kEwThreads) void k_sgd(const T *w,
+                                                    const T *g, T rate,
+                                                    T *out, uint64_t n, int policy,
                                                     unsigned long long *fault, NodeGate gate)
 {
     if (wave_gate_closed(gate))
@@ -1551,9 +1554,9 @@ __global__ __launch_bounds__(256) void k_mse_serial(const T *__restrict__ p, con
 // SGD (backends/rocm/tensor/native_sgd/native_sgd.rs:100-145): the product rounded before
 // the subtraction, or one fused multiply-add when contraction is permitted.
 template <typename T, bool VEC, bool CONTRACT>
-__global__ __launch_bounds__(kEwThreads) void k_native_sgd(const T *__restrict__ w,
-                                                           const T *__restrict__ g, T rate,
-                                                           T *__restrict__ out, uint64_t n, NodeGate gate)
+__global__ __launch_bounds__(kEwThreads) void k_native_sgd(const T *w,
+                                                           const T *g, T rate,
+                                                           T *out, uint64_t n, NodeGate gate)
 {
     if (wave_gate_closed(gate))
         return;
@@ -1977,6 +1980,41 @@ hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p
         return hipErrorInvalidValue;
     return dtype == 0 ? native_mse_t<float>(s, n, p, t, scratch, (float)scale, out, gate)
                       : native_mse_t<double>(s, n, p, t, scratch, scale, out, gate);
+}
+
+
+// ------------------------------------------------------------ program end
+// The fault words go to the host without a copy command: one workgroup copies them into
+// coherent pinned memory, resets them (and opens the stage gate) for the next program, and
+// then stores the program's sequence number, so the host waits on that one word instead of
+// the stream.
+__global__ __launch_bounds__(256) void k_program_publish(unsigned long long *words, uint64_t n,
+                                                         unsigned long long value, unsigned int *gate,
+                                                         unsigned long long *host_words,
+                                                         unsigned long long *host_seq, uint64_t seq)
+{
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const unsigned long long w = words[i];
+        __hip_atomic_store(&host_words[i], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        words[i] = value;
+    }
+    if (threadIdx.x == 0)
+        *gate = 0xffffffffu;
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store(host_seq, (unsigned long long)seq, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+hipError_t launch_program_publish(hipStream_t s, unsigned long long *words, uint64_t n,
+                                  uint64_t value, unsigned int *gate,
+                                  unsigned long long *host_words, unsigned long long *host_seq,
+                                  uint64_t seq)
+{
+    hipLaunchKernelGGL(k_program_publish, dim3(1), dim3(256), 0, s, words, n,
+                       (unsigned long long)value, gate, host_words, host_seq, seq);
+    return hipGetLastError();
 }
 
 } // namespace pcu

@@ -37,6 +37,9 @@
 namespace pcu {
 
 constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
+// The same in the 16-bit exponents of the tiny scan and the superslab tables (two of them
+// still sum far above any threshold).
+constexpr short kScanExpNone = 16000;
 
 // Branch-free: the prefilter applies it to every element of both operands.
 __device__ __forceinline__ int ilog2_abs(float v)
@@ -79,7 +82,16 @@ template <typename T> struct ExpJob {
     bool rows;
     bool vec; // C a multiple of 16 bytes and X 16-byte aligned
     unsigned long long *out;
+    // Optional superslab table: the smallest exponent (kScanExpNone for zero and non-finite
+    // entries) of each entry's run of kSuperSlab k. A rows job (k along its rows) writes it
+    // entry-major, tbl[row * ceil(C / kSuperSlab) + s]; a columns job (k down its columns)
+    // superslab-major, tbl[s * C + column]. Null: no table.
+    short *tbl;
 };
+
+// Superslab of the tables above: 64 k, four slabs of the tiny scan, and the 64-row group of a
+// columns-job block.
+constexpr uint64_t kSuperSlab = 64;
 
 // Rows job, block `bid`: one wave per row, four rows per 256-thread block; four 16-byte loads
 // per lane in flight.
@@ -133,6 +145,65 @@ __device__ __forceinline__ void exp_rows_block(const ExpJob<T> &j, uint64_t bid,
         j.out[r] = exp_word(gen, m);
 }
 
+// Rows job that also writes the row's superslab table: the same minima, from loops whose trip
+// counts are uniform across the wave so the lanes of a superslab can fold their minima.
+template <typename T, bool VEC>
+__device__ __forceinline__ void exp_rows_block_tbl(const ExpJob<T> &j, uint64_t bid, uint32_t gen)
+{
+    const uint64_t r = bid * 4 + threadIdx.x / 64;
+    if (r >= j.R)
+        return; // whole wave exits together
+    const int lane = threadIdx.x % 64;
+    const uint64_t C = j.C, nss = (C + kSuperSlab - 1) / kSuperSlab;
+    const T *row = j.X + r * C;
+    short *trow = j.tbl + r * nss;
+    int m = kExpNone;
+    if (VEC) {
+        constexpr int P = 16 / sizeof(T), L = (int)kSuperSlab / P; // lanes a superslab
+        constexpr uint64_t S = 64 * P;
+        constexpr int U = 4;
+        for (uint64_t base = 0; base < C; base += U * S) {
+            uint4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint64_t c = base + u * S + (uint64_t)lane * P;
+                q[u] = c < C ? *reinterpret_cast<const uint4 *>(row + c) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint64_t c = base + u * S + (uint64_t)lane * P;
+                const T *v = reinterpret_cast<const T *>(&q[u]);
+                int e = kExpNone; // zeros past the end count as zero entries
+#pragma unroll
+                for (int k = 0; k < P; k++) {
+                    const int x = ilog2_abs(v[k]);
+                    e = x < e ? x : e;
+                }
+                m = e < m ? e : m;
+#pragma unroll
+                for (int off = 1; off < L; off <<= 1) {
+                    const int o = __shfl_xor(e, off, 64);
+                    e = o < e ? o : e;
+                }
+                if (lane % L == 0 && c < C)
+                    trow[c / kSuperSlab] = (short)(e == kExpNone ? kScanExpNone : e);
+            }
+        }
+    } else {
+        for (uint64_t base = 0; base < C; base += 64) { // one superslab a trip
+            const uint64_t c = base + lane;
+            int e = c < C ? ilog2_abs(row[c]) : kExpNone;
+            m = e < m ? e : m;
+            e = wave_min_i32(e);
+            if (lane == 0)
+                trow[base / kSuperSlab] = (short)(e == kExpNone ? kScanExpNone : e);
+        }
+    }
+    m = wave_min_i32(m);
+    if (lane == 0)
+        j.out[r] = exp_word(gen, m);
+}
+
 // Columns job, block `bid` = (column block cb, 64-row group rg): 64 column-runs (16 bytes
 // each) by 4 row groups of 16 rows; the row groups meet in LDS and the block folds its
 // minimum into out with one atomicMax per column. Fewer rows per block measured slower: the
@@ -140,6 +211,7 @@ __device__ __forceinline__ void exp_rows_block(const ExpJob<T> &j, uint64_t bid,
 // 28.1 -> 29.6 / 28.7 us, K = 1024 12.5 -> 14.0 / 18.7 us, binary64 48.0 -> 51.1 / 49.8 us),
 // except when both jobs are column jobs (op(A) transposed: 34.7 -> 30.3 us).
 constexpr uint64_t kColRows = 64; // rows of a columns-job block
+static_assert(kColRows == kSuperSlab, "a columns-job block's rows are one superslab of k");
 
 template <typename T, bool VEC>
 __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen,
@@ -204,6 +276,9 @@ __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid,
             for (int g = 1; g < 4; g++)
                 v = part[g][cx * P + k] < v ? part[g][cx * P + k] : v;
             atomicMax(&j.out[c0 + k], exp_word(gen, v));
+            // The block's rows are superslab rg of k.
+            if (j.tbl && c0 + k < C)
+                j.tbl[rg * C + c0 + k] = (short)(v == kExpNone ? kScanExpNone : v);
         }
     }
 }
@@ -249,10 +324,16 @@ __global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, ui
     const ExpJob<T> &j = first ? a : b;
     const uint64_t bid = first ? blockIdx.x : blockIdx.x - na;
     if (j.rows) {
-        if (j.vec)
+        if (j.tbl) {
+            if (j.vec)
+                exp_rows_block_tbl<T, true>(j, bid, gen);
+            else
+                exp_rows_block_tbl<T, false>(j, bid, gen);
+        } else if (j.vec) {
             exp_rows_block<T, true>(j, bid, gen);
-        else
+        } else {
             exp_rows_block<T, false>(j, bid, gen);
+        }
     } else {
         if (j.vec)
             exp_cols_block<T, true>(j, bid, gen, part);
@@ -295,6 +376,7 @@ __global__ void k_fill_u64(unsigned long long *p, uint64_t n, unsigned long long
 // ------------------------------------------------------------------- main tile
 
 constexpr int BM = 128, BN = 128; // output tile of every MatMul kernel here
+constexpr unsigned kGfx950Cus = 256; // compute units of a gfx950 device (MI350X, MI355X)
 
 // Tile shape of the vector-unit kernel: 128 x 128 outputs per 256-thread workgroup (8 x 8
 // per thread); binary64 stages twice as deep a k-slab, halving its barriers.
@@ -326,11 +408,13 @@ __device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt
 // NATIVE (explicitly permitted native compound arithmetic): one fused multiply-add per
 // (cell, k) and no fault screen.
 // WHOLE: every slab of every tile is whole (see the MFMA kernel).
-template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false, bool WHOLE = false>
+// CHECK: the RejectSubnormal form with the partial-sum check (sck), its own instantiation.
+template <typename T, bool TA, bool TB, bool VA, bool VB, bool NATIVE = false, bool WHOLE = false,
+          bool CHECK = false>
 __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
     const unsigned long long *__restrict__ row_exp, const unsigned long long *__restrict__ col_exp,
-    int thr, int check_risk, int vec_c, unsigned long long *suspect, NodeGate gate)
+    int thr, int check_risk, int vec_c, unsigned long long *suspect, SumCheck sck, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -363,6 +447,15 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     int tile_m, tile_n;
     tile_of(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
+    // RejectSubnormal with the partial-sum check (sck.flag set) launches both forms over the
+    // whole grid: a tile that may meet a product below 2^sck.thr is computed by the CHECK form,
+    // which checks every partial sum it forms, and every other tile by the plain form.
+    if (!NATIVE && sck.flag != nullptr &&
+        tile_exp_sum_below<BM, BN>(row_exp, col_exp, m0, n0, M, N, sck.thr) != CHECK)
+        return;
+    SubLanes subl; // lanes that met a nonzero subnormal partial sum
+    const int cls = kClassSubnormal;
+    auto run_form = [&](auto &&run) { run(std::integral_constant<bool, CHECK && !NATIVE>{}); };
 
     T acc[8][8];
 #pragma unroll
@@ -377,7 +470,8 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     if (WHOLE)
         stage.begin_whole(A, B, M, N, K, m0, n0, tid);
     // One slab's products and sums from the stage (Ac, Bc).
-    auto compute = [&](const T (*Ac)[Cfg::LDA], const T (*Bc)[Cfg::LDB]) __attribute__((always_inline)) {
+    auto compute = [&](const T (*Ac)[Cfg::LDA], const T (*Bc)[Cfg::LDB], auto ck) __attribute__((always_inline)) {
+        constexpr bool CK = decltype(ck)::value;
         if constexpr (kAhead) {
             // The slab is unrolled; row k + 1's operands are read from LDS into the other
             // register set before row k is computed, and sched_barrier keeps the reads
@@ -420,6 +514,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 #pragma unroll
                             for (int j = 0; j < PB; j++)
                                 acc[i][h + j] = acc[i][h + j] + p[j];
+                            if constexpr (CK) {
+#pragma unroll
+                                for (int j = 0; j < PB; j += 4)
+                                    check_subnormal4(subl, acc[i][h + j], acc[i][h + j + 1],
+                                                     acc[i][h + j + 2], acc[i][h + j + 3], cls);
+                            }
                         }
                     }
                     // Emits nothing; ties the row's eight sums to this point of the stream.
@@ -460,6 +560,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
 #pragma unroll
                         for (int j = 0; j < 8; j++)
                             acc[i][j] = acc[i][j] + p[j];
+                        if constexpr (CK) {
+#pragma unroll
+                            for (int j = 0; j < 8; j += 4)
+                                check_subnormal4(subl, acc[i][j], acc[i][j + 1], acc[i][j + 2],
+                                                 acc[i][j + 3], cls);
+                        }
                     }
                 }
             }
@@ -474,19 +580,22 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             stage.stash(As[0], Bs[0], tid);
         }
         __syncthreads();
-        for (int kt = 0; kt < ktiles; kt++) {
-            const int cur = kt & 1;
-            if (kt + 1 < ktiles) {
-                if (WHOLE)
-                    stage.fetch_whole();
-                else
-                    stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+        auto run = [&](auto ck) {
+            for (int kt = 0; kt < ktiles; kt++) {
+                const int cur = kt & 1;
+                if (kt + 1 < ktiles) {
+                    if (WHOLE)
+                        stage.fetch_whole();
+                    else
+                        stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+                }
+                compute(As[cur], Bs[cur], ck);
+                if (kt + 1 < ktiles)
+                    stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
+                __syncthreads();
             }
-            compute(As[cur], Bs[cur]);
-            if (kt + 1 < ktiles)
-                stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
-            __syncthreads();
-        }
+        };
+        run_form(run);
     } else {
         // Wave w moves k rows w, w + 4, w + 8 and w + 12 of each directly loaded operand; lane
         // l's 16 bytes are the row's columns 2 l and 2 l + 1.
@@ -518,7 +627,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
         wait_lds_loads();
         __syncthreads();
         // Two slabs per trip: stage 0 holds even slabs, stage 1 odd ones.
-        auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+        auto slab = [&](auto cur_c, int kt, auto ck) __attribute__((always_inline)) {
             constexpr int cur = decltype(cur_c)::value;
             T (*Ac)[Cfg::LDA] = cur ? A1 : A0;
             T (*Bc)[Cfg::LDB] = cur ? B1 : B0;
@@ -526,20 +635,24 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             T (*Bn)[Cfg::LDB] = cur ? B0 : B1;
             if (kt + 1 < ktiles)
                 load(An, Bn);
-            compute(Ac, Bc);
+            compute(Ac, Bc, ck);
             if (kt + 1 < ktiles)
                 stash(An);
             wait_lds_loads();
             __syncthreads();
         };
-        for (int kt = 0; kt < ktiles; kt += 2) {
-            slab(std::integral_constant<int, 0>{}, kt);
-            if (kt + 1 < ktiles)
-                slab(std::integral_constant<int, 1>{}, kt + 1);
-        }
+        auto run = [&](auto ck) {
+            for (int kt = 0; kt < ktiles; kt += 2) {
+                slab(std::integral_constant<int, 0>{}, kt, ck);
+                if (kt + 1 < ktiles)
+                    slab(std::integral_constant<int, 1>{}, kt + 1, ck);
+            }
+        };
+        run_form(run);
     }
 
     // Epilogue: publish the tile and find the first suspect cell of this lane.
+    const bool sub = CHECK && ((subl.flush() >> (threadIdx.x & 63)) & 1);
     uint64_t key = kNoFault;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -568,9 +681,11 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                 int c = c0 + j;
                 if (NATIVE || c >= N)
                     continue;
-                bool bad = !finite_bits(acc[i][h * RUN + j]);
+                bool bad = !finite_bits(acc[i][h * RUN + j]) || sub;
                 if (check_risk)
                     bad |= rexp + exp_of(col_exp[c]) < thr;
+                if (sub)
+                    flag_sum_block(sck, r, c);
                 if (bad) {
                     uint64_t cell = (uint64_t)r * N + c;
                     key = cell < key ? cell : key;
@@ -734,7 +849,6 @@ __global__ __launch_bounds__(256, 3) void k_strict_gemm_f64n(
 // every k slab whose smallest A exponent and smallest B exponent (over the tile's rows and
 // columns) do.
 typedef short s16x2 __attribute__((ext_vector_type(2)));
-constexpr short kScanExpNone = 16000; // exponent of zero and non-finite operands
 
 template <typename T> __device__ __forceinline__ short scan_exp(T x)
 {
@@ -752,12 +866,20 @@ template <typename T> struct ScanCfg {
     template <bool TA> static constexpr bool kSplitRunsB = false;
 };
 
+// Superslab tables (when the screen filled them): op(A) rows and op(B) columns, entry-major
+// (x_major: tbl[x * nss + s]) or superslab-major (tbl[s * extent + x]).
+struct ScanTables {
+    const short *a = nullptr, *b = nullptr;
+    int a_xmajor = 0, b_xmajor = 0;
+};
+constexpr int kScanMaxSuperSlabs = 1024;
+
 template <typename T, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
     const T *__restrict__ A, const T *__restrict__ B, int M, int N, int K,
     const unsigned long long *__restrict__ row_exp, const unsigned long long *__restrict__ col_exp,
     int thr, const unsigned long long *suspect, unsigned long long *row_flag,
-    unsigned long long *flag_first, uint32_t gen, NodeGate gate)
+    unsigned long long *flag_first, uint32_t gen, ScanTables tb, NodeGate gate)
 {
     // No cell marked: nothing to scan (the same word for every thread). Most launches end
     // here, before the gate's block-wide read and its barrier.
@@ -772,32 +894,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
     constexpr int LA = BM + 8, LB = BN + 8;
     __shared__ __align__(16) short Ae[2][BK][LA];
     __shared__ __align__(16) short Be[2][BK][LB];
-    __shared__ int tile_min[2];
     __shared__ int slab_min[2][2][4]; // stage, operand, wave
+    __shared__ int ss_min[2][kScanMaxSuperSlabs]; // operand, superslab: the tile's minima
 
     const int tid = threadIdx.x;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    // The grid holds at most two workgroups a CU (all that fit at once); each takes tiles in
+    // turn, so an empty launch dispatches no more workgroups than that.
+    for (uint32_t t = blockIdx.x; t < (uint32_t)(tiles_m * tiles_n); t += gridDim.x) {
     int tile_m, tile_n;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
+    tile_of(t, tiles_m, tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    // Smallest row exponent of the tile's rows (wave 0) and column exponent of its columns
-    // (wave 1): the tile holds a marked cell only if their sum is below the threshold.
-    if (tid < 128) {
-        const int base = tid < 64 ? m0 : n0, lim = tid < 64 ? M : N, l = tid & 63;
-        const unsigned long long *w = tid < 64 ? row_exp : col_exp;
-        int e = kExpNone;
-        for (int i = l; i < BM; i += 64)
-            if (base + i < lim) {
-                const int x = exp_of(w[base + i]);
-                e = x < e ? x : e;
-            }
-        e = wave_min_i32(e);
-        if (l == 0)
-            tile_min[tid >> 6] = e;
-    }
-    __syncthreads();
-    if (tile_min[0] + tile_min[1] >= thr)
-        return;
+    // The tile holds a marked cell only if its smallest row exponent plus smallest column
+    // exponent is below the threshold.
+    const bool marked = tile_exp_sum_below<BM, BN>(row_exp, col_exp, m0, n0, M, N, thr);
+    if (marked) {
 
     const int tx = tid % 16, ty = tid / 16;
     s16x2 mn[8][4]; // row i, columns 2 jp and 2 jp + 1
@@ -854,15 +965,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
         }
     };
     const int ktiles = (K + BK - 1) / BK;
-    if (ktiles > 0) {
-        stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
-        stash(0);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles)
-            stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+    // One slab's (min, +) from stage `cur`, when its smallest A and B exponents allow a sum
+    // below the threshold.
+    auto scan_slab = [&](int cur) __attribute__((always_inline)) {
         int amin = slab_min[cur][0][0], bmin = slab_min[cur][1][0];
 #pragma unroll
         for (int w = 1; w < 4; w++) {
@@ -894,9 +999,60 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (kt + 1 < ktiles)
-            stash(cur ^ 1);
+    };
+    if (tb.a) {
+        // The tile's smallest exponent per superslab of op(A) rows and op(B) columns, from the
+        // tables; only superslabs whose two minima sum below the threshold are read.
+        constexpr int SS = (int)(kSuperSlab / BK);
+        const int nss = (K + (int)kSuperSlab - 1) / (int)kSuperSlab;
+        for (int i = tid; i < nss; i += 256) {
+            ss_min[0][i] = kScanExpNone;
+            ss_min[1][i] = kScanExpNone;
+        }
         __syncthreads();
+        const int x = tid & 127, half = tid >> 7, lane = tid & 63;
+        const bool ain = m0 + x < M, bin = n0 + x < N;
+        for (int ss = half; ss < nss; ss += 2) {
+            int ea = kScanExpNone, eb = kScanExpNone;
+            if (ain)
+                ea = tb.a_xmajor ? tb.a[(size_t)(m0 + x) * nss + ss] : tb.a[(size_t)ss * M + m0 + x];
+            if (bin)
+                eb = tb.b_xmajor ? tb.b[(size_t)(n0 + x) * nss + ss] : tb.b[(size_t)ss * N + n0 + x];
+            ea = wave_min_i32(ea);
+            eb = wave_min_i32(eb);
+            if (lane == 0) {
+                atomicMin(&ss_min[0][ss], ea);
+                atomicMin(&ss_min[1][ss], eb);
+            }
+        }
+        __syncthreads();
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int ss = kt / SS;
+            if (ss_min[0][ss] + ss_min[1][ss] >= thr) {
+                kt = SS * ss + SS - 1; // no product of the superslab sums below the threshold
+                continue;
+            }
+            stage.fetch(A, B, M, N, K, m0, n0, kt * BK, tid);
+            stash(0);
+            __syncthreads();
+            scan_slab(0);
+            __syncthreads();
+        }
+    } else {
+        if (ktiles > 0) {
+            stage.fetch(A, B, M, N, K, m0, n0, 0, tid);
+            stash(0);
+        }
+        __syncthreads();
+        for (int kt = 0; kt < ktiles; kt++) {
+            const int cur = kt & 1;
+            if (kt + 1 < ktiles)
+                stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+            scan_slab(cur);
+            if (kt + 1 < ktiles)
+                stash(cur ^ 1);
+            __syncthreads();
+        }
     }
     // Past the edges the operands stage as +0 (exponent 16000): those cells never flag.
 #pragma unroll
@@ -914,6 +1070,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
             atomicMax(&row_flag[r], ((unsigned long long)gen << 32) | (0xffffffffu - first));
             atomicMin(flag_first, (unsigned long long)r);
         }
+    }
+    } // marked
+    __syncthreads(); // the next tile reuses the tile-minimum words and the stages
     }
 }
 
@@ -1023,19 +1182,26 @@ __device__ __forceinline__ uint64_t wave_uniform_u64(uint64_t v)
 // it finds with atomicMin and stopping once that lies before the cells it has left. Every
 // loop is bounded, and each wave's branches are uniform, so each ballot sees its 64 lanes.
 //  1. Blocks of 64 cells in row-major order from the first suspect cell: the lanes screen
-//     the block's cells at once, and the wave takes its candidates in order (a non-finite
-//     result, and under RejectSubnormal, where a subnormal partial sum faults too, every
-//     cell the exponent screen marks) with the products and the ordered sums.
-//  2. Tiny (IEEE, after k_gemm_tiny_scan): rows in order from the first flagged row, each
-//     from its first flagged column. For a finite cell the first fault is the lowest k whose
-//     product is tiny and inexact, so only the products are classified.
+//     the block's cells at once, and the wave takes its candidates in order with the
+//     products and the ordered sums. Candidates: a non-finite result; under RejectSubnormal
+//     (where a subnormal partial sum faults too) a cell whose row and column exponents sum
+//     below `thr` and whose 32 x 32 block the tile kernel flagged (`sum_flag`: a partial
+//     sum in the block came out subnormal), or, when the tile kernel did not check its
+//     sums (`serial_screen`), every such cell.
+//  2. Tiny (after k_gemm_tiny_scan): rows in order from the first flagged row, each from its
+//     first flagged column, skipping cells whose exponents rule out a product below
+//     2^tiny_thr. For a finite cell whose partial sums are not subnormal the first fault is
+//     the lowest k whose product is tiny (under IEEE: and inexact), so only the products are
+//     classified; a cell with a subnormal partial sum is also a pass-1 candidate, whose walk
+//     finds the earlier of the two.
 template <typename T>
-__global__ __launch_bounds__(256) void k_strict_gemm_replay(
+__global__ __launch_bounds__(1024) void k_strict_gemm_replay(
     const T *__restrict__ A, const T *__restrict__ B, const T *__restrict__ C, uint64_t M,
     uint64_t N, uint64_t K, int ta, int tb, const unsigned long long *__restrict__ row_exp,
-    const unsigned long long *__restrict__ col_exp, int thr, int serial_screen, int tiny,
-    int policy, const unsigned long long *suspect, const unsigned long long *row_flag,
-    const unsigned long long *flag_first, uint32_t gen, unsigned long long *fault, NodeGate gate)
+    const unsigned long long *__restrict__ col_exp, int thr, int tiny_thr, int serial_screen,
+    int tiny, int policy, const unsigned long long *suspect, const unsigned long long *row_flag,
+    const unsigned long long *flag_first, const unsigned int *sum_flag, uint32_t flag_cols,
+    uint32_t gen, unsigned long long *fault, NodeGate gate)
 {
     // No suspect cell: nothing to replay, whatever the gate says. Most launches end here,
     // before the gate's block-wide read and its barrier.
@@ -1079,8 +1245,13 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
         bool cand = false;
         if (cell < cells) {
             cand = !finite_bits(C[cell]);
-            if (serial_screen)
-                cand |= exp_of(row_exp[cell / N]) + exp_of(col_exp[cell % N]) < thr;
+            if (serial_screen || sum_flag) {
+                const uint64_t r = cell / N, c = cell % N;
+                bool marked = exp_of(row_exp[r]) + exp_of(col_exp[c]) < thr;
+                if (sum_flag)
+                    marked = marked && sum_flag[(r >> 5) * flag_cols + (c >> 5)] == gen;
+                cand |= marked;
+            }
         }
         uint64_t mask = __ballot(cand);
         while (mask) {
@@ -1105,11 +1276,15 @@ __global__ __launch_bounds__(256) void k_strict_gemm_replay(
         const unsigned long long w = wave_uniform_u64(row_flag[r]);
         if ((uint32_t)(w >> 32) != gen)
             continue; // no cell of this row was flagged by this MatMul's scan
+        const int rexp = exp_of(row_exp[r]);
         bool done = false;
         for (uint64_t c = 0xffffffffu - (uint32_t)w; c < N && !done; c++) {
             const uint64_t cell = r * N + c;
             if (best_cell() < cell)
                 return; // rows only grow: this wave has nothing earlier left
+            // Every product of the cell is at least 2^(rexp + colexp): none is tiny.
+            if (rexp + exp_of(col_exp[c]) >= tiny_thr)
+                continue;
             if (!finite_bits(C[cell]))
                 continue; // the first pass took it
             const uint64_t f = cell_first_fault(A, B, M, N, K, ta, tb, cell, policy, false);
@@ -1254,11 +1429,29 @@ __global__ __launch_bounds__(256) void k_strict_gemm_fused(
 
 // ================================================================= launchers
 
-size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols)
+static size_t sum_flag_bytes(uint64_t rows, uint64_t cols)
+{
+    return (((rows + 31) / 32) * ((cols + 31) / 32) * sizeof(unsigned int) + 255) & ~(size_t)255;
+}
+
+// The superslab tables, when they take at most 32 MiB and K spans at most 1024 superslabs
+// (the tiny scan's per-tile list); 0 otherwise. They live in a buffer of their own: in the
+// MatMul scratch, a later call of another shape could find their bits where it keeps
+// generation-tagged words folded with atomicMax, and such bits may outrank its generation.
+size_t slab_table_bytes(uint64_t rows, uint64_t inner, uint64_t cols)
+{
+    const uint64_t nss = (inner + kSuperSlab - 1) / kSuperSlab;
+    const uint64_t bytes = (rows + cols) * nss * sizeof(short);
+    if (nss == 0 || nss > 1024 || bytes > (32ull << 20))
+        return 0;
+    return ((size_t)bytes + 255) & ~(size_t)255;
+}
+
+size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols, bool sum_flags)
 {
     size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
     size_t c = ((cols * sizeof(unsigned long long)) + 255) & ~(size_t)255;
-    return r + c + r + 256;
+    return r + c + r + 256 + (sum_flags ? sum_flag_bytes(rows, cols) : 0);
 }
 
 // The two words reset to kNoFault (first suspect cell, first flagged row) sit in a fixed
@@ -1266,7 +1459,8 @@ size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols)
 // exponents, row flags) after it. Calls of different shapes reuse one buffer, so a word of
 // one call can lie where another call keeps a different word; kNoFault (all ones) would
 // outrank every later word under atomicMax, so it must never lie in the tagged part.
-MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols)
+MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols, bool sum_flags,
+                                   void *tables, uint64_t inner)
 {
     char *p = (char *)base;
     size_t r = ((rows * sizeof(unsigned long long)) + 255) & ~(size_t)255;
@@ -1277,6 +1471,19 @@ MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols)
     s.row_exp = (unsigned long long *)(p + 256);
     s.col_exp = (unsigned long long *)(p + 256 + r);
     s.row_flag = (unsigned long long *)(p + 256 + r + c);
+    if (sum_flags) {
+        // Tagged with the generation like the exponent words: a word of an earlier call never
+        // equals this call's generation, and a pair of them read as one 64-bit word there
+        // carries an earlier generation.
+        s.sum_flag = (unsigned int *)(p + 256 + r + c + r);
+        s.flag_cols = (uint32_t)((cols + 31) / 32);
+    }
+    if (tables) {
+        // Rewritten whole by every screen that fills them.
+        const uint64_t nss = (inner + kSuperSlab - 1) / kSuperSlab;
+        s.tbl_a = (short *)tables;
+        s.tbl_b = s.tbl_a + rows * nss;
+    }
     return s;
 }
 
@@ -1398,38 +1605,39 @@ static void prefilter(hipStream_t s, ExpJob<T> ja, ExpJob<T> jb, uint32_t gen,
 template <typename T, bool TA, bool TB>
 static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C, int M, int N,
                           int K, const unsigned long long *re, const unsigned long long *ce,
-                          int thr, int risk, unsigned long long *suspect, NodeGate gate)
+                          int thr, int risk, unsigned long long *suspect, SumCheck sck,
+                          NodeGate gate)
 {
     bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     int vc = (N % 4 == 0) && aligned16(C);
     using Cfg = ValuCfg<T>;
     if (va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); }
     else if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, true, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); }
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, true, false, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); }
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, true, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); }
     else
-        hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm<T, TA, TB, false, false, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, re, ce, thr, risk, vc, suspect, sck, gate); }
 }
 
 template <typename T, bool TA, bool TB>
 static void tiny_scan_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, int M, int N,
-                               int K, const MatmulScratch &sc, int thr, NodeGate gate)
+                               int K, const MatmulScratch &sc, int thr, ScanTables tb, NodeGate gate)
 {
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     if (va && vb)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
     else if (va)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
     else
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
 }
 
 template <bool TA, bool TB>
@@ -1462,13 +1670,24 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
 {
     if (M == 0 || N == 0)
         return hipSuccess;
-    // Smallest exponent sum of a product that needs no replay (see pcu_device.hpp):
-    // IEEE: a product >= 2^-126 (2^-1022) is never tiny; RejectSubnormal: products
-    // >= 2^-103 (2^-970) are multiples of the smallest normal, so no partial sum is
-    // subnormal; AllowGradual: underflow is never a fault.
+    // Smallest exponent sums that need no replay: a product >= 2^-126 (2^-1022) is never
+    // tiny (tiny_thr); products >= 2^-103 (2^-970) are multiples of the smallest normal, and
+    // rounded sums of such multiples stay multiples, so no partial sum of a cell that meets
+    // no smaller product is a nonzero subnormal (sub_thr, RejectSubnormal). AllowGradual:
+    // underflow is never a fault.
     const bool f32 = sizeof(T) == 4;
+    const int tiny_thr = f32 ? -126 : -1022, sub_thr = f32 ? -103 : -970;
+    const bool reject = policy == kPolicyRejectSubnormal;
     int risk = policy != kPolicyAllowGradual;
-    int thr = policy == kPolicyRejectSubnormal ? (f32 ? -103 : -970) : (f32 ? -126 : -1022);
+    // Under RejectSubnormal the tile kernels check the partial sums of every tile that may
+    // meet a product below 2^sub_thr (all but the narrow binary64 tile, when the scratch has
+    // the block words); a cell is then suspect only for a non-finite result, a possibly tiny
+    // product or a subnormal partial sum in its lane. Without the check every cell the
+    // exponents put below sub_thr is suspect and walked in full.
+    const uint64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const bool sum_check = reject && K > 0 && sc.sum_flag != nullptr && (f32 || tiles >= 256);
+    int thr = reject && !sum_check ? sub_thr : tiny_thr;
+    const SumCheck sck = sum_check ? SumCheck{sc.sum_flag, sc.gen, sc.flag_cols, sub_thr} : SumCheck{};
     if (ev)
         (void)hipEventRecord(ev[0], s);
     if (engine == kEngineAuto && K > 0 && M * N <= fused_cells<T>()) {
@@ -1479,21 +1698,34 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
             (void)hipEventRecord(ev[1], s);
         const dim3 grid((unsigned)(((M + 15) / 16) * ((N + 15) / 16)));
         const int m = (int)M, n = (int)N, k = (int)K;
-        if (!ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, thr, risk, policy, fault, gate);
-        else if (!ta && tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, thr, risk, policy, fault, gate);
-        else if (ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, true, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, thr, risk, policy, fault, gate);
-        else hipLaunchKernelGGL((k_strict_gemm_fused<T, true, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, thr, risk, policy, fault, gate);
+        // The fused kernel walks every cell its exponents mark (no partial-sum check).
+        const int fthr = reject ? sub_thr : tiny_thr;
+        if (!ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
+        else if (!ta && tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
+        else if (ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, true, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
+        else hipLaunchKernelGGL((k_strict_gemm_fused<T, true, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
         if (ev) {
             (void)hipEventRecord(ev[2], s);
             (void)hipEventRecord(ev[3], s);
         }
         return hipGetLastError();
     }
+    // The superslab tables let the tiny scan read only the runs of k where a product below
+    // 2^tiny_thr is possible; the screen fills them under RejectSubnormal (where the scan runs
+    // whenever a tile is marked).
+    const bool tables = sum_check && sc.tbl_a != nullptr;
+    ScanTables tbls;
+    if (tables) {
+        tbls.a = sc.tbl_a;
+        tbls.b = sc.tbl_b;
+        tbls.a_xmajor = !ta; // a rows job over A (M x K), else a columns job over A (K x M)
+        tbls.b_xmajor = tb;  // a rows job over B (N x K), else a columns job over B (K x N)
+    }
     if (risk && K > 0) {
         // op(A) row r is stored row r (A is M x K) or stored column r (A is K x M); op(B)
         // column c is stored column c (B is K x N) or stored row c (B is N x K).
-        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp};
-        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp};
+        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp, tables ? sc.tbl_a : nullptr};
+        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp, tables ? sc.tbl_b : nullptr};
         prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate, open);
     } else {
         risk = 0; // AllowGradual, or an empty reduction: no underflow screen
@@ -1516,7 +1748,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
             tbt = false;
         }
         (void)launch_gemm_mfma_f32(s, m, n, k, ta, tbt, (const float *)A, Bt, (float *)C,
-                                   sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+                                   sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
     } else if (!f32 && (uint64_t)grid.x < 256) {
         const double *dA = (const double *)A, *dB = (const double *)B;
         double *dC = (double *)C;
@@ -1535,32 +1767,36 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
             Bk = (const T *)sc.bt;
             tbk = false;
         }
-        if (!ta && !tbk) gemm_dispatch<T, false, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-        else if (!ta && tbk) gemm_dispatch<T, false, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-        else if (ta && !tbk) gemm_dispatch<T, true, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
-        else gemm_dispatch<T, true, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, gate);
+        if (!ta && !tbk) gemm_dispatch<T, false, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
+        else if (!ta && tbk) gemm_dispatch<T, false, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
+        else if (ta && !tbk) gemm_dispatch<T, true, false>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
+        else gemm_dispatch<T, true, true>(s, grid, A, Bk, C, m, n, k, sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     if (ev)
         (void)hipEventRecord(ev[2], s);
-    // Under the IEEE policy a finite cell's first fault is a tiny-inexact product: the tiled
-    // scan narrows the screen's marks to the cells that have one, for the wave-parallel pass.
-    // Under RejectSubnormal a subnormal partial sum also faults, so the serial pass walks
-    // every marked cell.
-    const bool tiny = risk && policy == kPolicyIeee;
+    // A finite cell whose partial sums are not subnormal can first fault only in a tiny
+    // product: the tiled scan narrows the screen's marks to the cells that may have one, for
+    // the wave-parallel pass (IEEE, and RejectSubnormal when the tile kernel checked the
+    // sums). Otherwise the serial pass walks every marked cell.
+    const bool tiny = risk && (policy == kPolicyIeee || sum_check);
     if (tiny) {
-        if (!ta && !tb) tiny_scan_dispatch<T, false, false>(s, grid, A, B, m, n, k, sc, thr, gate);
-        else if (!ta && tb) tiny_scan_dispatch<T, false, true>(s, grid, A, B, m, n, k, sc, thr, gate);
-        else if (ta && !tb) tiny_scan_dispatch<T, true, false>(s, grid, A, B, m, n, k, sc, thr, gate);
-        else tiny_scan_dispatch<T, true, true>(s, grid, A, B, m, n, k, sc, thr, gate);
+        const dim3 sgrid(grid.x < 2u * kGfx950Cus ? grid.x : 2u * kGfx950Cus);
+        if (!ta && !tb) tiny_scan_dispatch<T, false, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
+        else if (!ta && tb) tiny_scan_dispatch<T, false, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
+        else if (ta && !tb) tiny_scan_dispatch<T, true, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
+        else tiny_scan_dispatch<T, true, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
     }
     const int serial_screen = risk && !tiny;
-    hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(1024), dim3(256), 0, s, A, B, (const T *)C, M, N, K,
-                       (int)ta, (int)tb, sc.row_exp, sc.col_exp, thr, serial_screen, (int)tiny, policy,
-                       (const unsigned long long *)sc.suspect, (const unsigned long long *)sc.row_flag,
-                       (const unsigned long long *)sc.flag_first, sc.gen, fault, gate);
+    // 4096 waves in 256 workgroups: an empty launch (no suspect cell) dispatches a quarter of
+    // the workgroups that 256-thread blocks would take.
+    hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(256), dim3(1024), 0, s, A, B, (const T *)C, M, N, K,
+                       (int)ta, (int)tb, sc.row_exp, sc.col_exp, reject ? sub_thr : tiny_thr, tiny_thr,
+                       serial_screen, (int)tiny, policy, (const unsigned long long *)sc.suspect,
+                       (const unsigned long long *)sc.row_flag, (const unsigned long long *)sc.flag_first,
+                       (const unsigned int *)sck.flag, sc.flag_cols, sc.gen, fault, gate);
     if (ev)
         (void)hipEventRecord(ev[3], s);
     return hipGetLastError();
@@ -1575,15 +1811,15 @@ static void native_f64_dispatch(hipStream_t s, dim3 grid, const double *A, const
     const int vc = (N % 4 == 0) && aligned16(C);
     using Cfg = ValuCfg<double>;
     if (va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, SumCheck{}, gate);
     else if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, SumCheck{}, gate);
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, true, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, SumCheck{}, gate);
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, SumCheck{}, gate);
     else
-        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, gate);
+        hipLaunchKernelGGL((k_strict_gemm<double, TA, TB, false, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, nullptr, nullptr, 0, 0, vc, nullptr, SumCheck{}, gate);
 }
 
 hipError_t launch_native_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,

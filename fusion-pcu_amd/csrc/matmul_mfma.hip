@@ -70,12 +70,14 @@ template <int N> __device__ __forceinline__ void wait_loads_but()
 
 // WHOLE: every slab of every tile is whole (M, N, K multiples of the tile and slab, 16-byte
 // loads allowed), so staging runs on advancing pointers with no bound checks.
-template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false>
+// CHECK: the RejectSubnormal form with the partial-sum check (sck), its own instantiation so
+// that the plain form keeps its registers and schedule.
+template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false, bool CHECK = false>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const unsigned long long *__restrict__ row_exp,
     const unsigned long long *__restrict__ col_exp, int thr, int check_risk,
-    unsigned long long *suspect, NodeGate gate)
+    unsigned long long *suspect, SumCheck sck, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -104,6 +106,16 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    // RejectSubnormal with the partial-sum check (sck.flag set) launches both forms over the
+    // whole grid: a tile that may meet a product below 2^sck.thr is computed by the CHECK form,
+    // which checks every partial sum it forms, and every other tile by the plain form. (One
+    // kernel holding both loops spilled registers.)
+    if (sck.flag != nullptr &&
+        tile_exp_sum_below<BM, BN>(row_exp, col_exp, m0, n0, M, N, sck.thr) != CHECK)
+        return;
+    SubLanes subl; // lanes that met a nonzero subnormal partial sum
+    const int cls = kClassSubnormal;
+    auto run_form = [&](auto &&run) { run(std::integral_constant<bool, CHECK>{}); };
 
     float acc[S][16];
 #pragma unroll
@@ -137,15 +149,27 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     // Fold one MFMA's products into a subtile: each cell adds its k product (register r),
     // then its k+1 product (register 16 + r). The sixteen k sums go first, so no add waits
     // on the add just before it (measured 2-3% faster with a transposed operand).
-    auto fold = [&](float (&c)[16], const v32f &p) {
+    // The checking form tests each of the 32 sums for a nonzero subnormal as it is formed.
+    auto fold = [&](float (&c)[16], const v32f &p, auto ck) {
+        constexpr bool CK = decltype(ck)::value;
         if (kFoldPrio)
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[r];
+        if constexpr (CK) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 4)
+                check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[16 + r];
+        if constexpr (CK) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 4)
+                check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+        }
         // Emits nothing; ties the sixteen sums to this point of the instruction stream.
         asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
                      "+v"(c[6]), "+v"(c[7]), "+v"(c[8]), "+v"(c[9]), "+v"(c[10]), "+v"(c[11]),
@@ -288,7 +312,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         }
         // One slab computed from stage CUR; the loop below runs three slabs per trip, so every
         // stage index, and with it every LDS address, is fixed at compile time.
-        auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+        auto slab = [&](auto cur_c, int kt, auto ck) __attribute__((always_inline)) {
             constexpr int cur = decltype(cur_c)::value, nn = (cur + 2) % 3;
             const std::integral_constant<int, (cur + 1) % 3> nxt_c;
             const std::integral_constant<int, nn> nn_c;
@@ -305,12 +329,12 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 if constexpr (SN == 2) {
                     const v32f q = mma(oa[g], ob[g][SN - 1]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[0], p);
+                    fold(acc[0], p, ck);
                     __builtin_amdgcn_sched_barrier(0);
                     if (j + 1 < NP || has_next)
                         p = mma(oa[g1], ob[g1][0]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[SN - 1], q);
+                    fold(acc[SN - 1], q, ck);
                     __builtin_amdgcn_sched_barrier(0);
                 } else {
                     v32f q;
@@ -318,7 +342,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                     if (more)
                         q = mma(oa[g1], ob[g1][0]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[0], p);
+                    fold(acc[0], p, ck);
                     __builtin_amdgcn_sched_barrier(0);
                     if (more)
                         p = q;
@@ -329,13 +353,16 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             wait_lds_loads();
             __syncthreads();
         };
-        for (int kt = 0; kt < ktiles; kt += 3) {
-            slab(std::integral_constant<int, 0>{}, kt);
-            if (kt + 1 < ktiles)
-                slab(std::integral_constant<int, 1>{}, kt + 1);
-            if (kt + 2 < ktiles)
-                slab(std::integral_constant<int, 2>{}, kt + 2);
-        }
+        auto run = [&](auto ck) {
+            for (int kt = 0; kt < ktiles; kt += 3) {
+                slab(std::integral_constant<int, 0>{}, kt, ck);
+                if (kt + 1 < ktiles)
+                    slab(std::integral_constant<int, 1>{}, kt + 1, ck);
+                if (kt + 2 < ktiles)
+                    slab(std::integral_constant<int, 2>{}, kt + 2, ck);
+            }
+        };
+        run_form(run);
     } else {
         if (ktiles > 0) {
             if (WHOLE)
@@ -345,6 +372,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             stage.stash(As[0], Bs[0], tid);
         }
         __syncthreads();
+        auto run = [&](auto ck) {
         for (int kt = 0; kt < ktiles; kt++) {
             const int cur = kt & 1;
             if (kt + 1 < ktiles) {
@@ -378,12 +406,12 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                         rd(j + 1);
                     const v32f q = mma(oa[j][0], ob[j][SN - 1]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[0], p);
+                    fold(acc[0], p, ck);
                     __builtin_amdgcn_sched_barrier(0);
                     if (j + 1 < NP)
                         p = mma(oa[j + 1][0], ob[j + 1][0]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[SN - 1], q);
+                    fold(acc[SN - 1], q, ck);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
@@ -400,7 +428,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                     if (j + 1 < NP)
                         q = mma(oa[j + 1][0], ob[j + 1][0]);
                     __builtin_amdgcn_sched_barrier(0);
-                    fold(acc[0], p);
+                    fold(acc[0], p, ck);
                     __builtin_amdgcn_sched_barrier(0);
                     if (j + 1 < NP)
                         p = q;
@@ -410,22 +438,26 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
             __syncthreads();
         }
-
+        };
+        run_form(run);
     }
 
     // Epilogue: for subtile (i, j) the lane owns rows m0+wm+32i+8(r/4)+4*half+(r%4) of column
     // n0+wn+2col+j (three stages, two subtiles: both columns in one 8-byte store, every cell
     // inside M x N) or n0+wn+32j+col.
+    const bool sub = CHECK && ((subl.flush() >> lane) & 1);
     uint64_t key = kNoFault;
     if constexpr (kStages == 3 && SN == 1) {
         const int c = n0 + wn + col;
         const int cexp = check_risk ? exp_of(col_exp[c]) : 0;
+        if (sub) // the lane's cells: rows m0 + wm .. m0 + wm + 31 of column c
+            flag_sum_block(sck, m0 + wm, c);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
             const float v = acc[0][r];
             C[(size_t)row * N + c] = v;
-            bool bad = !finite_bits(v);
+            bool bad = !finite_bits(v) || sub;
             if (check_risk)
                 bad |= exp_of(row_exp[row]) + cexp < thr;
             const uint64_t cell = (uint64_t)row * N + c;
@@ -438,12 +470,14 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         const int c = n0 + wn + 2 * col;
         const int cexp0 = check_risk ? exp_of(col_exp[c]) : 0;
         const int cexp1 = check_risk ? exp_of(col_exp[c + 1]) : 0;
+        if (sub) // rows m0 + wm .. m0 + wm + 31 of columns c and c + 1 (c even): one block
+            flag_sum_block(sck, m0 + wm, c);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
             const float v0 = acc[0][r], v1 = acc[1][r];
             *reinterpret_cast<float2 *>(&C[(size_t)row * N + c]) = make_float2(v0, v1);
-            bool bad0 = !finite_bits(v0), bad1 = !finite_bits(v1);
+            bool bad0 = !finite_bits(v0) || sub, bad1 = !finite_bits(v1) || sub;
             if (check_risk) {
                 const int rexp = exp_of(row_exp[row]);
                 bad0 |= rexp + cexp0 < thr;
@@ -464,6 +498,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         const int c = n0 + wn + 32 * j + col;
         const bool cin = c < N;
         const int cexp = (check_risk && cin) ? exp_of(col_exp[c]) : 0;
+        if (sub && cin && m0 + wm + 32 * i < M) // subtile t: one 32 x 32 block
+            flag_sum_block(sck, m0 + wm + 32 * i, c);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -471,7 +507,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 continue;
             const float v = acc[t][r];
             C[(size_t)row * N + c] = v;
-            bool bad = !finite_bits(v);
+            bool bad = !finite_bits(v) || sub;
             if (check_risk)
                 bad |= exp_of(row_exp[row]) + cexp < thr;
             if (bad) {
@@ -500,12 +536,12 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
 //    columns each) meets 64 distinct banks.
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, bool CHECK = false>
 __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const unsigned long long *__restrict__ row_exp,
     const unsigned long long *__restrict__ col_exp, int thr, int check_risk,
-    unsigned long long *suspect, NodeGate gate)
+    unsigned long long *suspect, SumCheck sck, NodeGate gate)
 {
     if (block_gate_closed(gate))
         return;
@@ -526,6 +562,13 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
     int tm, tn;
     tile_of(blockIdx.x, M / T, N / T, tm, tn);
     const int m0 = tm * T, n0 = tn * T;
+    // RejectSubnormal with the partial-sum check: each form takes its own tiles, as in
+    // k_strict_gemm_mfma.
+    if (sck.flag != nullptr &&
+        tile_exp_sum_below<T, T>(row_exp, col_exp, m0, n0, M, N, sck.thr) != CHECK)
+        return;
+    SubLanes subl;
+    const int cls = kClassSubnormal;
 
     // Loads: waves 0-3 move op(A), waves 4-7 op(B), one 1 KiB instruction each a slab
     // (quad g or rows 4 g .. 4 g + 3 of the slab, g = wave % 4).
@@ -569,12 +612,16 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
         zero[r] = 0.0f;
     // Fold one MFMA's products: each cell q adds its k0, k0 + 1, k0 + 2, k0 + 3 products in
     // turn; the four cells' chains interleave.
-    auto fold = [&](const v16f &p) {
+    auto fold = [&](const v16f &p, auto ck) {
+        constexpr bool CK = decltype(ck)::value;
 #pragma unroll
-        for (int blk = 0; blk < 4; blk++)
+        for (int blk = 0; blk < 4; blk++) {
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 acc[q] = acc[q] + p[4 * blk + q];
+            if constexpr (CK)
+                check_subnormal4(subl, acc[0], acc[1], acc[2], acc[3], cls);
+        }
         asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
     };
     const int ktiles = K / BK;
@@ -585,7 +632,7 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
     }
     wait_lds_loads();
     __syncthreads();
-    auto slab = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+    auto slab = [&](auto cur_c, int kt, auto ck) __attribute__((always_inline)) {
         constexpr int cur = decltype(cur_c)::value;
         if (kt + 2 < ktiles)
             load_slab(std::integral_constant<int, (cur + 2) % 3>{});
@@ -603,7 +650,7 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
             if (q + 1 < 4)
                 nx = __builtin_amdgcn_mfma_f32_16x16x1f32(a[q + 1], bb[q + 1], zero, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            fold(p);
+            fold(p, ck);
             __builtin_amdgcn_sched_barrier(0);
             if (q + 1 < 4)
                 p = nx;
@@ -616,23 +663,29 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
             wait_lds_loads();
         __syncthreads();
     };
-    for (int kt = 0; kt < ktiles; kt += 3) {
-        slab(std::integral_constant<int, 0>{}, kt);
-        if (kt + 1 < ktiles)
-            slab(std::integral_constant<int, 1>{}, kt + 1);
-        if (kt + 2 < ktiles)
-            slab(std::integral_constant<int, 2>{}, kt + 2);
-    }
+    auto run = [&](auto ck) {
+        for (int kt = 0; kt < ktiles; kt += 3) {
+            slab(std::integral_constant<int, 0>{}, kt, ck);
+            if (kt + 1 < ktiles)
+                slab(std::integral_constant<int, 1>{}, kt + 1, ck);
+            if (kt + 2 < ktiles)
+                slab(std::integral_constant<int, 2>{}, kt + 2, ck);
+        }
+    };
+    run(std::integral_constant<bool, CHECK>{});
     // Epilogue: cells (m0 + wm + 4 (lane / 16) + q, n0 + wn + lane % 16).
+    const bool sub = CHECK && ((subl.flush() >> lane) & 1);
     uint64_t key = kNoFault;
     const int c = n0 + wn + i;
     const int cexp = check_risk ? exp_of(col_exp[c]) : 0;
+    if (sub) // rows m0 + wm .. m0 + wm + 15 of column c: one 32 x 32 block
+        flag_sum_block(sck, m0 + wm, c);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int row = m0 + wm + 4 * b + q;
         const float v = acc[q];
         C[(size_t)row * N + c] = v;
-        bool bad = !finite_bits(v);
+        bool bad = !finite_bits(v) || sub;
         if (check_risk)
             bad |= exp_of(row_exp[row]) + cexp < thr;
         const uint64_t cell = (uint64_t)row * N + c;
@@ -647,7 +700,8 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; 
 template <class Cfg, bool TA, bool TB>
 static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
                           int K, const unsigned long long *re, const unsigned long long *ce,
-                          int thr, int risk, unsigned long long *suspect, NodeGate gate)
+                          int thr, int risk, unsigned long long *suspect, SumCheck sck,
+                          NodeGate gate)
 {
     const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
     const dim3 block(Cfg::kThreads);
@@ -661,27 +715,27 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
                        ((uintptr_t)C & 7u) == 0 && offsets32;
     if (whole)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
     else if (va && vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
     else if (va)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
     else if (vb)
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
     else
-        hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
 }
 
 template <class Cfg>
 static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, const float *A,
                         const float *B, float *C, const unsigned long long *re,
                         const unsigned long long *ce, int thr,
-                        int risk, unsigned long long *suspect, NodeGate gate)
+                        int risk, unsigned long long *suspect, SumCheck sck, NodeGate gate)
 {
-    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
-    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, gate);
+    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
+    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
+    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
+    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
 }
 
 // 8 waves of 32 x 64 over a 128 x 128 tile, 123-126 VGPRs (4 waves per SIMD). On MI355X at
@@ -698,7 +752,7 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 const float *A, const float *B, float *C,
                                 const unsigned long long *row_exp,
                                 const unsigned long long *col_exp, int thr, int risk,
-                                unsigned long long *suspect, NodeGate gate)
+                                unsigned long long *suspect, SumCheck sck, NodeGate gate)
 {
     const uint64_t big_tiles = (uint64_t)((M + GemmCfg::BM - 1) / GemmCfg::BM) * ((N + GemmCfg::BN - 1) / GemmCfg::BN);
     // 16 x 16 waves: whole 64 x 64 tiles, 16-byte loads, lane offsets within 32 bits, and
@@ -713,16 +767,16 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                      fits32(tb ? 64 * ldb * 4 : (3 * ldb + 64) * 4);
     if (big_tiles < 256 && w16) {
         const dim3 grid((unsigned)((M / 64) * (N / 64)));
-        if (!ta && !tb) hipLaunchKernelGGL((k_strict_gemm_mfma16<false, false>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, gate);
-        else if (!ta && tb) hipLaunchKernelGGL((k_strict_gemm_mfma16<false, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, gate);
-        else if (ta && !tb) hipLaunchKernelGGL((k_strict_gemm_mfma16<true, false>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, gate);
-        else hipLaunchKernelGGL((k_strict_gemm_mfma16<true, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, gate);
+        if (!ta && !tb) { hipLaunchKernelGGL((k_strict_gemm_mfma16<false, false>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma16<false, false, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); }
+        else if (!ta && tb) { hipLaunchKernelGGL((k_strict_gemm_mfma16<false, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma16<false, true, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); }
+        else if (ta && !tb) { hipLaunchKernelGGL((k_strict_gemm_mfma16<true, false>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma16<true, false, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); }
+        else { hipLaunchKernelGGL((k_strict_gemm_mfma16<true, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma16<true, true, true>), grid, dim3(1024), 0, s, A, B, C, M, N, K, row_exp, col_exp, thr, risk, suspect, sck, gate); }
         return hipGetLastError();
     }
     if (big_tiles < 256)
-        mfma_launch<SmallCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
+        mfma_launch<SmallCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, sck, gate);
     else
-        mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, gate);
+        mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, sck, gate);
     return hipGetLastError();
 }
 

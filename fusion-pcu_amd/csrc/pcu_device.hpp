@@ -414,6 +414,139 @@ __device__ __forceinline__ unsigned long long exp_word(uint32_t gen, int e)
 }
 __device__ __forceinline__ int exp_of(unsigned long long w) { return kExpBias - (int)(uint32_t)w; }
 
+// The tile kernels' partial-sum check, one v_cmp_class per sum (class bits 4 and 7:
+// negative and positive subnormal) into a lane mask. Masks rotate through four slots: a check
+// first ORs into `flag` the mask its slot got four checks earlier (long since written), then
+// compares v into the slot, so no scalar OR waits on the compare just before it (a single
+// vcc chain ran the checked loop 2.6x slower). The asm keeps every compare beside its sum (v
+// is in-out, so the next sum of the cell waits for it): the compiler's own form batched the
+// compares and spilled. The slots are named (an indexed array of them was not kept in
+// scalar registers). s_or_b64 writes scc, which the asm declares (a loop branch on scc may
+// follow it). `cls` holds kClassSubnormal; flush() ORs the slots at the end.
+constexpr int kClassSubnormal = (1 << 4) | (1 << 7);
+struct SubLanes {
+    uint64_t flag = 0, s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    __device__ __forceinline__ uint64_t flush() const { return flag | s0 | s1 | s2 | s3; }
+};
+__device__ __forceinline__ void check_subnormal(uint64_t &flag, uint64_t &slot, float &v, int cls)
+{
+    asm volatile("s_or_b64 %0, %0, %1\n\tv_cmp_class_f32_e64 %1, %2, %3"
+                 : "+s"(flag), "+s"(slot), "+v"(v)
+                 : "v"(cls)
+                 : "scc");
+}
+__device__ __forceinline__ void check_subnormal(uint64_t &flag, uint64_t &slot, double &v, int cls)
+{
+    asm volatile("s_or_b64 %0, %0, %1\n\tv_cmp_class_f64_e64 %1, %2, %3"
+                 : "+s"(flag), "+s"(slot), "+v"(v)
+                 : "v"(cls)
+                 : "scc");
+}
+// Checks of four consecutive sums, one slot each.
+template <typename T>
+__device__ __forceinline__ void check_subnormal4(SubLanes &s, T &a, T &b, T &c, T &d, int cls)
+{
+    check_subnormal(s.flag, s.s0, a, cls);
+    check_subnormal(s.flag, s.s1, b, cls);
+    check_subnormal(s.flag, s.s2, c, cls);
+    check_subnormal(s.flag, s.s3, d, cls);
+}
+
+// Whether the smallest exponent over the tile's rows [m0, m0 + BM) of op(A) plus the
+// smallest over its columns [n0, n0 + BN) of op(B) lies below thr (zero and non-finite
+// operands count 2^20). Block-wide, with one barrier: every thread of a block of at least
+// 128 threads calls it and gets the same answer.
+template <int BM, int BN>
+__device__ __forceinline__ bool tile_exp_sum_below(const unsigned long long *row_exp,
+                                                   const unsigned long long *col_exp, int m0,
+                                                   int n0, int M, int N, int thr)
+{
+    __shared__ int tile_min[2];
+    const int tid = threadIdx.x;
+    if (tid < 128) {
+        const bool rows = tid < 64;
+        const int l = tid & 63, base = rows ? m0 : n0, lim = rows ? M : N, ext = rows ? BM : BN;
+        const unsigned long long *w = rows ? row_exp : col_exp;
+        int e = 1 << 20;
+        for (int i = l; i < ext; i += 64)
+            if (base + i < lim) {
+                const int x = exp_of(w[base + i]);
+                e = x < e ? x : e;
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const int o = __shfl_xor(e, off, 64);
+            e = o < e ? o : e;
+        }
+        if (l == 0)
+            tile_min[tid >> 6] = e;
+    }
+    __syncthreads();
+    // Uniform by construction; readfirstlane tells the compiler, so values that merge after a
+    // branch on it may stay in scalar registers.
+    return __builtin_amdgcn_readfirstlane(tile_min[0] + tile_min[1]) < thr;
+}
+
+// Which superslabs (64 k) of a checking tile need their partial sums checked: fine[s] = 1
+// when the smallest exponent of the tile's op(A) rows plus that of its op(B) columns over
+// superslab s, from the screen's tables, lies below sck.thr (a product there may be below
+// 2^thr, not a multiple of the smallest normal); all 1 without tables. Block-wide, one
+// barrier. K spans at most kSumMaxSuperSlabs superslabs when there are tables.
+constexpr int kSumMaxSuperSlabs = 1024;
+template <int BM, int BN>
+__device__ __forceinline__ void tile_fine_superslabs(const SumCheck &sck, int m0, int n0, int M,
+                                                     int N, int K, unsigned char *fine)
+{
+    const int nss = (K + 63) / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    for (int s = wave; s < nss; s += waves) {
+        int ea = 16000, eb = 16000; // zero and non-finite entries
+        if (sck.tbl_a) {
+            for (int i = lane; i < BM; i += 64)
+                if (m0 + i < M) {
+                    const int v = sck.a_xmajor ? sck.tbl_a[(size_t)(m0 + i) * nss + s]
+                                               : sck.tbl_a[(size_t)s * M + m0 + i];
+                    ea = v < ea ? v : ea;
+                }
+            for (int i = lane; i < BN; i += 64)
+                if (n0 + i < N) {
+                    const int v = sck.b_xmajor ? sck.tbl_b[(size_t)(n0 + i) * nss + s]
+                                               : sck.tbl_b[(size_t)s * N + n0 + i];
+                    eb = v < eb ? v : eb;
+                }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const int oa = __shfl_xor(ea, off, 64), ob = __shfl_xor(eb, off, 64);
+                ea = oa < ea ? oa : ea;
+                eb = ob < eb ? ob : eb;
+            }
+        } else {
+            ea = eb = -(1 << 20);
+        }
+        if (lane == 0)
+            fine[s] = ea + eb < sck.thr;
+    }
+    __syncthreads();
+}
+
+// A partial sum that a later sum could still carry to a nonzero subnormal: nonzero and below
+// 2^-102 (2^-969), so perhaps not a multiple of the smallest normal. A sum of zero, or of
+// at least that magnitude, is such a multiple, and sums of multiples stay multiples.
+__device__ __forceinline__ bool sum_may_go_subnormal(float v)
+{
+    return (bits_of(v) & 0x7fffffffu) - 1u < 0x0C7FFFFFu;
+}
+__device__ __forceinline__ bool sum_may_go_subnormal(double v)
+{
+    return (bits_of(v) & 0x7fffffffffffffffull) - 1ull < (54ull << 52) - 1ull;
+}
+
+// The partial-sum block word of output cell (row, col).
+__device__ __forceinline__ void flag_sum_block(const SumCheck &sck, int row, int col)
+{
+    sck.flag[(size_t)(row >> 5) * sck.blocks_n + (uint32_t)(col >> 5)] = sck.gen;
+}
+
 // Record the wave's earliest packed fault with one atomic. `key` is kNoFault on lanes
 // without a fault; the ballot keeps the fault-free path to one instruction. A fault word
 // (as opposed to a scratch word such as the MatMul's first suspect cell) also closes the

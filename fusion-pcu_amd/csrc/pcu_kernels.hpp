@@ -83,6 +83,32 @@ struct MatmulScratch {
     // K x N elements for a transposed op(B) copied out for the tile kernel, or null (the
     // tile kernel then reads B in place). See matmul_bt_wanted.
     void *bt = nullptr;
+    // One word per 32 x 32 block of output cells (flag_cols a block row), set to `gen` by a
+    // tile kernel when a partial sum of a cell in the block came out a nonzero subnormal
+    // (RejectSubnormal); null when the scratch carries none (the no-allocation call).
+    unsigned int *sum_flag = nullptr;
+    uint32_t flag_cols = 0;
+    // Superslab tables of op(A) rows and op(B) columns (the smallest exponent of each run of
+    // 64 k, int16), which let the tiny scan skip runs without reading the operands; null when
+    // the scratch carries none. The exponent screen fills them when asked.
+    short *tbl_a = nullptr, *tbl_b = nullptr;
+};
+
+// RejectSubnormal's partial-sum check in a tile kernel. A workgroup whose smallest row
+// exponent plus smallest column exponent lies below `thr` (so a product below 2^thr, one
+// that is not a multiple of the smallest normal, may occur) checks every partial sum it
+// forms for a nonzero subnormal; a lane that meets one marks its cells suspect and sets its
+// blocks' words to `gen`. flag == nullptr: no check.
+struct SumCheck {
+    unsigned int *flag = nullptr;
+    uint32_t gen = 0;
+    uint32_t blocks_n = 0; // words a block row
+    int thr = 0;
+    // The screen's superslab tables (see MatmulScratch) or null. With them a checking tile
+    // checks only the slabs of superslabs that may hold a product below 2^thr, and the slabs
+    // after them while a partial sum might still be subnormal later; without, every slab.
+    const short *tbl_a = nullptr, *tbl_b = nullptr;
+    int a_xmajor = 0, b_xmajor = 0;
 };
 // Whether a strict MatMul (F32 on the matrix-core engine, or F64) runs its tile kernel on a
 // copy of a transposed op(B) stored K x N (grids of whole 128 x 128 tiles, K a multiple of
@@ -90,8 +116,12 @@ struct MatmulScratch {
 // one through registers.
 bool matmul_bt_wanted(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, bool tl,
                       bool tr, int engine);
-size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols);
-MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols);
+// `sum_flags`: the scratch also carries the partial-sum block words. The superslab tables
+// take a buffer of their own of slab_table_bytes() bytes (0: too large, none), or none.
+size_t matmul_scratch_bytes(uint64_t rows, uint64_t cols, bool sum_flags);
+size_t slab_table_bytes(uint64_t rows, uint64_t inner, uint64_t cols);
+MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols, bool sum_flags,
+                                   void *tables, uint64_t inner);
 
 // Main-kernel engine of the strict F32 MatMul: products from the vector unit (v_mul_f32),
 // or from the matrix cores used as a K=1 multiplier array with a +0 accumulator (bit-equal
@@ -102,7 +132,7 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 const float *A, const float *B, float *C,
                                 const unsigned long long *row_exp,
                                 const unsigned long long *col_exp, int thr, int risk,
-                                unsigned long long *suspect, NodeGate gate);
+                                unsigned long long *suspect, SumCheck sck, NodeGate gate);
 
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
 // Every kernel of the op skips its work once `gate` shows that an earlier program node
@@ -145,6 +175,14 @@ hipError_t launch_native_mse(hipStream_t s, int dtype, uint64_t n, const void *p
 hipError_t launch_fill_u64(hipStream_t s, unsigned long long *p, uint64_t n, uint64_t value);
 hipError_t launch_fill_u32(hipStream_t s, unsigned int *p, uint64_t n, uint32_t value);
 // Program start: words[0, n) = value and *gate = 0xffffffff (open), in one launch.
+// Program end: host_words[0, n) = words[0, n), then words[0, n) = value and *gate =
+// 0xffffffff (the next program starts open), then *host_seq = seq, stored at system scope
+// after the copies, so a host that reads seq there may read the words. host_words and
+// host_seq are coherent pinned host memory. One launch of one workgroup.
+hipError_t launch_program_publish(hipStream_t s, unsigned long long *words, uint64_t n,
+                                  uint64_t value, unsigned int *gate,
+                                  unsigned long long *host_words, unsigned long long *host_seq,
+                                  uint64_t seq);
 hipError_t launch_program_open(hipStream_t s, unsigned long long *words, uint64_t n, uint64_t value,
                                unsigned int *gate);
 

@@ -46,10 +46,15 @@ struct Ctx {
     hipEvent_t staging_ev[2] = {nullptr, nullptr};
     hipEvent_t marks[16] = {};
     unsigned long long *fault_words = nullptr; // device, kMaxNodes words
-    unsigned long long *host_words = nullptr;  // pinned mirror
+    // Coherent pinned mirror of the fault words, then the sequence word the program-end
+    // kernel stores after copying them (see read_words).
+    unsigned long long *host_words = nullptr;
+    unsigned long long *host_seq = nullptr;
+    uint64_t pub_seq = 0;
     bool in_program = false;
     bool implicit_program = false;
-    bool words_pending = false;
+    bool words_pending = false; // the open program's words and gate await their reset
+    bool words_clean = false;   // the last program's end reset them for the next one
     pcu_fault held_fault{};      // first fault of the most recent program
     pcu_fault protocol_fault{};  // node and raw word of the last malformed fault status
     bool has_held_fault = false; // the open program's fault words and gate await their reset
@@ -96,7 +101,7 @@ struct Ctx {
         void *p = nullptr;
         size_t cap = 0;
     };
-    Scratch matmul_scratch, mse_scratch, bt_scratch;
+    Scratch matmul_scratch, mse_scratch, bt_scratch, table_scratch;
     uint32_t screen_gen = 0; // generation of the latest MatMul exponent screen
     // Buffers released by the caller are kept for reuse by an allocation of the same size
     // (a training step frees its previous weights and takes as many new ones of the same
@@ -114,6 +119,8 @@ struct Ctx {
     // buffers are released while the context's streams still exist).
     std::vector<Prepared *> prepared;
     pcu_status scratch(Scratch &buf, size_t bytes, bool side_reader, void **out);
+    // A buffer that only speeds a call up: nullptr (and no error) when it cannot be had.
+    void *optional_scratch(Scratch &buf, size_t bytes);
 
     pcu_status open_words();
     pcu_status begin_program(bool implicit);

@@ -21,7 +21,7 @@
 // pcu_strict_matmul_noalloc keeps the MatMul screen's words (one exponent word per row of
 // op(A) and per column of op(B), one flag word per output row, then the first-suspect and
 // first-flagged-row words) in this array instead of the context's pool, so that call
-// allocates nothing. Its size is matmul_scratch_bytes(rows, cols) at the largest admitted
+// allocates nothing. Its size is matmul_scratch_bytes(rows, cols, false) at the largest admitted
 // shape: three runs of 8 * 65536 bytes and 256 bytes, i.e. 1.5 MiB + 256 B, which each device
 // keeps until the process ends. In host code
 // `scratch` is a host-side stand-in: only the address hipGetSymbolAddress returns for the
@@ -128,9 +128,12 @@ pcu_status Ctx::open(int dev)
     // The fault words of a program's nodes, then its stage gate (one 32-bit word).
     if ((st = hip(hipMalloc(&fault_words, sizeof(unsigned long long) * (kMaxNodes + 1)), "hipMalloc")))
         return st;
-    if ((st = hip(hipHostMalloc((void **)&host_words, sizeof(unsigned long long) * kMaxNodes,
-                                hipHostMallocDefault), "hipHostMalloc")))
+    // Coherent: the program-end kernel stores into it directly (see read_words).
+    if ((st = hip(hipHostMalloc((void **)&host_words, sizeof(unsigned long long) * (kMaxNodes + 1),
+                                hipHostMallocCoherent), "hipHostMalloc")))
         return st;
+    host_seq = host_words + kMaxNodes;
+    *host_seq = 0;
     nodes.reserve(kMaxNodes); // adding a node never reallocates
     return hip(noalloc_setup(dev), "hipGetSymbolAddress(scratch)");
 }
@@ -146,7 +149,7 @@ Ctx::~Ctx()
         (void)hipStreamSynchronize(stream);
     if (side)
         (void)hipStreamSynchronize(side);
-    for (Scratch *b : {&matmul_scratch, &mse_scratch, &bt_scratch})
+    for (Scratch *b : {&matmul_scratch, &mse_scratch, &bt_scratch, &table_scratch})
         if (b->p)
             (void)hipFreeAsync(b->p, stream);
     for (const Released &r : reuse)
@@ -319,7 +322,9 @@ pcu_status Ctx::begin_program(bool implicit)
     in_program = true;
     implicit_program = implicit;
     nodes.clear();
-    words_pending = true;
+    // The previous program's end left the words reset and the gate open, unless it failed.
+    words_pending = !words_clean;
+    words_clean = false;
     return PCU_OK;
 }
 
@@ -422,15 +427,41 @@ pcu_status Ctx::read_words(size_t *used)
     if (st)
         return st;
     *used = nodes.size();
-    if (*used) {
-        // Nodes that launched nothing (empty shapes) still have their words read.
-        if ((st = open_words()))
-            return st;
-        if ((st = hip(hipMemcpyAsync(host_words, fault_words, *used * sizeof(unsigned long long),
-                                     hipMemcpyDeviceToHost, stream), "hipMemcpyAsync")))
-            return st;
+    if (!*used)
+        return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    // Nodes that launched nothing (empty shapes) still have their words read.
+    if ((st = open_words()))
+        return st;
+    // One kernel copies the words into the coherent mirror, resets them and the gate for the
+    // next program (which then needs no opening launch), and stores this program's sequence
+    // number last; the host spins on that word. Against a D2H copy and a stream
+    // synchronization this saves the copy command and the runtime's wake-up.
+    const uint64_t seq = ++pub_seq;
+    if ((st = hip(launch_program_publish(stream, fault_words, *used, kNoFaultWord, gate_word(),
+                                         host_words, host_seq, seq),
+                  "program publish")))
+        return st;
+    for (unsigned spin = 1;; spin++) {
+        if (__atomic_load_n(host_seq, __ATOMIC_ACQUIRE) == seq)
+            break;
+        if ((spin & 1023) == 0) {
+            // Now and then ask the runtime: an error ends the wait, and a stream that is done
+            // must have stored the word.
+            const hipError_t e = hipStreamQuery(stream);
+            if (e == hipErrorNotReady)
+                continue;
+            if (e != hipSuccess)
+                return hip(e, "hipStreamQuery");
+            if (__atomic_load_n(host_seq, __ATOMIC_ACQUIRE) != seq) {
+                fail("program end: the stream finished without storing its fault words");
+                return PCU_ERR_DEVICE;
+            }
+            break;
+        }
+        __builtin_ia32_pause();
     }
-    return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    words_clean = true;
+    return PCU_OK;
 }
 
 // Node i's word, read by read_words and holding a fault, as a decoded record.
@@ -544,6 +575,26 @@ pcu_status Ctx::scratch(Scratch &buf, size_t bytes, bool side_reader, void **out
     }
     *out = buf.p;
     return PCU_OK;
+}
+
+void *Ctx::optional_scratch(Scratch &buf, size_t bytes)
+{
+    if (bytes <= buf.cap)
+        return buf.p;
+    if (buf.p && hipFreeAsync(buf.p, stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr; // keep the old buffer: it is still owned here
+    }
+    buf.p = nullptr;
+    buf.cap = 0;
+    if (hipMallocFromPoolAsync(&buf.p, bytes, pool, stream) != hipSuccess) {
+        // Clear the runtime's last error, which the next launch check would otherwise read.
+        (void)hipGetLastError();
+        buf.p = nullptr;
+        return nullptr;
+    }
+    buf.cap = bytes;
+    return buf.p;
 }
 
 // ------------------------------------------------------------------ timing
@@ -689,7 +740,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         gen = ++d.gen;
     } else {
         const Scratch old = matmul_scratch;
-        if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols), false, &sc)))
+        if ((st = scratch(matmul_scratch, matmul_scratch_bytes(rows, cols, true), false, &sc)))
             return st;
         if (matmul_scratch.p != old.p || matmul_scratch.cap != old.cap || screen_gen == UINT32_MAX) {
             clear_words = matmul_scratch.cap / 8;
@@ -697,16 +748,23 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         }
         gen = ++screen_gen;
     }
-    MatmulScratch s = matmul_scratch_carve(sc, rows, cols);
+    // The fixed array has no partial-sum block words and no superslab tables: under
+    // RejectSubnormal the no-allocation call walks every cell its exponents mark. The tables
+    // only speed the tiny scan up, so a table buffer that cannot be had is left out.
+    void *tables = nullptr;
+    if (!noalloc && policy == PCU_UNDERFLOW_REJECT_SUBNORMAL) {
+        const size_t tb = slab_table_bytes(rows, inner, cols);
+        if (tb)
+            tables = optional_scratch(table_scratch, tb);
+    }
+    MatmulScratch s = matmul_scratch_carve(sc, rows, cols, !noalloc, tables, inner);
     s.gen = gen;
     // The copy of a transposed op(B) for the tile kernel; the no-allocation call reads B in
     // place.
-    if (!noalloc && matmul_bt_wanted(dtype, rows, inner, cols, tl != 0, tr != 0, matmul_engine)) {
-        void *bt = nullptr;
-        if ((st = scratch(bt_scratch, (size_t)(inner * cols * dsize(dtype)), false, &bt)))
-            return st;
-        s.bt = bt;
-    }
+    // The copy is only a speed-up: when it cannot be allocated the tile kernel reads B in
+    // place, as for every other layout.
+    if (!noalloc && matmul_bt_wanted(dtype, rows, inner, cols, tl != 0, tr != 0, matmul_engine))
+        s.bt = optional_scratch(bt_scratch, (size_t)(inner * cols * dsize(dtype)));
 
     // Per-kernel timing takes events from a pool that may grow, so the no-allocation call
     // is never timed.

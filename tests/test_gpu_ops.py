@@ -815,6 +815,77 @@ def test_output_overlapping_an_operand_is_rejected(ctx, pcu_pkg):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_in_place_calls_report_the_oracles_first_fault(ctx, pcu_pkg, dtype):
+    """Every in-place form (out equal to an operand) with planted faults of several kinds.
+    The kernels store a whole vector before they classify its flagged lanes, so the store
+    overwrites the operand a fault is classified from: the reported first fault must still
+    be the oracle's on the original operands."""
+    rng = np.random.default_rng(23)
+    n = 70_001
+    big, tiny = np.finfo(dtype).max, np.finfo(dtype).tiny
+
+    def fresh():
+        return rng.uniform(-1, 1, n).astype(dtype)
+
+    def spots():
+        return sorted(int(x) for x in rng.choice(n, 3, replace=False))
+
+    # checked Add / Multiply into either operand: a tiny-inexact product, an overflow, a NaN
+    for op, into in ((0, "a"), (0, "b"), (2, "a"), (2, "b")):
+        a, b = fresh(), fresh()
+        i, j, k = spots()
+        a[i], b[i] = tiny, dtype(1.0 / 3.0)
+        a[j], b[j] = big, big if op == 0 else dtype(2.0)
+        b[k] = np.nan
+        _, rf = oracle.binary(op, a, b)
+        assert rf is not None
+        da, db = ctx.upload(a), ctx.upload(b)
+        out = da if into == "a" else db
+        _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_binary(op, da, db, out=out))
+        assert gf == _ofault(rf), (op, into, gf, rf)
+        da.free()
+        db.free()
+    # ReLU backward into its input or its upstream gradient: a NaN input, an infinite upstream
+    for into in ("x", "up"):
+        x, up = fresh(), fresh()
+        i, j, _ = spots()
+        x[j] = np.nan
+        up[i] = -np.inf
+        _, rf = oracle.relu_backward(x, up)
+        assert rf is not None
+        dx, du = ctx.upload(x), ctx.upload(up)
+        out = dx if into == "x" else du
+        _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_relu_backward(dx, du, out=out))
+        assert gf == _ofault(rf), (into, gf, rf)
+        dx.free()
+        du.free()
+    # SGD into its weights: an invalid Multiply (NaN gradient) and an overflowing Subtract
+    w, g = fresh(), fresh() * dtype(1e-3)
+    i, j, _ = spots()
+    w[i], g[i] = -big, big
+    g[j] = np.nan
+    _, rf = oracle.sgd(w, g, 0.01)
+    assert rf is not None
+    dw, dg = ctx.upload(w), ctx.upload(g)
+    _, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_sgd(dw, dg, 0.01, out=dw))
+    assert gf == _ofault(rf), (gf, rf)
+    dw.free()
+    dg.free()
+    # fused Add -> ReLU into its left operand: the Add's overflow comes first
+    a, b = fresh(), fresh()
+    i, j, _ = spots()
+    a[i], b[i] = big, big
+    a[j] = np.inf
+    _, rf = oracle.binary(0, a, b)
+    assert rf is not None
+    da, db = ctx.upload(a), ctx.upload(b)
+    _, gf = _gpu_fault(pcu_pkg, lambda: ctx.checked_add_relu(da, db, out=da))
+    assert gf == _ofault(rf), (gf, rf)
+    da.free()
+    db.free()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 def test_matmul_first_fault_late_in_a_long_reduction(ctx, pcu_pkg, dtype, engine):
     """The replay's walk of one cell over K = 1000 (sixteen chunks of 64, the last one
     partial), every layout and policy, against the oracle: (a) cell (2, 3) overflows in the

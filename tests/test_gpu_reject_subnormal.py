@@ -1,0 +1,160 @@
+"""RejectSubnormal on the screened tile kernels, against the oracle.
+
+Under RejectSubnormalResult (core/scalar_float_underflow.rs:61-73) a nonzero subnormal
+partial sum faults as well as a tiny product. A product of at least 2^-103 (2^-970 for
+binary64) is a multiple of the smallest normal, and rounded sums of such multiples stay
+multiples, so only a cell that meets a smaller product can have a subnormal partial sum. The
+tile kernels check every partial sum of a tile whose row and column exponents allow such a
+product, mark the cells of each lane that met a subnormal sum, and flag their 32 x 32
+blocks; the replay walks only those cells (and the tiny scan's candidates for products).
+
+Each case plants, in zeroed rows of op(A), a pair of products that cancel to a subnormal
+partial sum at a chosen k (and, in some, tiny products elsewhere), on shapes that reach each
+tile kernel: the 128 x 128 matrix-core tile (whole, three stages), the 16 x 16-wave tile,
+the 64 x 64 tile with bound checks, the vector-unit binary32 tile and the binary64 tile.
+Every output bit and first fault is compared with the oracle under all three policies.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx(pcu_pkg):
+    c = pcu_pkg.Context(0)
+    yield c
+    c.set_matmul_engine("auto")
+    c.close()
+
+
+def _bits(a):
+    a = np.asarray(a)
+    return a.view(np.uint32 if a.dtype == np.float32 else np.uint64)
+
+
+def _run(ctx, pcu_pkg, a, b, tl, tr, policy):
+    da, db = ctx.upload(a), ctx.upload(b)
+    try:
+        out = ctx.strict_matmul(da, db, tl, tr, policy)
+        got = out.numpy()
+        out.free()
+        return got, None
+    except pcu_pkg.PcuExecutionError as e:
+        f = e.tensor_fault
+        return None, (f.element_index, f.reduction_index, int(f.step), int(f.kind))
+    finally:
+        da.free()
+        db.free()
+
+
+def _of(f):
+    return None if f is None else (f.element_index, f.reduction_index, f.step, f.kind)
+
+
+def _plant_cancellation(a, b, r, c, k1, k2, dtype):
+    """Row r of op(A) zero but for k1 and k2; cell (r, c)'s products there are
+    2^e (1 + ulp) and -2^e, so its partial sum at k2 is 2^e ulp: subnormal. The row's other
+    cells get 2^e (1 + ulp) b1 - 2^e b2 for their own column entries, normal in general."""
+    f32 = dtype == np.float32
+    e, ulp = (-104, 2.0 ** -23) if f32 else (-971, 2.0 ** -52)
+    a[r, :] = 0
+    a[r, k1] = dtype(2.0 ** e * (1 + ulp))
+    a[r, k2] = dtype(-(2.0 ** e))
+    b[k1, c] = b[k2, c] = dtype(1.0)
+
+
+SHAPES = [  # (M, K, N, dtype, engine): the tile kernel each reaches
+    (2048, 64, 2048, np.float32, "mfma_products"),   # 128 x 128 whole tiles, three stages
+    (1024, 48, 1024, np.float32, "mfma_products"),   # 16 x 16 waves, whole 64 x 64 tiles
+    (1000, 40, 700, np.float32, "mfma_products"),    # 64 x 64 tiles with bound checks
+    (512, 64, 640, np.float32, "valu"),              # vector-unit binary32
+    (2048, 32, 2048, np.float64, "valu"),            # binary64 8 x 8 block, full grid
+]
+IDS = ["mfma128", "mfma16", "mfma64-ragged", "valu-f32", "valu-f64"]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=IDS)
+def test_reject_subnormal_partial_sums(ctx, pcu_pkg, shape):
+    m, k, n, dtype, engine = shape
+    ctx.set_matmul_engine(engine)
+    rng = np.random.default_rng(m + k + n)
+    f32 = dtype == np.float32
+    cases = []
+    # (1) one subnormal partial sum, first slab to last slab
+    for k1, k2 in ((0, 3), (5, k // 2), (1, k - 1)):
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        r, c = int(rng.integers(m)), int(rng.integers(n))
+        _plant_cancellation(a, b, r, c, k1, k2, dtype)
+        cases.append((f"sum-at-k{k2}", a, b))
+    # (2) two planted cells: the later row's pair cancels in an earlier k; plus a tiny
+    #     product (subnormal under every policy's screen) in a third row after both
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    r1, r2 = sorted(int(x) for x in rng.choice(m - 1, 2, replace=False))
+    _plant_cancellation(a, b, r1, n - 1, 2, k - 2, dtype)
+    _plant_cancellation(a, b, r2, 0, 1, 4, dtype)
+    a[m - 1, 7] = dtype(2.0 ** (-140 if f32 else -1060))
+    cases.append(("two-cells-and-tiny", a, b))
+    # (3) a tiny product in a cell before the subnormal sum's cell
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    _plant_cancellation(a, b, m // 2, n // 2, 3, 9, dtype)
+    a[m // 4, k - 1] = dtype(3 * 2.0 ** (-140 if f32 else -1060))  # a subnormal operand
+    cases.append(("tiny-before-sum", a, b))
+    # (4) every cell marked (one tiny column of op(A)), no fault under RejectSubnormal
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    sign = np.where(rng.random(m) < 0.5, -1.0, 1.0)
+    a[:, 0] = (2.0 ** (-120 if f32 else -1000) * sign).astype(dtype)
+    b[0, :] = (rng.uniform(0.5, 1.0, n) * np.where(rng.random(n) < 0.5, -1.0, 1.0)).astype(dtype)
+    cases.append(("all-marked-clean", a, b))
+    try:
+        for name, a, b in cases:
+            for tl, tr in ((False, False), (True, False), (False, True)):
+                aa = np.ascontiguousarray(a.T) if tl else a
+                bb = np.ascontiguousarray(b.T) if tr else b
+                for policy in (1, 0, 2):
+                    ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+                    if name.startswith("sum-at") and policy == 1:
+                        assert rf is not None and rf.step == 2, (name, rf)  # an Add faults
+                    if name == "all-marked-clean" and policy == 1:
+                        assert rf is None
+                    got, gf = _run(ctx, pcu_pkg, aa, bb, tl, tr, policy)
+                    assert gf == _of(rf), (name, tl, tr, policy, gf, rf)
+                    if rf is None:
+                        np.testing.assert_array_equal(_bits(got), _bits(ref),
+                                                      err_msg=f"{name} {tl}{tr} {policy}")
+    finally:
+        ctx.set_matmul_engine("auto")
+
+
+def test_reject_subnormal_after_calls_of_other_shapes(pcu_pkg):
+    """A fresh context runs RejectSubnormal MatMuls of smaller shapes (each filling its
+    superslab tables and partial-sum block words), then the planted 2048 x 32 x 2048 case,
+    whose scratch reuses those bytes for its generation-tagged words: the first fault must
+    still be the oracle's. (With the tables kept in the MatMul scratch, their bits outranked
+    the new generation under atomicMax and the planted fault went unseen.)"""
+    with pcu_pkg.Context(0) as c:
+        rng = np.random.default_rng(99)
+        for (m, k, n) in ((2048, 64, 2048), (1024, 48, 1024), (1000, 40, 700), (512, 64, 640)):
+            a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+            b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+            a[:, 0] = np.float32(2.0 ** -120)  # every tile marked: tables and block words written
+            for policy in (1, 0):
+                ref, rf = oracle.matmul(a, b, policy=policy)
+                got, gf = _run(c, pcu_pkg, a, b, False, False, policy)
+                assert gf == _of(rf), ((m, k, n), policy, gf, rf)
+        for dtype in (np.float32, np.float64):
+            for engine in ("valu", "mfma_products"):
+                c.set_matmul_engine(engine)
+                a = rng.uniform(-1, 1, (2048, 32)).astype(dtype)
+                b = rng.uniform(-1, 1, (32, 2048)).astype(dtype)
+                _plant_cancellation(a, b, 1500, 77, 0, 3, dtype)
+                _, rf = oracle.matmul(a, b, policy=1)
+                assert rf is not None and rf.step == 2
+                _, gf = _run(c, pcu_pkg, a, b, False, False, 1)
+                assert gf == _of(rf), (dtype, engine, gf, rf)

@@ -113,3 +113,54 @@ def test_noalloc_refuses_shapes_beyond_its_scratch(ctx, pcu_pkg):
     assert st == _abi.PCU_ERR_ARGUMENT
     for x in (a, b, out):
         x.free()
+
+
+def test_noalloc_allocates_nothing(pcu_pkg):
+    """A fresh context whose only MatMuls are no-allocation calls, a full F32 grid with op(B)
+    transposed among them (where the allocating entry point keeps a K x N copy of op(B)):
+    the device memory pool's used bytes, current and high-water, do not move across the
+    calls, so neither the screen scratch nor the copy of op(B) is allocated."""
+    from fusion_pcu_amd import _abi
+    from fusion_pcu_amd import dtype_code
+    lib = pcu_pkg.lib()
+    hip = ctypes.CDLL("libamdhip64.so")
+    used_current, used_high = 7, 8  # hipMemPoolAttrUsedMemCurrent, hipMemPoolAttrUsedMemHigh
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), 0) == 0
+
+    def pool_bytes(attr):
+        v = ctypes.c_uint64()
+        assert hip.hipMemPoolGetAttribute(pool, attr, ctypes.byref(v)) == 0
+        return v.value
+
+    rng = np.random.default_rng(8)
+    shapes = [(2048, 48, 2048, (False, True), np.float32, 0),
+              (1000, 300, 700, (False, False), np.float32, 1),
+              (300, 257, 130, (False, True), np.float64, 0),
+              (1024, 64, 1024, (True, False), np.float32, 0)]
+    with pcu_pkg.Context(0) as c:
+        calls, bufs = [], []
+        for rows, inner, cols, (tl, tr), dtype, policy in shapes:
+            a = rng.uniform(-1, 1, (inner, rows) if tl else (rows, inner)).astype(dtype)
+            b = rng.uniform(-1, 1, (cols, inner) if tr else (inner, cols)).astype(dtype)
+            da, db, out = c.upload(a), c.upload(b), c.empty((rows, cols), dtype)
+            bufs += [da, db, out]
+            calls.append((dtype_code(dtype), rows, inner, cols, int(tl), int(tr), da.ptr, db.ptr,
+                          out.ptr, policy))
+        c.synchronize()
+        assert hip.hipDeviceSynchronize() == 0
+        used0 = pool_bytes(used_current)
+        zero = ctypes.c_uint64(0)
+        high_reset = hip.hipMemPoolSetAttribute(pool, used_high, ctypes.byref(zero)) == 0
+        f = _abi.Fault()
+        for _ in range(2):
+            for args in calls:
+                st = lib.pcu_strict_matmul_noalloc(c.handle, *args, ctypes.byref(f))
+                assert st == _abi.PCU_OK, (args[1:4], st, c.error_text())
+        c.synchronize()
+        assert hip.hipDeviceSynchronize() == 0
+        assert pool_bytes(used_current) == used0
+        if high_reset:  # reset to the current usage (or to 0): no allocation rose above it
+            assert pool_bytes(used_high) <= used0
+        for x in bufs:
+            x.free()
