@@ -95,18 +95,23 @@ def time_matmul(ctx, da, db, dc, m, k, n, steps, warmup, expect=0, policy=0):
     }
 
 
-def settle_clock(ctx, ms):
-    """Bring the GPU out of its idle clock before the first leg. A cold MI355X runs the first
-    ~15 strict 4096^3 launches (about 30 ms of load) up to 25% slower while its clock ramps
+def settle_clock(ctx, ms, bufs=None):
+    """Bring the GPU out of its idle clock before a leg. A cold MI355X runs the first ~15
+    strict 4096^3 launches (about 30 ms of load) up to 25% slower while its clock ramps
     (2291 -> 1890 us a launch in one trace), which a short warm-up leaves inside the timed
-    steps. This runs a different workload, the native (BackendDefined) F32 MatMul 4096^3,
-    for about `ms` milliseconds; no leg's timed region includes it."""
+    steps, and the host-to-device uploads of a leg's inputs leave it idle again. This runs a
+    different workload, the native (BackendDefined) F32 MatMul, for about `ms` milliseconds,
+    on the leg's own F32 buffers `bufs` = (A, B, C) when given (so nothing is uploaded after
+    it); no leg's timed region includes it."""
     from fusion_pcu_amd import synthetic as syn
     if ms <= 0:
         return 0
-    da = ctx.upload(syn.uniform(91, (4096, 4096), np.float32))
-    db = ctx.upload(syn.uniform(92, (4096, 4096), np.float32))
-    dc = ctx.empty((4096, 4096), np.float32)
+    own = bufs is None
+    if own:
+        bufs = (ctx.upload(syn.uniform(91, (4096, 4096), np.float32)),
+                ctx.upload(syn.uniform(92, (4096, 4096), np.float32)),
+                ctx.empty((4096, 4096), np.float32))
+    da, db, dc = bufs
     calls = 0
     t0 = time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < ms:
@@ -114,17 +119,20 @@ def settle_clock(ctx, ms):
             ctx.native_matmul(da, db, out=dc)
         ctx.synchronize()
         calls += 8
-    for x in (da, db, dc):
-        x.free()
+    if own:
+        for x in bufs:
+            x.free()
     return calls
 
 
-def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12):
+def bench_matmul(pkg, ctx, m, k, n, dtype, steps, warmup, seed_a=11, seed_b=12, settle_ms=0.0):
     from fusion_pcu_amd import synthetic as syn
     a = syn.uniform(seed_a, (m, k), dtype)
     b = syn.uniform(seed_b, (k, n), dtype)
     da, db = ctx.upload(a), ctx.upload(b)
     dc = ctx.empty((m, n), dtype)
+    if dtype == np.float32:
+        settle_clock(ctx, settle_ms, (da, db, dc))
     res = time_matmul(ctx, da, db, dc, m, k, n, steps, warmup)
     for x in (da, db, dc):
         x.free()
@@ -179,9 +187,11 @@ def bench_policies(pkg, ctx, steps):
     """The strict F32 MatMul 4096^3 under the two other underflow policies
     (core/scalar_float_underflow.rs:61-73), clean, and the suspect-heavy input (A column 0
     at +-2^-120, so every cell meets a product below 2^-103 and the exponent screen marks
-    all of them) under RejectSubnormal, where a subnormal partial sum faults too: the tile
-    kernel checks the partial sums of every marked tile, so the replay walks only cells whose
-    lane met a subnormal sum (none here)."""
+    all of them) under RejectSubnormal, where a subnormal partial sum faults too: in each
+    marked tile the tile kernel checks the partial sums of the 64-k superslabs that may form
+    a subnormal one (here the first, where the small products are, and none after it, since
+    no sum leaves it below 2^-103), so the replay walks only cells whose lane met a
+    subnormal sum (none here). Each leg starts after a 30 ms clock settle."""
     from fusion_pcu_amd import synthetic as syn
     M = 4096
     a = syn.uniform(11, (M, M), np.float32)
@@ -190,6 +200,7 @@ def bench_policies(pkg, ctx, steps):
     dc = ctx.empty((M, M), np.float32)
     da, db = ctx.upload(a), ctx.upload(b)
     for name, policy in (("reject_subnormal_clean", 1), ("allow_gradual_clean", 2), ("ieee_clean", 0)):
+        settle_clock(ctx, 30.0, (da, db, dc))
         out[name] = time_matmul(ctx, da, db, dc, M, M, M, steps, 3, policy=policy)
     da.free()
     db.free()
@@ -197,6 +208,7 @@ def bench_policies(pkg, ctx, steps):
     a[:, 0] = (2.0 ** -120 * sign).astype(np.float32)
     b[0, :] = (np.random.default_rng(4).uniform(0.5, 1.0, M) * sign[::-1]).astype(np.float32)
     da, db = ctx.upload(a), ctx.upload(b)
+    settle_clock(ctx, 30.0, (da, db, dc))
     r = time_matmul(ctx, da, db, dc, M, M, M, steps, 3, policy=1)
     r["input"] = "A col 0 = +-2^-120, B row 0 in +-[0.5, 1), rest uniform[-1,1]: every cell marked, none faults"
     out["reject_subnormal_suspect_heavy"] = r
@@ -539,10 +551,10 @@ def main() -> int:
     G.configure(0)
     ctx = G.default_context()
     if True:
-        log(f"clock settle: native F32 MatMul for {args.settle_ms:.0f} ms")
-        settle_calls = settle_clock(ctx, args.settle_ms)
-        log("strict F32 MatMul 4096^3")
-        mm = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup)
+        log(f"strict F32 MatMul 4096^3 (clock settle: native F32 MatMul for {args.settle_ms:.0f} ms "
+            f"on the uploaded inputs first)")
+        mm = bench_matmul(pkg, ctx, M, K, N, np.float32, args.steps, args.warmup,
+                          settle_ms=args.settle_ms)
         extra = {}
         if not args.no_extra:
             log("strict F32 MLP training step (C5)")
@@ -623,8 +635,8 @@ def main() -> int:
                                "with per-kernel timing off (the roofline's kernel duration comes "
                                "from a second, timed pass)",
                    "m": M, "k": K, "n": N,
-                   "clock_settle": f"{settle_calls} native F32 MatMul 4096^3 calls (~{args.settle_ms:.0f} ms) "
-                                   f"before the first leg, outside every timed region"},
+                   "clock_settle": f"native F32 MatMul 4096^3 on the uploaded inputs for ~{args.settle_ms:.0f} ms "
+                                   f"before the warm-up, outside the timed region"},
         "pct_fp32_vector_peak": round(100.0 * mm["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 3),
         "mlp_train_steps_per_s": (round(extra["mlp_c5"]["steps_per_s"], 3)
                                   if "mlp_c5" in extra else None),

@@ -37,9 +37,6 @@
 namespace pcu {
 
 constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
-// The same in the 16-bit exponents of the tiny scan and the superslab tables (two of them
-// still sum far above any threshold).
-constexpr short kScanExpNone = 16000;
 
 // Branch-free: the prefilter applies it to every element of both operands.
 __device__ __forceinline__ int ilog2_abs(float v)
@@ -456,6 +453,16 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
     SubLanes subl; // lanes that met a nonzero subnormal partial sum
     const int cls = kClassSubnormal;
     auto run_form = [&](auto &&run) { run(std::integral_constant<bool, CHECK && !NATIVE>{}); };
+    // The checking form checks the superslabs that need it (SumGate).
+    __shared__ unsigned char fine_ss[kSumMaxSuperSlabs];
+    SumGate<BK> sgate{nullptr, false};
+    bool chk = true; // the current slab's sums are checked (checking form)
+    if constexpr (CHECK && !NATIVE) {
+        if (sck.tbl_a != nullptr) {
+            tile_fine_superslabs<BM, BN>(sck, m0, n0, M, N, K, fine_ss);
+            sgate.fine = fine_ss;
+        }
+    }
 
     T acc[8][8];
 #pragma unroll
@@ -515,10 +522,12 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                             for (int j = 0; j < PB; j++)
                                 acc[i][h + j] = acc[i][h + j] + p[j];
                             if constexpr (CK) {
+                                if (chk) {
 #pragma unroll
-                                for (int j = 0; j < PB; j += 4)
-                                    check_subnormal4(subl, acc[i][h + j], acc[i][h + j + 1],
-                                                     acc[i][h + j + 2], acc[i][h + j + 3], cls);
+                                    for (int j = 0; j < PB; j += 4)
+                                        check_subnormal4(subl, acc[i][h + j], acc[i][h + j + 1],
+                                                         acc[i][h + j + 2], acc[i][h + j + 3], cls);
+                                }
                             }
                         }
                     }
@@ -561,15 +570,33 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                         for (int j = 0; j < 8; j++)
                             acc[i][j] = acc[i][j] + p[j];
                         if constexpr (CK) {
+                            if (chk) {
 #pragma unroll
-                            for (int j = 0; j < 8; j += 4)
-                                check_subnormal4(subl, acc[i][j], acc[i][j + 1], acc[i][j + 2],
-                                                 acc[i][j + 3], cls);
+                                for (int j = 0; j < 8; j += 4)
+                                    check_subnormal4(subl, acc[i][j], acc[i][j + 1],
+                                                     acc[i][j + 2], acc[i][j + 3], cls);
+                            }
                         }
                     }
                 }
             }
         }
+    };
+    auto off_grid = [&]() {
+        bool o = false;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                o |= sum_off_grid(acc[i][j]);
+        return __builtin_amdgcn_ballot_w64(o) != 0;
+    };
+    // Slab kt; the checking form checks its sums when the gate opens it.
+    auto gcompute = [&](const T (*Ac)[Cfg::LDA], const T (*Bc)[Cfg::LDB], int kt, auto ck)
+                        __attribute__((always_inline)) {
+        if constexpr (decltype(ck)::value)
+            chk = sgate.at(kt, off_grid);
+        compute(Ac, Bc, ck);
     };
     if constexpr (!kDirect) {
         if (ktiles > 0) {
@@ -589,7 +616,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
                     else
                         stage.fetch(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
                 }
-                compute(As[cur], Bs[cur], ck);
+                gcompute(As[cur], Bs[cur], kt, ck);
                 if (kt + 1 < ktiles)
                     stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
                 __syncthreads();
@@ -635,7 +662,7 @@ __global__ __launch_bounds__(256, 2) void k_strict_gemm(
             T (*Bn)[Cfg::LDB] = cur ? B0 : B1;
             if (kt + 1 < ktiles)
                 load(An, Bn);
-            compute(Ac, Bc, ck);
+            gcompute(Ac, Bc, kt, ck);
             if (kt + 1 < ktiles)
                 stash(An);
             wait_lds_loads();
@@ -1687,7 +1714,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const uint64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const bool sum_check = reject && K > 0 && sc.sum_flag != nullptr && (f32 || tiles >= 256);
     int thr = reject && !sum_check ? sub_thr : tiny_thr;
-    const SumCheck sck = sum_check ? SumCheck{sc.sum_flag, sc.gen, sc.flag_cols, sub_thr} : SumCheck{};
+    SumCheck sck = sum_check ? SumCheck{sc.sum_flag, sc.gen, sc.flag_cols, sub_thr} : SumCheck{};
     if (ev)
         (void)hipEventRecord(ev[0], s);
     if (engine == kEngineAuto && K > 0 && M * N <= fused_cells<T>()) {
@@ -1720,6 +1747,12 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         tbls.b = sc.tbl_b;
         tbls.a_xmajor = !ta; // a rows job over A (M x K), else a columns job over A (K x M)
         tbls.b_xmajor = tb;  // a rows job over B (N x K), else a columns job over B (K x N)
+        // The checking tiles check only the superslabs that need it (the tables describe
+        // op(B) as stored, also when the tile kernel reads its K x N copy).
+        sck.tbl_a = tbls.a;
+        sck.tbl_b = tbls.b;
+        sck.a_xmajor = tbls.a_xmajor;
+        sck.b_xmajor = tbls.b_xmajor;
     }
     if (risk && K > 0) {
         // op(A) row r is stored row r (A is M x K) or stored column r (A is K x M); op(B)

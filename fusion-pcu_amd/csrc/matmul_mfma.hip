@@ -116,6 +116,16 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
     SubLanes subl; // lanes that met a nonzero subnormal partial sum
     const int cls = kClassSubnormal;
     auto run_form = [&](auto &&run) { run(std::integral_constant<bool, CHECK>{}); };
+    // The checking form checks the superslabs that need it (SumGate).
+    __shared__ unsigned char fine_ss[kSumMaxSuperSlabs];
+    SumGate<BK> sgate{nullptr, false};
+    bool chk = true; // the current slab's sums are checked (checking form)
+    if constexpr (CHECK) {
+        if (sck.tbl_a != nullptr) {
+            tile_fine_superslabs<BM, BN>(sck, m0, n0, M, N, K, fine_ss);
+            sgate.fine = fine_ss;
+        }
+    }
 
     float acc[S][16];
 #pragma unroll
@@ -125,6 +135,21 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             acc[t][r] = 0.0f;
 
     SlabStager<float, Cfg, TA, TB, VA, VB> stage;
+    auto off_grid = [&]() {
+        bool o = false;
+#pragma unroll
+        for (int t = 0; t < S; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                o |= sum_off_grid(acc[t][r]);
+        return __builtin_amdgcn_ballot_w64(o) != 0;
+    };
+    // Slab kt; the checking form checks its sums when the gate opens it.
+    auto gated = [&](auto &&slab_fn, int kt, auto ck) __attribute__((always_inline)) {
+        if constexpr (decltype(ck)::value)
+            chk = sgate.at(kt, off_grid);
+        slab_fn(ck);
+    };
 
     v32f zero;
 #pragma unroll
@@ -158,17 +183,21 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[r];
         if constexpr (CK) {
+            if (chk) {
 #pragma unroll
-            for (int r = 0; r < 16; r += 4)
-                check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+                for (int r = 0; r < 16; r += 4)
+                    check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 16; r++)
             c[r] = c[r] + p[16 + r];
         if constexpr (CK) {
+            if (chk) {
 #pragma unroll
-            for (int r = 0; r < 16; r += 4)
-                check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+                for (int r = 0; r < 16; r += 4)
+                    check_subnormal4(subl, c[r], c[r + 1], c[r + 2], c[r + 3], cls);
+            }
         }
         // Emits nothing; ties the sixteen sums to this point of the instruction stream.
         asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
@@ -355,11 +384,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         };
         auto run = [&](auto ck) {
             for (int kt = 0; kt < ktiles; kt += 3) {
-                slab(std::integral_constant<int, 0>{}, kt, ck);
+                gated([&](auto c) { slab(std::integral_constant<int, 0>{}, kt, c); }, kt, ck);
                 if (kt + 1 < ktiles)
-                    slab(std::integral_constant<int, 1>{}, kt + 1, ck);
+                    gated([&](auto c) { slab(std::integral_constant<int, 1>{}, kt + 1, c); }, kt + 1, ck);
                 if (kt + 2 < ktiles)
-                    slab(std::integral_constant<int, 2>{}, kt + 2, ck);
+                    gated([&](auto c) { slab(std::integral_constant<int, 2>{}, kt + 2, c); }, kt + 2, ck);
             }
         };
         run_form(run);
@@ -372,8 +401,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             stage.stash(As[0], Bs[0], tid);
         }
         __syncthreads();
-        auto run = [&](auto ck) {
-        for (int kt = 0; kt < ktiles; kt++) {
+        auto slab2 = [&](int kt, auto ck) __attribute__((always_inline)) {
             const int cur = kt & 1;
             if (kt + 1 < ktiles) {
                 if (WHOLE)
@@ -437,7 +465,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
             if (kt + 1 < ktiles)
                 stage.stash(As[cur ^ 1], Bs[cur ^ 1], tid);
             __syncthreads();
-        }
+        };
+        auto run = [&](auto ck) {
+            for (int kt = 0; kt < ktiles; kt++)
+                gated([&](auto c) { slab2(kt, c); }, kt, ck);
         };
         run_form(run);
     }
@@ -569,6 +600,15 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
         return;
     SubLanes subl;
     const int cls = kClassSubnormal;
+    __shared__ unsigned char fine_ss[kSumMaxSuperSlabs];
+    SumGate<BK> sgate{nullptr, false};
+    bool chk = true; // the current slab's sums are checked (checking form)
+    if constexpr (CHECK) {
+        if (sck.tbl_a != nullptr) {
+            tile_fine_superslabs<T, T>(sck, m0, n0, M, N, K, fine_ss);
+            sgate.fine = fine_ss;
+        }
+    }
 
     // Loads: waves 0-3 move op(A), waves 4-7 op(B), one 1 KiB instruction each a slab
     // (quad g or rows 4 g .. 4 g + 3 of the slab, g = wave % 4).
@@ -619,8 +659,10 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 acc[q] = acc[q] + p[4 * blk + q];
-            if constexpr (CK)
-                check_subnormal4(subl, acc[0], acc[1], acc[2], acc[3], cls);
+            if constexpr (CK) {
+                if (chk)
+                    check_subnormal4(subl, acc[0], acc[1], acc[2], acc[3], cls);
+            }
         }
         asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
     };
@@ -663,13 +705,25 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
             wait_lds_loads();
         __syncthreads();
     };
+    auto off_grid = [&]() {
+        bool o = false;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            o |= sum_off_grid(acc[q]);
+        return __builtin_amdgcn_ballot_w64(o) != 0;
+    };
+    auto gated = [&](auto cur_c, int kt, auto ck) __attribute__((always_inline)) {
+        if constexpr (decltype(ck)::value)
+            chk = sgate.at(kt, off_grid);
+        slab(cur_c, kt, ck);
+    };
     auto run = [&](auto ck) {
         for (int kt = 0; kt < ktiles; kt += 3) {
-            slab(std::integral_constant<int, 0>{}, kt, ck);
+            gated(std::integral_constant<int, 0>{}, kt, ck);
             if (kt + 1 < ktiles)
-                slab(std::integral_constant<int, 1>{}, kt + 1, ck);
+                gated(std::integral_constant<int, 1>{}, kt + 1, ck);
             if (kt + 2 < ktiles)
-                slab(std::integral_constant<int, 2>{}, kt + 2, ck);
+                gated(std::integral_constant<int, 2>{}, kt + 2, ck);
         }
     };
     run(std::integral_constant<bool, CHECK>{});

@@ -487,41 +487,48 @@ __device__ __forceinline__ bool tile_exp_sum_below(const unsigned long long *row
     return __builtin_amdgcn_readfirstlane(tile_min[0] + tile_min[1]) < thr;
 }
 
-// Which superslabs (64 k) of a checking tile need their partial sums checked: fine[s] = 1
-// when the smallest exponent of the tile's op(A) rows plus that of its op(B) columns over
-// superslab s, from the screen's tables, lies below sck.thr (a product there may be below
-// 2^thr, not a multiple of the smallest normal); all 1 without tables. Block-wide, one
-// barrier. K spans at most kSumMaxSuperSlabs superslabs when there are tables.
-constexpr int kSumMaxSuperSlabs = 1024;
+// The 16-bit exponent of zero and non-finite entries in the superslab tables (two of them
+// still sum far above any threshold).
+constexpr short kScanExpNone = 16000;
+
+// Gating of the partial-sum check in a checking tile, by superslab (64 k). Products of at
+// least 2^thr (thr = -103, binary64 -970), and zero, are multiples of the smallest normal
+// 2^-126 (2^-1022), and so is every rounded sum of such multiples: a partial sum can only be
+// a nonzero subnormal in a superslab that holds a product below 2^thr ("fine" by the screen's
+// tables: the tile's smallest op(A) row exponent plus smallest op(B) column exponent over
+// the superslab is below thr), or in a later one that a sum which is not such a multiple
+// enters (such sums are below 2^-103, 2^-970 in magnitude). So superslab s is checked when it
+// is fine, or when s - 1 was checked and one of the wave's partial sums is nonzero and below
+// 2^-102 (2^-969) at its start; every other superslab begins and ends on multiples.
+// Without tables every slab is checked.
+constexpr int kSumMaxSuperSlabs = 1024; // K of at most 65536 when there are tables
+
+// fine[s] for the tile's superslabs from the tables: block-wide, ends with a barrier.
 template <int BM, int BN>
 __device__ __forceinline__ void tile_fine_superslabs(const SumCheck &sck, int m0, int n0, int M,
                                                      int N, int K, unsigned char *fine)
 {
     const int nss = (K + 63) / 64;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    for (int s = wave; s < nss; s += waves) {
-        int ea = 16000, eb = 16000; // zero and non-finite entries
-        if (sck.tbl_a) {
-            for (int i = lane; i < BM; i += 64)
-                if (m0 + i < M) {
-                    const int v = sck.a_xmajor ? sck.tbl_a[(size_t)(m0 + i) * nss + s]
-                                               : sck.tbl_a[(size_t)s * M + m0 + i];
-                    ea = v < ea ? v : ea;
-                }
-            for (int i = lane; i < BN; i += 64)
-                if (n0 + i < N) {
-                    const int v = sck.b_xmajor ? sck.tbl_b[(size_t)(n0 + i) * nss + s]
-                                               : sck.tbl_b[(size_t)s * N + n0 + i];
-                    eb = v < eb ? v : eb;
-                }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const int oa = __shfl_xor(ea, off, 64), ob = __shfl_xor(eb, off, 64);
-                ea = oa < ea ? oa : ea;
-                eb = ob < eb ? ob : eb;
+    const int lane = threadIdx.x & 63, waves = blockDim.x >> 6;
+    for (int s = (int)(threadIdx.x >> 6); s < nss; s += waves) {
+        int ea = kScanExpNone, eb = kScanExpNone;
+        for (int i = lane; i < BM; i += 64)
+            if (m0 + i < M) {
+                const int v = sck.a_xmajor ? sck.tbl_a[(size_t)(m0 + i) * nss + s]
+                                           : sck.tbl_a[(size_t)s * M + m0 + i];
+                ea = v < ea ? v : ea;
             }
-        } else {
-            ea = eb = -(1 << 20);
+        for (int i = lane; i < BN; i += 64)
+            if (n0 + i < N) {
+                const int v = sck.b_xmajor ? sck.tbl_b[(size_t)(n0 + i) * nss + s]
+                                           : sck.tbl_b[(size_t)s * N + n0 + i];
+                eb = v < eb ? v : eb;
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const int oa = __shfl_xor(ea, off, 64), ob = __shfl_xor(eb, off, 64);
+            ea = oa < ea ? oa : ea;
+            eb = ob < eb ? ob : eb;
         }
         if (lane == 0)
             fine[s] = ea + eb < sck.thr;
@@ -529,17 +536,39 @@ __device__ __forceinline__ void tile_fine_superslabs(const SumCheck &sck, int m0
     __syncthreads();
 }
 
-// A partial sum that a later sum could still carry to a nonzero subnormal: nonzero and below
-// 2^-102 (2^-969), so perhaps not a multiple of the smallest normal. A sum of zero, or of
-// at least that magnitude, is such a multiple, and sums of multiples stay multiples.
-__device__ __forceinline__ bool sum_may_go_subnormal(float v)
+// A partial sum that may not be a multiple of the smallest normal: nonzero and below 2^-102
+// (binary64 2^-969).
+__device__ __forceinline__ bool sum_off_grid(float v)
 {
     return (bits_of(v) & 0x7fffffffu) - 1u < 0x0C7FFFFFu;
 }
-__device__ __forceinline__ bool sum_may_go_subnormal(double v)
+__device__ __forceinline__ bool sum_off_grid(double v)
 {
     return (bits_of(v) & 0x7fffffffffffffffull) - 1ull < (54ull << 52) - 1ull;
 }
+
+// The wave's gate over slabs of BK k; slabs are presented in order from 0.
+template <int BK> struct SumGate {
+    static_assert(64 % BK == 0, "a slab lies in one superslab");
+    static constexpr int kPer = 64 / BK;
+    const unsigned char *fine; // LDS; null: check every slab
+    bool chk;
+    // Whether slab kt is checked. off_grid() reports whether one of the wave's partial sums
+    // is off the grid of multiples (uniform over the wave); it is called only at the start of
+    // a superslab that follows a checked one and is not fine itself.
+    template <class F> __device__ __forceinline__ bool at(int kt, F &&off_grid)
+    {
+        if (fine == nullptr)
+            return true;
+        if (kt % kPer == 0) {
+            bool c = __builtin_amdgcn_readfirstlane(fine[kt / kPer]) != 0;
+            if (!c && chk)
+                c = off_grid();
+            chk = c;
+        }
+        return chk;
+    }
+};
 
 // The partial-sum block word of output cell (row, col).
 __device__ __forceinline__ void flag_sum_block(const SumCheck &sck, int row, int col)

@@ -158,3 +158,72 @@ def test_reject_subnormal_after_calls_of_other_shapes(pcu_pkg):
                 assert rf is not None and rf.step == 2
                 _, gf = _run(c, pcu_pkg, a, b, False, False, 1)
                 assert gf == _of(rf), (dtype, engine, gf, rf)
+
+
+DEEP = [  # (M, K, N, dtype, engine): the same tile kernels over four superslabs of 64 k
+    (2048, 256, 2048, np.float32, "mfma_products"),
+    (1024, 256, 1024, np.float32, "mfma_products"),
+    (1000, 200, 700, np.float32, "mfma_products"),
+    (512, 256, 640, np.float32, "valu"),
+    (2048, 256, 2048, np.float64, "valu"),
+]
+
+
+def _plant_carried(a, b, r, c, kc, dtype, fault):
+    """Row r of op(A) zero but for k = 3 and k = kc (superslab 2): cell (r, c) first adds
+    the largest value below 2^-103 (binary64 2^-970), a product below that bound and so not
+    a multiple of the smallest normal; superslab 1 adds nothing; at kc it adds -2^-103
+    (2^-970), a product at the bound, which leaves the subnormal -2^-127 (-2^-1023) when
+    `fault`, or -2^-102 (-2^-969), which leaves a normal sum. op(B)'s superslab 2 is kept in
+    +-[1, 2), so no product there is below the bound: the check reaches kc only because the
+    partial sum entering superslabs 1 and 2 is off the grid of multiples."""
+    f32 = dtype == np.float32
+    bound, eps = (2.0 ** -103, 2.0 ** -24) if f32 else (2.0 ** -970, 2.0 ** -53)
+    rng = np.random.default_rng(r + c + kc)
+    k = b.shape[0]
+    hi = min(192, k)
+    b[128:hi, :] = (rng.uniform(1.0, 2.0, (hi - 128, b.shape[1]))
+                    * np.where(rng.random((hi - 128, b.shape[1])) < 0.5, -1.0, 1.0)).astype(dtype)
+    a[r, :] = 0
+    a[r, 3] = dtype(bound * (1 - eps))
+    a[r, kc] = dtype(-bound if fault else -2 * bound)
+    b[3, c] = b[kc, c] = dtype(1.0)
+
+
+@pytest.mark.parametrize("shape", DEEP, ids=IDS)
+def test_reject_subnormal_across_superslabs(ctx, pcu_pkg, shape):
+    """The checking tiles check a superslab when a product in it may fall below 2^-103, or
+    when a partial sum entering it is off the grid of multiples of the smallest normal: a
+    subnormal sum formed from an off-grid sum carried across superslabs with no small
+    product, a cancellation in the last superslabs, and a carried sum that stays normal."""
+    m, k, n, dtype, engine = shape
+    ctx.set_matmul_engine(engine)
+    rng = np.random.default_rng(7 * m + k + n)
+    cases = []
+    for name, fault in (("carried-subnormal", True), ("carried-normal", False)):
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        _plant_carried(a, b, int(rng.integers(m)), int(rng.integers(n)), 150, dtype, fault)
+        cases.append((name, a, b))
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    _plant_cancellation(a, b, int(rng.integers(m)), int(rng.integers(n)), k - 50, k - 3, dtype)
+    cases.append(("late-cancellation", a, b))
+    try:
+        for name, a, b in cases:
+            for tl, tr in ((False, False), (True, False), (False, True)):
+                aa = np.ascontiguousarray(a.T) if tl else a
+                bb = np.ascontiguousarray(b.T) if tr else b
+                for policy in (1, 0):
+                    ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+                    if policy == 1 and name != "carried-normal":
+                        assert rf is not None and rf.step == 2 and rf.kind == 4, (name, rf)
+                    if name == "carried-subnormal" and policy == 1:
+                        assert rf.reduction_index == 150, rf
+                    got, gf = _run(ctx, pcu_pkg, aa, bb, tl, tr, policy)
+                    assert gf == _of(rf), (name, tl, tr, policy, gf, rf)
+                    if rf is None:
+                        np.testing.assert_array_equal(_bits(got), _bits(ref),
+                                                      err_msg=f"{name} {tl}{tr} {policy}")
+    finally:
+        ctx.set_matmul_engine("auto")
