@@ -334,27 +334,38 @@ template <typename T> __device__ __forceinline__ uint32_t chain_classify(int op,
     return classify_div(a, b, r, policy);
 }
 
+// The other operand of step S on the lanes [base, base + W) (nothing for a ReLU).
+template <typename T, bool VEC, int S>
+__device__ __forceinline__ void chain_other(const ChainLaunch &c, uint64_t base, uint64_t n,
+                                            T (&o)[Lanes<T, VEC>::W])
+{
+    constexpr int W = Lanes<T, VEC>::W;
+    const ChainStep &st = c.step[S];
+    if (S >= c.steps || st.op == kStepRelu)
+        return;
+    if (st.other) {
+        load_lanes<T, VEC>((const T *)st.other, base, n, o);
+    } else {
+        const T u = chain_uniform<T>(st.other_bits);
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            o[j] = u;
+    }
+}
+
 // Step S of a chain on the lanes [base, base + W): v holds the value the step takes and is
-// replaced by the step's result; key keeps the step's first fault in this thread.
+// replaced by the step's result, o the step's other operand (chain_other); key keeps the
+// step's first fault in this thread.
 template <typename T, bool VEC, int S>
 __device__ __forceinline__ void chain_step(const ChainLaunch &c, uint64_t base, uint64_t n,
-                                           T (&v)[Lanes<T, VEC>::W], uint64_t &key)
+                                           T (&v)[Lanes<T, VEC>::W], const T (&o)[Lanes<T, VEC>::W],
+                                           uint64_t &key)
 {
     constexpr int W = Lanes<T, VEC>::W;
     const ChainStep &st = c.step[S];
     const int op = st.op, policy = st.policy;
     const bool right = st.chain_right != 0;
-    T o[W], r[W];
-    if (op != kStepRelu) {
-        if (st.other) {
-            load_lanes<T, VEC>((const T *)st.other, base, n, o);
-        } else {
-            const T u = chain_uniform<T>(st.other_bits);
-#pragma unroll
-            for (int j = 0; j < W; j++)
-                o[j] = u;
-        }
-    }
+    T r[W];
     bool any = false;
     if (op == kStepRelu) {
 #pragma unroll
@@ -412,15 +423,22 @@ __global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n,
     uint64_t k0 = kNoFault, k1 = kNoFault, k2 = kNoFault, k3 = kNoFault;
     PCU_EW_LOOP(W)
     {
-        T v[W];
+        // Every operand is loaded before any step stores: no step reads a value stored in
+        // this launch (the plan keeps chain members out of other operands), so the loads go
+        // out together, one round trip, instead of one after each step's stores.
+        T v[W], o0[W], o1[W], o2[W], o3[W];
         load_lanes<T, VEC>((const T *)c.head, base, n, v);
-        chain_step<T, VEC, 0>(c, base, n, v, k0);
+        chain_other<T, VEC, 0>(c, base, n, o0);
+        chain_other<T, VEC, 1>(c, base, n, o1);
+        chain_other<T, VEC, 2>(c, base, n, o2);
+        chain_other<T, VEC, 3>(c, base, n, o3);
+        chain_step<T, VEC, 0>(c, base, n, v, o0, k0);
         if (c.steps > 1)
-            chain_step<T, VEC, 1>(c, base, n, v, k1);
+            chain_step<T, VEC, 1>(c, base, n, v, o1, k1);
         if (c.steps > 2)
-            chain_step<T, VEC, 2>(c, base, n, v, k2);
+            chain_step<T, VEC, 2>(c, base, n, v, o2, k2);
         if (c.steps > 3)
-            chain_step<T, VEC, 3>(c, base, n, v, k3);
+            chain_step<T, VEC, 3>(c, base, n, v, o3, k3);
     }
     wave_record_fault(k0, c.step[0].fault, gate);
     if (c.steps > 1)
@@ -435,18 +453,18 @@ __global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n,
 // core/dialect/tensor/reference/strict_sgd/strict_sgd.rs:20-46: p = rate (x) g, then
 // w' = w (-) p; ordinal 2i (Multiply) and 2i+1 (Subtract).
 
+// Blocks [bid, ...) of nb blocks over one update.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_sgd(const T *w,
-                                                    const T *g, T rate,
-                                                    T *out, uint64_t n, int policy,
-                                                    unsigned long long *fault, NodeGate gate)
+__device__ __forceinline__ void sgd_range(const T *w, const T *g, T rate, T *out, uint64_t n,
+                                          int policy, unsigned long long *fault, NodeGate gate,
+                                          uint64_t bid, uint64_t nb)
 {
     if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
     uint64_t key = kNoFault;
-    PCU_EW_LOOP(W)
-    {
+    const uint64_t stride = nb * kEwThreads * W;
+    for (uint64_t base = (bid * kEwThreads + threadIdx.x) * W; base < n; base += stride) {
         T wv[W], gv[W], p[W], r[W];
         load_lanes<T, VEC>(w, base, n, wv);
         load_lanes<T, VEC>(g, base, n, gv);
@@ -476,6 +494,38 @@ __global__ __launch_bounds__(kEwThreads) void k_sgd(const T *w,
         }
     }
     wave_record_fault(key, fault, gate);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_sgd(const T *w,
+                                                    const T *g, T rate,
+                                                    T *out, uint64_t n, int policy,
+                                                    unsigned long long *fault, NodeGate gate)
+{
+    sgd_range<T, VEC>(w, g, rate, out, n, policy, fault, gate, blockIdx.x, gridDim.x);
+}
+
+// Two updates of one program in one launch: blocks [0, blocks0) take update 0, the rest
+// update 1; each keeps its own fault word and gate.
+template <typename T> struct SgdPairArgs {
+    const T *w[2], *g[2];
+    T *out[2];
+    T rate[2];
+    uint64_t n[2];
+    unsigned long long *fault[2];
+    NodeGate gate[2];
+    unsigned blocks0;
+};
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_sgd_pair(SgdPairArgs<T> a, int policy)
+{
+    const bool first = blockIdx.x < a.blocks0;
+    const int u = first ? 0 : 1;
+    const uint64_t bid = first ? blockIdx.x : blockIdx.x - a.blocks0;
+    const uint64_t nb = first ? a.blocks0 : gridDim.x - a.blocks0;
+    sgd_range<T, VEC>(a.w[u], a.g[u], a.rate[u], a.out[u], a.n[u], policy, a.fault[u], a.gate[u],
+                      bid, nb);
 }
 
 // -------------------------------------------------------------------- MSE
@@ -1438,14 +1488,16 @@ __global__ __launch_bounds__(kSumThreads) __attribute__((amdgpu_waves_per_eu(4))
 }
 
 // Small inputs (n <= kMseSerialMax), one workgroup. Its four waves form every difference and
-// square in parallel into LDS and find the first faulting Subtract or Multiply; then one wave
-// folds the squares before that element into the total in order, 64 at a time, each lane
-// holding the chunk's squares in registers. The squares folded are finite, so a sum can only
-// fault by overflowing (the total turns, and stays, infinite) or, under RejectSubnormal, by
-// being subnormal: a chunk is folded with plain adds (under RejectSubnormal each partial
-// total is kept and checked after), and folded again with the exact add classifier only when
-// that trips. The same results and first fault as the pipeline above, in one launch and no
-// scratch.
+// square in parallel into LDS (each thread issues all of its loads before it computes, so
+// the inputs arrive in one round trip) and find the first faulting Subtract or Multiply; then
+// one wave folds the squares before that element into the total in order, a chunk of 60
+// (binary64 30) at a time, each lane holding the chunk's squares in registers and the next
+// chunk's loads in flight. The
+// squares folded are finite, so a sum can only fault by overflowing (the total turns, and
+// stays, infinite) or, under RejectSubnormal, by being subnormal: a chunk is folded with
+// plain adds (under RejectSubnormal each partial total is kept and checked after), and folded
+// again with the exact add classifier only when that trips. The same results and first fault
+// as the pipeline above, in one launch and no scratch.
 template <typename T, bool REJECT_SUB>
 __global__ __launch_bounds__(256) void k_mse_serial(const T *__restrict__ p, const T *__restrict__ t,
                                                     uint64_t n, T count, int policy,
@@ -1454,27 +1506,40 @@ __global__ __launch_bounds__(256) void k_mse_serial(const T *__restrict__ p, con
 {
     if (block_gate_closed(gate))
         return;
-    constexpr int P = 16 / sizeof(T); // squares per 16-byte LDS read
+    constexpr int P = 16 / sizeof(T);           // squares per 16-byte LDS read
+    constexpr int R = (int)(kMseSerialMax / 256); // elements a thread
     __shared__ __align__(16) T sq[kMseSerialMax];
     __shared__ unsigned long long first_sm; // earliest Subtract or Multiply fault word
     const int tid = threadIdx.x;
     if (tid == 0)
         first_sm = kNoFault;
+    T pv[R], tv[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const uint64_t i = (uint64_t)tid + 256u * (uint64_t)j;
+        if (i < n) {
+            pv[j] = p[i];
+            tv[j] = t[i];
+        }
+    }
     __syncthreads();
     uint64_t key = kNoFault;
-    for (uint64_t i = tid; i < n; i += 256) {
-        const T pv = p[i], tv = t[i];
-        const T d = pv - tv;
-        const T s = d * d;
-        sq[i] = s;
-        if (key == kNoFault) {
-            const uint32_t ks = classify_add(pv, tv, d, policy);
-            if (ks != kOk) {
-                key = pack_fault(3 * i, ks);
-            } else {
-                const uint32_t km = classify_mul(d, d, s, policy);
-                if (km != kOk)
-                    key = pack_fault(3 * i + 1, km);
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const uint64_t i = (uint64_t)tid + 256u * (uint64_t)j;
+        if (i < n) {
+            const T d = pv[j] - tv[j];
+            const T s = d * d;
+            sq[i] = s;
+            if (key == kNoFault) {
+                const uint32_t ks = classify_add(pv[j], tv[j], d, policy);
+                if (ks != kOk) {
+                    key = pack_fault(3 * i, ks);
+                } else {
+                    const uint32_t km = classify_mul(d, d, s, policy);
+                    if (km != kOk)
+                        key = pack_fault(3 * i + 1, km);
+                }
             }
         }
     }
@@ -1492,47 +1557,81 @@ __global__ __launch_bounds__(256) void k_mse_serial(const T *__restrict__ p, con
         }
     };
     T total = (T)0;
-    for (uint64_t i0 = 0; i0 < limit; i0 += 64) {
-        const int here = limit - i0 < 64 ? (int)(limit - i0) : 64;
+    // The exact pass over squares i0 .. i0 + here - 1 from `total`: false when an add faults
+    // (recorded).
+    auto exact = [&](uint64_t i0, int here) {
+        T tot = total;
+        for (int j = 0; j < here; j++) {
+            const T sj = sq[i0 + j];
+            const T nxt = tot + sj;
+            const uint32_t k_add = classify_add(tot, sj, nxt, policy);
+            if (k_add != kOk) {
+                record(pack_fault(3 * (i0 + j) + 2, k_add));
+                return false;
+            }
+            tot = nxt;
+        }
+        return true;
+    };
+    // A chunk is 15 LDS reads: with the next chunk's 15 reads issued before its adds, the
+    // wait for this chunk (in-order LDS counter, at most 15 outstanding) leaves all of them in
+    // flight.
+    constexpr int CH = 15 * P;
+    auto load = [&](T (&v)[CH], uint64_t i0) {
+#pragma unroll
+        for (int q = 0; q < CH / P; q++)
+            *reinterpret_cast<uint4 *>(&v[P * q]) = *reinterpret_cast<const uint4 *>(&sq[i0 + P * q]);
+    };
+    // Folds a whole chunk held in v; false when an add faults (recorded).
+    auto fold = [&](T (&v)[CH], uint64_t i0) __attribute__((always_inline)) {
         T sum = total;
         bool trip = false;
-        if (here == 64) {
-            T v[64];
+        if constexpr (!REJECT_SUB) {
 #pragma unroll
-            for (int q = 0; q < 64 / P; q++)
-                *reinterpret_cast<uint4 *>(&v[P * q]) = *reinterpret_cast<const uint4 *>(&sq[i0 + P * q]);
-            if constexpr (!REJECT_SUB) {
-#pragma unroll
-                for (int j = 0; j < 64; j++)
-                    sum = sum + v[j];
-            } else {
-#pragma unroll
-                for (int j = 0; j < 64; j++) {
-                    sum = sum + v[j];
-                    v[j] = sum;
-                }
-#pragma unroll
-                for (int j = 0; j < 64; j++)
-                    trip |= subnormal(v[j]);
-            }
+            for (int j = 0; j < CH; j++)
+                sum = sum + v[j];
         } else {
-            for (int j = 0; j < here; j++) {
-                sum = sum + sq[i0 + j];
-                trip |= REJECT_SUB && subnormal(sum);
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                sum = sum + v[j];
+                v[j] = sum;
             }
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+                trip |= subnormal(v[j]);
         }
-        if (!finite_bits(sum) || trip) {
-            for (int j = 0; j < here; j++) {
-                const T sj = sq[i0 + j];
-                const T nxt = total + sj;
-                const uint32_t k_add = classify_add(total, sj, nxt, policy);
-                if (k_add != kOk) {
-                    record(pack_fault(3 * (i0 + j) + 2, k_add));
-                    return;
-                }
-                total = nxt;
-            }
+        if ((!finite_bits(sum) || trip) && !exact(i0, CH))
+            return false;
+        total = sum;
+        return true;
+    };
+    const uint64_t full = limit / CH * CH;
+    T va[CH], vb[CH];
+    if (full > 0)
+        load(va, 0);
+    for (uint64_t i0 = 0; i0 < full; i0 += 2 * CH) {
+        const bool second = i0 + CH < full;
+        if (second)
+            load(vb, i0 + CH);
+        if (!fold(va, i0))
+            return;
+        if (!second)
+            break;
+        if (i0 + 2 * CH < full)
+            load(va, i0 + 2 * CH);
+        if (!fold(vb, i0 + CH))
+            return;
+    }
+    if (limit > full) {
+        const int here = (int)(limit - full);
+        T sum = total;
+        bool trip = false;
+        for (int j = 0; j < here; j++) {
+            sum = sum + sq[full + j];
+            trip |= REJECT_SUB && subnormal(sum);
         }
+        if ((!finite_bits(sum) || trip) && !exact(full, here))
+            return;
         total = sum;
     }
     if (fsm != kNoFault) {
@@ -1817,6 +1916,43 @@ hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const
         return hipSuccess;
     return dtype == 0 ? sgd_t<float>(s, n, w, g, (float)rate, out, policy, fault, gate)
                       : sgd_t<double>(s, n, w, g, rate, out, policy, fault, gate);
+}
+
+template <typename T>
+static hipError_t sgd_pair_t(hipStream_t s, const SgdJob &j0, const SgdJob &j1, int policy)
+{
+    constexpr int Wd = Vec<T>::width;
+    const SgdJob *j[2] = {&j0, &j1};
+    bool vec = true;
+    for (int u = 0; u < 2; u++)
+        vec = vec && aligned16(j[u]->w) && aligned16(j[u]->g) && aligned16(j[u]->out);
+    SgdPairArgs<T> a;
+    unsigned blocks[2];
+    for (int u = 0; u < 2; u++) {
+        a.w[u] = (const T *)j[u]->w;
+        a.g[u] = (const T *)j[u]->g;
+        a.out[u] = (T *)j[u]->out;
+        a.rate[u] = (T)j[u]->rate;
+        a.n[u] = j[u]->n;
+        a.fault[u] = j[u]->fault;
+        a.gate[u] = j[u]->gate;
+        // grid_for caps each at 2^24 blocks, so the sum fits a launch.
+        blocks[u] = grid_for(vec ? (j[u]->n + Wd - 1) / Wd : j[u]->n);
+    }
+    a.blocks0 = blocks[0];
+    const dim3 grid(blocks[0] + blocks[1]);
+    if (vec)
+        hipLaunchKernelGGL((k_sgd_pair<T, true>), grid, dim3(kEwThreads), 0, s, a, policy);
+    else
+        hipLaunchKernelGGL((k_sgd_pair<T, false>), grid, dim3(kEwThreads), 0, s, a, policy);
+    return hipGetLastError();
+}
+
+hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy)
+{
+    if (j0.n == 0 || j1.n == 0)
+        return hipErrorInvalidValue;
+    return dtype == 0 ? sgd_pair_t<float>(s, j0, j1, policy) : sgd_pair_t<double>(s, j0, j1, policy);
 }
 
 // Scratch of one MSE call: the squares, then the chunk sums and the chunk summaries.

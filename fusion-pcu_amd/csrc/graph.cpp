@@ -796,10 +796,37 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
             k += members.size();
         }
     }
+    sgd_partner.assign(n, UINT32_MAX);
+    sgd_second.assign(n, 0);
+    {
+        std::vector<uint32_t> run;
+        for (uint32_t i : order) {
+            const Op op = graph.nodes[i].op;
+            if (op != Op::Input && op != Op::Constant && op != Op::Uniform && fused_into[i] < 0 &&
+                !chain_member[i])
+                run.push_back(i);
+        }
+        auto strict_sgd = [&](uint32_t i) {
+            return graph.nodes[i].op == Op::SgdUpdate && route[i] == Route::Strict;
+        };
+        for (size_t k = 0; k + 1 < run.size(); k++) {
+            const uint32_t x = run[k], y = run[k + 1];
+            const Node &xn = graph.nodes[x], &yn = graph.nodes[y];
+            if (strict_sgd(x) && strict_sgd(y) && !sgd_second[x] && xn.dtype == yn.dtype &&
+                xn.policy == yn.policy && yn.a != x && yn.b != x && graph.elements(x) > 0 &&
+                graph.elements(y) > 0) {
+                sgd_partner[x] = y;
+                sgd_second[y] = 1;
+            }
+        }
+    }
     // The ordered MSE sum runs on the side stream when nothing in the plan consumes its
-    // value (the training-loss case): it then overlaps the backward pass.
+    // value (the training-loss case): it then overlaps the backward pass. A small one (one
+    // kernel of one workgroup) stays on the main stream: the fork and join cost the host
+    // more than the overlap saves.
     for (uint32_t i : order)
-        if (graph.nodes[i].op == Op::MeanSquaredError && uses[i] == 0 && route[i] == Route::Strict)
+        if (graph.nodes[i].op == Op::MeanSquaredError && uses[i] == 0 && route[i] == Route::Strict &&
+            graph.elements(graph.nodes[i].a) > kMseSerialMax)
             mse_side[i] = 1;
     // Device storage: one buffer per computed node; outputs get two banks so a faulting
     // execution never overwrites the published results. A Constant is uploaded once here
@@ -927,7 +954,7 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
         if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0 ||
-            chain_member[i])
+            chain_member[i] || sgd_second[i])
             continue;
         uint64_t n = graph.elements(i);
         int policy = nd.policy < 0 ? 0 : nd.policy;
@@ -1005,11 +1032,24 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
             prog_to_graph.push_back(i);
             break;
         case Op::SgdUpdate:
-            if (route[i] == Route::Native)
+            if (route[i] == Route::Native) {
                 st = ctx->op_native_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr,
                                         nd.options.precision == 1, ptr(i));
-            else
+            } else if (sgd_partner[i] != UINT32_MAX) {
+                const uint32_t j = sgd_partner[i];
+                const Node &jn = graph.nodes[j];
+                const uint64_t cnt[2] = {n, graph.elements(j)};
+                const void *const w[2] = {ptr(nd.a), ptr(jn.a)};
+                const void *const g[2] = {ptr(nd.b), ptr(jn.b)};
+                const float lr[2] = {nd.lr, jn.lr};
+                void *const out[2] = {ptr(i), ptr(j)};
+                st = ctx->op_sgd_pair(nd.dtype, cnt, w, g, lr, out, policy);
+                prog_to_graph.push_back(i);
+                prog_to_graph.push_back(j);
+                break;
+            } else {
                 st = ctx->op_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr, ptr(i), policy);
+            }
             prog_to_graph.push_back(i);
             break;
         default:

@@ -1371,24 +1371,43 @@ __global__ __launch_bounds__(256) void k_strict_gemm_fused(
     for (int k0 = 0; k0 < K; k0 += kFusedBK) {
         const int kc = K - k0 < kFusedBK ? K - k0 : kFusedBK;
         __syncthreads(); // the previous chunk is consumed
-        int ea = kExpNone, eb = kExpNone;
-        for (int k = ka; k < kc; k += 16) {
-            const int row = m0 + ra;
-            T v = (T)0;
-            if (row < M)
-                v = TA ? A[(size_t)(k0 + k) * M + row] : A[(size_t)row * K + k0 + k];
-            As[ra][k] = v;
-            const int e = ilog2_abs(v);
-            ea = e < ea ? e : ea;
+        // All of the thread's loads of the chunk are issued before any is used, so the chunk
+        // arrives in one round trip.
+        constexpr int L = kFusedBK / 16;
+        T va[L], vb[L];
+        const int row = m0 + ra, col = n0 + cb;
+#pragma unroll
+        for (int j = 0; j < L; j++) {
+            const int k = ka + 16 * j;
+            va[j] = (T)0;
+            if (k < kc && row < M)
+                va[j] = TA ? A[(size_t)(k0 + k) * M + row] : A[(size_t)row * K + k0 + k];
         }
-        for (int k = kb; k < kc; k += 16) {
-            const int col = n0 + cb;
-            T v = (T)0;
-            if (col < N)
-                v = TB ? B[(size_t)col * K + k0 + k] : B[(size_t)(k0 + k) * N + col];
-            Bs[cb][k] = v;
-            const int e = ilog2_abs(v);
-            eb = e < eb ? e : eb;
+#pragma unroll
+        for (int j = 0; j < L; j++) {
+            const int k = kb + 16 * j;
+            vb[j] = (T)0;
+            if (k < kc && col < N)
+                vb[j] = TB ? B[(size_t)col * K + k0 + k] : B[(size_t)(k0 + k) * N + col];
+        }
+        int ea = kExpNone, eb = kExpNone;
+#pragma unroll
+        for (int j = 0; j < L; j++) {
+            const int k = ka + 16 * j;
+            if (k < kc) {
+                As[ra][k] = va[j];
+                const int e = ilog2_abs(va[j]);
+                ea = e < ea ? e : ea;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < L; j++) {
+            const int k = kb + 16 * j;
+            if (k < kc) {
+                Bs[cb][k] = vb[j];
+                const int e = ilog2_abs(vb[j]);
+                eb = e < eb ? e : eb;
+            }
         }
         if (ea < kExpNone)
             atomicMin(&rexp[ra], ea);

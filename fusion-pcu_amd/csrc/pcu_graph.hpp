@@ -100,6 +100,10 @@ struct Prepared {
     std::vector<uint32_t> chain_next;
     std::vector<int> chain_len;
     std::vector<char> chain_member, chain_store;
+    // Consecutive strict SGD updates of one dtype and policy, the second not reading the
+    // first, run as one launch: sgd_partner[first] = second, sgd_second[second] = 1.
+    std::vector<uint32_t> sgd_partner;
+    std::vector<char> sgd_second;
     std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
     std::vector<void *> constant_buf; // resident copy of each planned Constant, uploaded at build

@@ -31,6 +31,17 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                            unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
                       double rate, void *out, int policy, unsigned long long *fault, NodeGate gate);
+// Two strict SGD updates of one dtype and policy in one launch, each with its own fault word
+// and gate (both counts nonzero).
+struct SgdJob {
+    const void *w, *g;
+    void *out;
+    uint64_t n;
+    double rate;
+    unsigned long long *fault;
+    NodeGate gate;
+};
+hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy);
 
 // A chain of elementwise nodes (checked binary, ReLU, ReLU backward) evaluated in one pass:
 // each step takes the value of the step before it (the first takes `head`) and, for a binary

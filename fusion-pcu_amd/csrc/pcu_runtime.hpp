@@ -155,6 +155,10 @@ struct Ctx {
     pcu_status op_chain(int dtype, uint64_t n, ChainLaunch chain);
     pcu_status op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate, void *out,
                       int policy);
+    // Two updates of one dtype and policy, each its own node, in one launch.
+    pcu_status op_sgd_pair(int dtype, const uint64_t n[2], const void *const w[2],
+                           const void *const g[2], const float rate[2], void *const out[2],
+                           int policy);
     pcu_status op_mse(int dtype, uint64_t n, const void *p, const void *t, void *out, int policy,
                       bool on_side);
     pcu_status op_native_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,

@@ -942,23 +942,59 @@ pcu_status Ctx::op_add_relu(int dtype, uint64_t n, const void *a, const void *b,
 
 // The F64 rate is the exact widening of the F32 literal (reference.rs:507-514); a float
 // converts to double exactly.
-pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
-                       void *out, int policy)
+static bool sgd_args_ok(Ctx *c, int dtype, uint64_t n, const void *w, const void *g, float rate,
+                        void *out, int policy)
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || (n && (!w || !g || !out))) {
-        fail("strict_sgd: invalid argument");
-        return PCU_ERR_ARGUMENT;
+        c->fail("strict_sgd: invalid argument");
+        return false;
     }
     if (partial_overlap(out, w, n * dsize(dtype)) || partial_overlap(out, g, n * dsize(dtype))) {
-        fail("strict_sgd: the output partly overlaps an operand");
-        return PCU_ERR_ARGUMENT;
+        c->fail("strict_sgd: the output partly overlaps an operand");
+        return false;
     }
     uint32_t rb;
     memcpy(&rb, &rate, 4);
     if ((rb & 0x7f800000u) == 0x7f800000u) {
-        fail("strict_sgd: learning rate must be finite (TensorError::InvalidLearningRate)");
-        return PCU_ERR_ARGUMENT;
+        c->fail("strict_sgd: learning rate must be finite (TensorError::InvalidLearningRate)");
+        return false;
     }
+    return true;
+}
+
+pcu_status Ctx::op_sgd_pair(int dtype, const uint64_t n[2], const void *const w[2],
+                            const void *const g[2], const float rate[2], void *const out[2],
+                            int policy)
+{
+    if (n[0] == 0 || n[1] == 0) {
+        // An empty update launches nothing: the two go alone.
+        pcu_status st = op_sgd(dtype, n[0], w[0], g[0], rate[0], out[0], policy);
+        return st ? st : op_sgd(dtype, n[1], w[1], g[1], rate[1], out[1], policy);
+    }
+    for (int u = 0; u < 2; u++)
+        if (!sgd_args_ok(this, dtype, n[u], w[u], g[u], rate[u], out[u], policy))
+            return PCU_ERR_ARGUMENT;
+    unsigned long long *word[2];
+    pcu_status st;
+    for (int u = 0; u < 2; u++)
+        if ((st = add_node(NodeInfo{Prim::Sgd, n[u], 0}, &word[u])))
+            return st;
+    if ((st = open_words()))
+        return st;
+    SgdJob j[2];
+    for (int u = 0; u < 2; u++)
+        j[u] = SgdJob{w[u], g[u], out[u], n[u], (double)rate[u], word[u], gate_for(word[u])};
+    hipEvent_t t = timer_start(stream);
+    st = hip(launch_sgd_pair(stream, dtype, j[0], j[1], policy), "strict_sgd launch");
+    timer_stop(PCU_KERNEL_SGD, t, stream);
+    return st;
+}
+
+pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
+                       void *out, int policy)
+{
+    if (!sgd_args_ok(this, dtype, n, w, g, rate, out, policy))
+        return PCU_ERR_ARGUMENT;
     unsigned long long *word;
     pcu_status st = add_node(NodeInfo{Prim::Sgd, n, 0}, &word);
     if (st)

@@ -344,3 +344,54 @@ def test_constant_through_the_facade(G):
     want, f3 = oracle.relu(s)
     assert f1 is None and f2 is None and f3 is None
     np.testing.assert_array_equal(_bits(got).reshape(-1), _bits(want))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_paired_sgd_updates_fault_order(G, pcu_pkg, dtype):
+    """Two consecutive strict SGD updates of a prepared graph run as one launch, each with
+    its own fault word: with a fault planted in the first update, the second, both or
+    neither (odd and 16-byte-multiple sizes), the outputs, or the first faulting node and its
+    coordinates, match the oracle's ordered graph."""
+    big = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    ctx = G.default_context()
+    rng = np.random.default_rng(23)
+    for n1, n2 in ((37, 1000), (4096, 8192), (5, 3)):
+        g = G.Graph()
+        g.set_numerical_mode(True)
+        w1, g1 = g.input((n1,), dtype), g.input((n1,), dtype)
+        w2, g2 = g.input((n2,), dtype), g.input((n2,), dtype)
+        outs = [g.sgd_update(w1, g1, 4.0), g.sgd_update(w2, g2, 0.5)]
+        prep = g.prepare(ctx, outs)
+        ref = og.Graph()
+        ref.mode = "Strict"
+        r1, rg1 = ref.input((n1,), dtype), ref.input((n1,), dtype)
+        r2, rg2 = ref.input((n2,), dtype), ref.input((n2,), dtype)
+        routs = [ref.sgd_update(r1, rg1, 4.0), ref.sgd_update(r2, rg2, 0.5)]
+        for plant in ("none", "first", "second", "both"):
+            a1, b1 = rng.uniform(-1, 1, n1).astype(dtype), rng.uniform(-1, 1, n1).astype(dtype)
+            a2, b2 = rng.uniform(-1, 1, n2).astype(dtype), rng.uniform(-1, 1, n2).astype(dtype)
+            if plant in ("first", "both"):
+                b1[n1 // 2] = big  # 4 x big overflows in the first update's Multiply
+            if plant in ("second", "both"):
+                a2[n2 - 1] = -big
+                b2[n2 - 1] = big  # -big - 0.5 big overflows in the second update's Subtract
+            vals, rf = ref.evaluate({r1: a1, rg1: b1, r2: a2, rg2: b2}, routs)
+            assert (rf is None) == (plant == "none"), (plant, rf)
+            dev = {w1: ctx.upload(a1), g1: ctx.upload(b1), w2: ctx.upload(a2), g2: ctx.upload(b2)}
+            try:
+                if rf is None:
+                    prep.execute([dev[i].ptr for i in prep.input_ids])
+                    for k, want in enumerate(routs):
+                        d = prep.output_desc[k]
+                        have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(k), d["shape"], d["dtype"]).numpy()
+                        np.testing.assert_array_equal(_bits(have), _bits(vals[want]))
+                else:
+                    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                        prep.execute([dev[i].ptr for i in prep.input_ids])
+                    tf = exc.value.tensor_fault
+                    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                         rf.fault.kind), (n1, n2, plant)
+            finally:
+                for d in dev.values():
+                    d.free()
