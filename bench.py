@@ -479,8 +479,9 @@ def cpu_fast_oracle(m, k, n, seconds=5.0):
 def probe(pkg, M, K, N) -> int:
     """One launch of each kernel whose counters are read with rocprofv3 --pmc: the strict
     F32 MatMul 4096^3 (both engines), a copy-like calibration kernel (checked Add of +0 over
-    2^26 f32: 256 MiB read + 256 MiB written), strict SGD over 2^26 f32 and the strict F64
-    MatMul 4096^3 (after one warm-up launch)."""
+    2^26 f32: 256 MiB read + 256 MiB written), the direct-load calibration copy (256 MiB
+    read with global_load_lds_dwordx4, 256 MiB written), strict SGD over 2^26 f32 and the
+    strict F64 MatMul 4096^3 (after one warm-up launch)."""
     from fusion_pcu_amd import synthetic as syn
     n = 1 << 26
     with pkg.Context(0) as ctx:
@@ -494,9 +495,11 @@ def probe(pkg, M, K, N) -> int:
         ctx.strict_matmul(da, db, out=dc)
         ctx.checked_binary(0, x, 0.0, out=y)
         ctx.strict_sgd(x, g, 0.01, out=y)
+        ctx.calibrate_direct_copy(x, y)
         log("probe: one launch each (MatMul: matrix-core products, then vector-unit engine)")
         ctx.strict_matmul(da, db, out=dc)
         ctx.checked_binary(0, x, 0.0, out=y)
+        ctx.calibrate_direct_copy(x, y)
         ctx.strict_sgd(x, g, 0.01, out=y)
         ctx.set_matmul_engine("valu")
         ctx.strict_matmul(da, db, out=dc)

@@ -296,6 +296,14 @@ class Context:
                                               ctypes.byref(ms), ctypes.byref(n)))
         return float(ms.value), int(n.value)
 
+    def calibrate_direct_copy(self, src: "DeviceArray", dst: "DeviceArray") -> None:
+        """Measurement aid: copy src into dst (same byte size, a multiple of 4 KiB) reading
+        with the direct global-to-LDS load of the matrix-core MatMul tiles (see
+        pcu_calibrate_direct_copy); synchronizes."""
+        if src.nbytes != dst.nbytes:
+            raise PcuExecutionError(_abi.PCU_ERR_SHAPE, "calibration copy: sizes differ")
+        self.check(self._lib.pcu_calibrate_direct_copy(self.handle, src.ptr, dst.ptr, src.nbytes))
+
     # ------------------------------------------------------------------- ops
     def _call(self, fn, *args) -> None:
         f = _abi.Fault()

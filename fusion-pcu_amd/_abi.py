@@ -85,6 +85,7 @@ SIGNATURES = {
     "pcu_elapsed_ms": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_float)]),
     "pcu_profile_enable": (_i32, [_vp, _i32]),
     "pcu_profile_read": (_i32, [_vp, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]),
+    "pcu_calibrate_direct_copy": (_i32, [_vp, _vp, _vp, ctypes.c_uint64]),
 }
 
 

@@ -751,6 +751,37 @@ __global__ __launch_bounds__(1024, 2) void k_strict_gemm_mfma16(
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Measurement aid: a copy of known traffic whose reads are global_load_lds_dwordx4, the load
+// the whole matrix-core tiles stage with, so that the HBM read counter can be scaled for
+// that load (it is scaled for ordinary loads by a copy kernel of ordinary loads). Each
+// workgroup moves 4 KiB chunks: wave w loads bytes 1024 w .. 1024 w + 1023 of the chunk
+// into its own LDS kilobyte, waits for it, and each lane stores its 16 bytes with an ordinary
+// 16-byte store.
+__global__ __launch_bounds__(256) void k_direct_copy(const float *src, float *dst, uint64_t chunks)
+{
+    __shared__ __align__(16) float buf[1024];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    for (uint64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const float *g = src + c * 1024 + (uint64_t)wave * 256;
+        load_lds16(g, (uint32_t)lane * 16u, buf + wave * 256);
+        wait_lds_loads();
+        const float4 v = *reinterpret_cast<const float4 *>(buf + wave * 256 + lane * 4);
+        // The store consumes the LDS read, so the read has completed before the wave's next
+        // direct load (an asm statement with a memory clobber) overwrites the kilobyte.
+        *reinterpret_cast<float4 *>(dst + c * 1024 + (uint64_t)wave * 256 + lane * 4) = v;
+    }
+}
+
+hipError_t launch_direct_copy(hipStream_t s, const void *src, void *dst, uint64_t bytes)
+{
+    if (bytes == 0 || bytes % 4096 != 0 || !aligned16(src) || !aligned16(dst))
+        return hipErrorInvalidValue;
+    const uint64_t chunks = bytes / 4096;
+    const unsigned grid = (unsigned)(chunks < 8192 ? chunks : 8192);
+    hipLaunchKernelGGL(k_direct_copy, dim3(grid), dim3(256), 0, s, (const float *)src, (float *)dst, chunks);
+    return hipGetLastError();
+}
+
 template <class Cfg, bool TA, bool TB>
 static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
                           int K, const unsigned long long *re, const unsigned long long *ce,

@@ -41,6 +41,9 @@ struct SgdJob {
     unsigned long long *fault;
     NodeGate gate;
 };
+// Measurement aid: copy `bytes` (a multiple of 4 KiB, 16-byte-aligned pointers) reading
+// with global_load_lds_dwordx4 and writing with ordinary stores.
+hipError_t launch_direct_copy(hipStream_t s, const void *src, void *dst, uint64_t bytes);
 hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy);
 
 // A chain of elementwise nodes (checked binary, ReLU, ReLU backward) evaluated in one pass:

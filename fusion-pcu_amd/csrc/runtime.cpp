@@ -1515,6 +1515,26 @@ pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t
     return PCU_OK;
 }
 
+pcu_status pcu_calibrate_direct_copy(pcu_ctx *ctx, const void *src, void *dst, uint64_t bytes)
+{
+    if (!ctx)
+        return bad_ctx();
+    Ctx *c = reinterpret_cast<Ctx *>(ctx);
+    if (c->in_program) {
+        c->fail("calibration copy inside a program");
+        return PCU_ERR_STATE;
+    }
+    if (!src || !dst || bytes == 0 || bytes % 4096 != 0 || ((uintptr_t)src & 15u) ||
+        ((uintptr_t)dst & 15u) || pcu::ranges_overlap(dst, bytes, src, bytes)) {
+        c->fail("calibration copy: invalid argument");
+        return PCU_ERR_ARGUMENT;
+    }
+    pcu_status st = c->hip(pcu::launch_direct_copy(c->stream, src, dst, bytes), "calibration copy launch");
+    if (st)
+        return st;
+    return c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
 pcu_status pcu_mark(pcu_ctx *ctx, int slot)
 {
     if (!ctx)

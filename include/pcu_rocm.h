@@ -280,6 +280,14 @@ typedef enum pcu_kernel_id {
 pcu_status pcu_profile_enable(pcu_ctx *ctx, int on);
 pcu_status pcu_profile_read(pcu_ctx *ctx, int kernel, double *total_ms, uint64_t *launches);
 
+/* Measurement aid with no counterpart in the reference: copies `bytes` (a nonzero multiple
+ * of 4096; both pointers 16-byte aligned; no overlap) from src to dst, reading with the
+ * direct global-to-LDS load (global_load_lds_dwordx4) that the matrix-core MatMul tiles
+ * stage with and writing with ordinary stores, then synchronizes. Hardware read counters of
+ * one launch of known traffic scale those of the MatMul kernels' direct loads.
+ * PCU_ERR_ARGUMENT for an invalid size, alignment or overlap. */
+pcu_status pcu_calibrate_direct_copy(pcu_ctx *ctx, const void *src, void *dst, uint64_t bytes);
+
 /* -------------------------------------------------------------------- graph
  * Host mirror of the reference's tensor Graph for the strict path: the builder calls
  * (core/dialect/tensor.rs:4028-4329), reverse mode for an MSE root

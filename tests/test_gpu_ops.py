@@ -1052,3 +1052,22 @@ def test_matmul_f64_full_grid_tile(ctx, pcu_pkg, shape):
                 assert gf == _ofault(rf), (shape, tl, tr, plant, gf, rf)
                 if rf is None:
                     np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{shape} {tl} {tr}")
+
+
+def test_calibration_direct_copy(ctx, pcu_pkg):
+    """The measurement copy (direct global-to-LDS reads) moves every byte, and refuses sizes
+    that are not whole 4 KiB chunks."""
+    rng = np.random.default_rng(8)
+    for n in (1024, 1024 * 37, 1 << 22):
+        x = rng.standard_normal(n).astype(np.float32)
+        dx = ctx.upload(x)
+        dy = ctx.empty((n,), np.float32)
+        ctx.calibrate_direct_copy(dx, dy)
+        assert np.array_equal(dy.numpy().view(np.uint32), x.view(np.uint32))
+        dx.free()
+        dy.free()
+    dx, dy = ctx.upload(np.zeros(1000, np.float32)), ctx.empty((1000,), np.float32)
+    with pytest.raises(pcu_pkg.PcuExecutionError):
+        ctx.calibrate_direct_copy(dx, dy)
+    dx.free()
+    dy.free()
