@@ -91,7 +91,7 @@ template <typename T> struct ExpJob {
 constexpr uint64_t kSuperSlab = 64;
 
 // Rows job, block `bid`: one wave per row, four rows per 256-thread block; four 16-byte loads
-// per lane in flight.
+// per lane in flight (sixteen measured 3-6% slower over whole screens).
 template <typename T, bool VEC>
 __device__ __forceinline__ void exp_rows_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen)
 {
@@ -229,14 +229,15 @@ __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid,
     if (c0 < C) {
         uint64_t r = r0 + ry;
         if (VEC) {
-            // Four rows per step: four 16-byte loads per thread in flight.
-            for (; r + 12 < r1; r += 16) {
-                uint4 q[4];
+            // All sixteen of the thread's rows at once: sixteen 16-byte loads in flight (four
+            // at a time measured 4-9% slower where both jobs are column jobs).
+            for (; r + 60 < r1; r += 64) {
+                uint4 q[16];
 #pragma unroll
-                for (int u = 0; u < 4; u++)
+                for (int u = 0; u < 16; u++)
                     q[u] = *reinterpret_cast<const uint4 *>(X + (r + 4 * u) * C + c0);
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
+                for (int u = 0; u < 16; u++) {
                     const T *v = reinterpret_cast<const T *>(&q[u]);
 #pragma unroll
                     for (int k = 0; k < P; k++) {
