@@ -1758,15 +1758,18 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         return hipGetLastError();
     }
     // The superslab tables let the tiny scan read only the runs of k where a product below
-    // 2^tiny_thr is possible; the screen fills them under RejectSubnormal (where the scan runs
-    // whenever a tile is marked).
-    const bool tables = sum_check && sc.tbl_a != nullptr;
+    // 2^tiny_thr is possible; the screen fills them wherever the scan may run (IEEE, and
+    // RejectSubnormal with the partial-sum check). On a clean input they cost the screen
+    // about 1.5 us at 4096^3; on a fully marked one they cut the scan from 0.84 to 0.17 ms.
+    const bool tables = sc.tbl_a != nullptr && (policy == kPolicyIeee || sum_check);
     ScanTables tbls;
     if (tables) {
         tbls.a = sc.tbl_a;
         tbls.b = sc.tbl_b;
         tbls.a_xmajor = !ta; // a rows job over A (M x K), else a columns job over A (K x M)
         tbls.b_xmajor = tb;  // a rows job over B (N x K), else a columns job over B (K x N)
+    }
+    if (tables && sum_check) {
         // The checking tiles check only the superslabs that need it (the tables describe
         // op(B) as stored, also when the tile kernel reads its K x N copy).
         sck.tbl_a = tbls.a;

@@ -750,9 +750,10 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     }
     // The fixed array has no partial-sum block words and no superslab tables: under
     // RejectSubnormal the no-allocation call walks every cell its exponents mark. The tables
-    // only speed the tiny scan up, so a table buffer that cannot be had is left out.
+    // only speed the tiny scan up (IEEE and RejectSubnormal), so a table buffer that cannot
+    // be had is left out.
     void *tables = nullptr;
-    if (!noalloc && policy == PCU_UNDERFLOW_REJECT_SUBNORMAL) {
+    if (!noalloc && policy != PCU_UNDERFLOW_ALLOW_GRADUAL) {
         const size_t tb = slab_table_bytes(rows, inner, cols);
         if (tb)
             tables = optional_scratch(table_scratch, tb);

@@ -227,3 +227,40 @@ def test_reject_subnormal_across_superslabs(ctx, pcu_pkg, shape):
                                                       err_msg=f"{name} {tl}{tr} {policy}")
     finally:
         ctx.set_matmul_engine("auto")
+
+
+@pytest.mark.parametrize("shape", DEEP, ids=IDS)
+def test_tiny_products_through_superslab_tables(ctx, pcu_pkg, shape):
+    """The tiny scan reads only the 64-k superslabs whose table minima allow a tiny product
+    (under IEEE and RejectSubnormal): an inexact tiny product planted in the first, a middle
+    or the last superslab, some behind an exact tiny product of the same cell in an earlier
+    superslab, under every transpose pair, against the oracle."""
+    m, k, n, dtype, engine = shape
+    ctx.set_matmul_engine(engine)
+    f32 = dtype == np.float32
+    half, ulp = (2.0 ** -70, 2.0 ** -23) if f32 else (2.0 ** -530, 2.0 ** -52)
+    rng = np.random.default_rng(11 * m + k + n)
+    cases = []
+    for k_exact, k_inexact in ((None, 5), (3, k // 2 + 7), (70, k - 2)):
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        r, c = int(rng.integers(m)), int(rng.integers(n))
+        if k_exact is not None:
+            a[r, k_exact] = dtype(half)  # half * half is an exact subnormal: no fault
+            b[k_exact, c] = dtype(half)
+        a[r, k_inexact] = dtype(half * (1 + ulp))  # half^2 (1 + ulp): tiny and inexact
+        b[k_inexact, c] = dtype(half)
+        cases.append((f"inexact-at-k{k_inexact}", a, b))
+    try:
+        for name, a, b in cases:
+            for tl, tr in ((False, False), (True, False), (False, True)):
+                aa = np.ascontiguousarray(a.T) if tl else a
+                bb = np.ascontiguousarray(b.T) if tr else b
+                for policy in (0, 1):
+                    ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+                    if policy == 0:
+                        assert rf is not None and rf.kind == 4, (name, rf)
+                    got, gf = _run(ctx, pcu_pkg, aa, bb, tl, tr, policy)
+                    assert gf == _of(rf), (name, tl, tr, policy, gf, rf)
+    finally:
+        ctx.set_matmul_engine("auto")
