@@ -264,3 +264,54 @@ def test_tiny_products_through_superslab_tables(ctx, pcu_pkg, shape):
                     assert gf == _of(rf), (name, tl, tr, policy, gf, rf)
     finally:
         ctx.set_matmul_engine("auto")
+
+
+FUZZ_FAMILIES = [  # (M, N, K choices, dtype, engine): each reaches one tile kernel
+    (2048, 2048, (64, 144, 256), np.float32, "mfma_products"),  # whole 128 x 128, three stages
+    (2100, 2000, (48, 200), np.float32, "mfma_products"),       # 128 x 128 with bound checks
+    (1024, 1024, (112, 256), np.float32, "mfma_products"),      # 16 x 16 waves, 64 x 64 tiles
+    (1000, 700, (40, 177), np.float32, "mfma_products"),        # 64 x 64 with bound checks
+    (640, 520, (96, 250), np.float32, "valu"),                  # vector-unit binary32
+    (2048, 2048, (80, 192), np.float64, "valu"),                # binary64 full grid
+]
+FUZZ_IDS = ["mfma128", "mfma128-ragged", "mfma16", "mfma64-ragged", "valu-f32", "valu-f64"]
+
+
+@pytest.mark.parametrize("family", FUZZ_FAMILIES, ids=FUZZ_IDS)
+def test_reject_subnormal_gating_fuzz(ctx, pcu_pkg, family):
+    """Seeded fuzz of the superslab-gated partial-sum check: per case one to three planted
+    cancellations at random k (either side of a superslab boundary), sometimes an off-grid
+    sum carried into a later superslab, and random tiny operands, under RejectSubnormal
+    (and IEEE for every other case), in random transpose pairs; bits and first fault
+    against the oracle."""
+    m, n, ks, dtype, engine = family
+    ctx.set_matmul_engine(engine)
+    f32 = dtype == np.float32
+    rng = np.random.default_rng(1000 + m + n + len(ks))
+    try:
+        for case in range(8):
+            k = int(ks[case % len(ks)])
+            a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+            b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+            if k >= 192 and rng.random() < 0.5:
+                _plant_carried(a, b, int(rng.integers(m)), int(rng.integers(n)), 150, dtype,
+                               bool(rng.random() < 0.5))
+            for _ in range(int(rng.integers(1, 4))):
+                k1 = int(rng.integers(0, k - 1))
+                k2 = int(rng.integers(k1 + 1, k))
+                _plant_cancellation(a, b, int(rng.integers(m)), int(rng.integers(n)), k1, k2, dtype)
+            for _ in range(int(rng.integers(0, 3))):
+                e = int(rng.integers(-150, -100)) if f32 else int(rng.integers(-1070, -960))
+                a[int(rng.integers(m)), int(rng.integers(k))] = dtype(2.0 ** e * rng.uniform(1, 2))
+            tl, tr = bool(rng.random() < 0.4), bool(rng.random() < 0.4)
+            aa = np.ascontiguousarray(a.T) if tl else a
+            bb = np.ascontiguousarray(b.T) if tr else b
+            for policy in ((1, 0) if case % 2 else (1,)):
+                ref, rf = oracle.matmul(aa, bb, tl, tr, policy=policy)
+                got, gf = _run(ctx, pcu_pkg, aa, bb, tl, tr, policy)
+                assert gf == _of(rf), (case, k, tl, tr, policy, gf, rf)
+                if rf is None:
+                    np.testing.assert_array_equal(_bits(got), _bits(ref),
+                                                  err_msg=f"case {case} k {k} {tl}{tr} {policy}")
+    finally:
+        ctx.set_matmul_engine("auto")
