@@ -2,8 +2,8 @@
 
 Headline (BASELINE.json `metric`): strict F32 MatMul 4096^3, A and B uniform[-1,1]
 (seeded), inputs resident in HBM. One step = one complete strict MatMul call through the C
-ABI: exponent prefilter, main tile kernel, exact-replay check and the terminal fault-word
-readback. `value` is GFLOP/s = 2*M*N*K / step time. The dominant kernel's live duration
+ABI: exponent screen, main tile kernel, tiny-product scan, exact-replay check and the
+terminal fault-word publication. `value` is GFLOP/s = 2*M*N*K / step time. The dominant kernel's live duration
 (HIP events on its own stream) gives the roofline; `cpu_baseline` times the faithful
 single-thread CPU port of the reference's integer-law MatMul on a bounded row sample.
 
@@ -51,7 +51,7 @@ def log(msg: str) -> None:
 
 def _abi_matmul_call(ctx, da, db, dc, m, k, n, policy=0):
     """A zero-argument callable making one complete strict MatMul call straight through the
-    C ABI (launches and fault readback); it returns the call's status, so a fault variant
+    C ABI (launches and fault-word publication); it returns the call's status, so a fault variant
     returns PCU_ARITHMETIC_FAULT without a Python exception in the timed loop. The argument
     list and the fault record are built once, so the loop times the call itself."""
     import ctypes
@@ -634,7 +634,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (SplitMix64 uniform[-1,1], seeds 11/12)",
         "config": {"workload": "strict F32 MatMul 4096x4096x4096 (A,B uniform[-1,1]); one step = "
-                               "prefilter + tile kernel + replay check + fault readback; timed "
+                               "exponent screen + tile kernel + tiny scan + replay check + "
+                               "fault-word publication; timed "
                                "with per-kernel timing off (the roofline's kernel duration comes "
                                "from a second, timed pass)",
                    "m": M, "k": K, "n": N,

@@ -2,9 +2,11 @@
 //
 // Execution model: one ordered HIP stream per context. Every op enqueues its kernels and
 // records into its own 64-bit fault word (node-indexed array in device memory, filled
-// with the no-fault sentinel when a program begins). A program ends with one stream
-// synchronization and one device-to-host copy of the used fault words; the first word
-// holding a fault in node order is decoded into TensorError coordinates. This replaces the
+// with the no-fault sentinel by a program's first kernel unless the previous program ended
+// clean). A program ends with one kernel that copies the used fault words and a sequence
+// number into coherent pinned host memory, and the host spins on that sequence word; the
+// first word holding a fault in node order is decoded into TensorError coordinates. This
+// replaces the
 // reference's per-node sentinel upload, launch, event wait and 8-byte readback
 // (backends/rocm/owned_dispatch.rs:1137-1204, 1556-1580).
 #include "pcu_runtime.hpp"
