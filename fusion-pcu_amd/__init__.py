@@ -135,6 +135,17 @@ class DeviceArray:
         self.shape = tuple(int(s) for s in shape)
         self.dtype = np.dtype(dtype)
 
+    @classmethod
+    def _of(cls, ctx: "Context", ptr: int, shape: Tuple[int, ...], dtype: np.dtype) -> "DeviceArray":
+        """Wrap a pointer whose shape (a tuple of ints) and dtype (a numpy dtype) are already
+        normalized: the per-call path of prepared programs."""
+        a = cls.__new__(cls)
+        a.ctx = ctx
+        a.ptr = ptr
+        a.shape = shape
+        a.dtype = dtype
+        return a
+
     @property
     def size(self) -> int:
         return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1

@@ -206,6 +206,14 @@ class Prepared:
             ctx.check(self._lib.pcu_prepared_input_id(h, i, ctypes.byref(v)))
             self.input_ids.append(int(v.value))
         self.output_desc = [graph.describe(o) for o in self.outputs]
+        # Reused per call: the pointer array, the fault record and the outputs' shapes.
+        self._ptr_arrays = {}
+        self._fault = _abi.Fault()
+        self._fault_ref = ctypes.byref(self._fault)
+        self._out_meta = [(tuple(int(x) for x in d["shape"]), np.dtype(d["dtype"]))
+                          for d in self.output_desc]
+        self._take = ctypes.c_void_p()
+        self._take_ref = ctypes.byref(self._take)
 
     def __del__(self):
         try:
@@ -217,9 +225,14 @@ class Prepared:
 
     def execute(self, device_ptrs: Sequence[int]) -> None:
         """Run once; on a fault raise PcuExecutionError (nothing is published)."""
-        arr = (ctypes.c_void_p * max(1, len(device_ptrs)))(*device_ptrs)
-        f = _abi.Fault()
-        st = self._lib.pcu_prepared_execute(self.handle, len(device_ptrs), arr, ctypes.byref(f))
+        n = len(device_ptrs)
+        arr = self._ptr_arrays.get(n)
+        if arr is None:
+            arr = self._ptr_arrays[n] = (ctypes.c_void_p * max(1, n))()
+        for i, p in enumerate(device_ptrs):
+            arr[i] = p
+        f = self._fault
+        st = self._lib.pcu_prepared_execute(self.handle, n, arr, self._fault_ref)
         if st == _abi.PCU_ARITHMETIC_FAULT:
             tf = CompoundFault(int(f.node), int(f.element_index), int(f.reduction_index),
                                TensorArithmeticStep(int(f.step)), PcuExecutionFaultKind(int(f.kind)))
@@ -230,10 +243,9 @@ class Prepared:
         return self._lib.pcu_prepared_output(self.handle, index) or 0
 
     def take_output(self, index: int) -> "PcuTensor":
-        p = ctypes.c_void_p()
-        self.ctx.check(self._lib.pcu_prepared_take_output(self.handle, index, ctypes.byref(p)))
-        d = self.output_desc[index]
-        return PcuTensor(DeviceArray(self.ctx, p.value, d["shape"], d["dtype"]), owned=True)
+        self.ctx.check(self._lib.pcu_prepared_take_output(self.handle, index, self._take_ref))
+        shape, dtype = self._out_meta[index]
+        return PcuTensor(DeviceArray._of(self.ctx, self._take.value, shape, dtype), owned=True)
 
 
 # ------------------------------------------------------------ owners and values
@@ -449,9 +461,10 @@ class _Entry:
                     d = self.ctx.upload(np.ascontiguousarray(a))
                     staged.append(d)
                     by_node[node] = d.ptr
-            ptrs = [by_node[n] for n in self.prepared.input_ids]
-            self.prepared.execute(ptrs)
-            outs = tuple(self.prepared.take_output(i) for i in range(len(self.prepared.outputs)))
+            prep = self.prepared
+            prep.execute([by_node[n] for n in prep.input_ids])
+            take = prep.take_output
+            outs = tuple([take(i) for i in range(len(prep.outputs))])
         finally:
             for d in staged:
                 d.free()
@@ -474,10 +487,21 @@ def function(strict: bool = False, underflow: int = PcuFloatUnderflowPolicy.Ieee
 
         @functools.wraps(fn)
         def wrapper(*args):
-            ctx = default_context() if not any(isinstance(a, PcuTensor) for a in args) else \
-                next(a.array.ctx for a in args if isinstance(a, PcuTensor))
-            key = (id(ctx),) + tuple((tuple(np.shape(a)) if not isinstance(a, PcuTensor) else a.shape,
-                                      str(a.dtype)) for a in args)
+            # The cache key: the context and each argument's shape and dtype (dtype objects,
+            # not their names: formatting a dtype costs microseconds a call).
+            ctx = None
+            key = []
+            for a in args:
+                if isinstance(a, PcuTensor):
+                    if ctx is None:
+                        ctx = a.array.ctx
+                    key.append((a.array.shape, a.array.dtype))
+                else:
+                    arr = a if isinstance(a, np.ndarray) else np.asarray(a)
+                    key.append((arr.shape, arr.dtype))
+            if ctx is None:
+                ctx = default_context()
+            key = (id(ctx), tuple(key))
             entry = cache.get(key)
             if entry is None:
                 entry = _capture(fn, args, strict, int(underflow), ctx, options)

@@ -395,3 +395,55 @@ def test_paired_sgd_updates_fault_order(G, pcu_pkg, dtype):
             finally:
                 for d in dev.values():
                     d.free()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_mse_then_chain_fault_order(G, pcu_pkg, dtype):
+    """A serial MSE followed by an elementwise chain that the MSE does not feed (each node
+    with its own fault word): with a fault planted in the chain, in the MSE, in both or in
+    neither, at odd and whole sizes up to the serial limit, the outputs, or the first
+    faulting node and its coordinates, match the oracle's ordered graph."""
+    big = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    ctx = G.default_context()
+    rng = np.random.default_rng(31)
+    for n in (37, 1000, 4096):
+        g = G.Graph()
+        g.set_numerical_mode(True)
+        p, y = g.input((n,), dtype), g.input((n,), dtype)
+        q, r = g.input((n,), dtype), g.input((n,), dtype)
+        loss = g.mean_squared_error(p, y)
+        d = g.mul(g.sub(q, r), g.uniform((n,), dtype, 3.0))
+        out = g.relu(d)
+        outs = [loss, out]
+        prep = g.prepare(ctx, outs)
+        ref = og.Graph()
+        ref.mode = "Strict"
+        rp, ry, rq, rr = (ref.input((n,), dtype) for _ in range(4))
+        rloss = ref.mean_squared_error(rp, ry)
+        rout = ref.relu(ref.mul(ref.sub(rq, rr), ref.uniform((n,), dtype, 3.0)))
+        for plant in ("none", "chain", "mse", "both"):
+            a = [rng.uniform(-1, 1, n).astype(dtype) for _ in range(4)]
+            if plant in ("chain", "both"):
+                a[2][n // 3], a[3][n // 3] = big, -big  # q - r overflows in the Subtract
+            if plant in ("mse", "both"):
+                a[0][n - 1] = np.nan  # the MSE's Subtract is invalid at its last element
+            vals, rf = ref.evaluate({rp: a[0], ry: a[1], rq: a[2], rr: a[3]}, [rloss, rout])
+            assert (rf is None) == (plant == "none"), (plant, rf)
+            dev = {p: ctx.upload(a[0]), y: ctx.upload(a[1]), q: ctx.upload(a[2]), r: ctx.upload(a[3])}
+            try:
+                if rf is None:
+                    prep.execute([dev[i].ptr for i in prep.input_ids])
+                    for k, want in enumerate((rloss, rout)):
+                        desc = prep.output_desc[k]
+                        have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(k), desc["shape"], desc["dtype"]).numpy()
+                        np.testing.assert_array_equal(_bits(have), _bits(vals[want]))
+                else:
+                    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                        prep.execute([dev[i].ptr for i in prep.input_ids])
+                    tf = exc.value.tensor_fault
+                    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                         rf.fault.kind), (n, plant)
+            finally:
+                for x in dev.values():
+                    x.free()
