@@ -173,7 +173,9 @@ pcu_status pcu_strict_matmul(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint6
  * cols are each at most PCU_NOALLOC_MAX_DIM; larger shapes return PCU_ERR_ARGUMENT. The
  * array (1.5 MiB + 256 B per device, held until the process ends) is shared by every call on
  * the device and keeps the last call's contents; the library clears what must start at zero.
- * Calls that overlap on one device (from two contexts or two host threads) race. */
+ * Calls that overlap on one device (from two contexts or two host threads) race. The array
+ * holds no partial-sum block flags, so under RejectSubnormal the call walks every cell the
+ * exponent screen marks (same results and first fault, slower on marked inputs). */
 #define PCU_NOALLOC_MAX_DIM 65536u
 pcu_status pcu_strict_matmul_noalloc(pcu_ctx *ctx, pcu_dtype dtype, uint64_t rows, uint64_t inner,
                                      uint64_t cols, int transpose_left, int transpose_right,
