@@ -820,6 +820,54 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
             }
         }
     }
+    gemm_epi.assign(n, UINT32_MAX);
+    epi_member.assign(n, 0);
+    prog_pos.assign(n, UINT32_MAX);
+    {
+        // Launch order, and each launch's program nodes (a chain: one per step; an Add
+        // fused into its ReLU and a paired SGD: two), as the execution loop adds them.
+        std::vector<uint32_t> run;
+        std::vector<int> pos(n, -1);
+        uint32_t next = 0;
+        for (uint32_t i : order) {
+            const Node &nd = graph.nodes[i];
+            if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform ||
+                fused_into[i] >= 0 || chain_member[i] || sgd_second[i])
+                continue;
+            pos[i] = (int)run.size();
+            run.push_back(i);
+            prog_pos[i] = next;
+            if (chain_len[i] > 1)
+                next += (uint32_t)chain_len[i];
+            else if ((nd.op == Op::Relu && fused_into[nd.a] == (int)i) ||
+                     sgd_partner[i] != UINT32_MAX)
+                next += 2;
+            else
+                next += 1;
+        }
+        // The node's operands other than the product must be ready when the MatMul runs:
+        // not produced by a launch between the two.
+        auto ready = [&](uint32_t v, size_t at) { return pos[v] < 0 || (size_t)pos[v] < at; };
+        for (size_t k = 0; k < run.size(); k++) {
+            const uint32_t m = run[k];
+            const Node &mn = graph.nodes[m];
+            if (mn.op != Op::MatMul || route[m] != Route::Strict)
+                continue;
+            for (size_t j = k + 1; j < run.size() && j <= k + kEpiWindow; j++) {
+                const uint32_t r = run[j];
+                const Node &rn = graph.nodes[r];
+                if (epi_member[r] || chain_len[r] > 1 || rn.dtype != mn.dtype || rn.shape != mn.shape)
+                    continue;
+                const bool relu = rn.op == Op::Relu && rn.a == m;
+                const bool back = rn.op == Op::ReluBackward && rn.b == m && rn.a != m && ready(rn.a, k);
+                if (relu || back) {
+                    gemm_epi[m] = r;
+                    epi_member[r] = 1;
+                    break;
+                }
+            }
+        }
+    }
     // The ordered MSE sum runs on the side stream when nothing in the plan consumes its
     // value (the training-loss case): it then overlaps the backward pass. A small one (one
     // kernel of one workgroup) stays on the main stream: the fork and join cost the host
@@ -950,12 +998,24 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     if ((st = ctx->begin_program(false)))
         return st;
     std::vector<uint32_t> prog_to_graph;
+    std::vector<unsigned long long *> epi_word(graph.nodes.size(), nullptr);
     auto ptr = [&](uint32_t id) { return value_ptr(id, in, bank_w); };
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
         if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0 ||
             chain_member[i] || sgd_second[i])
             continue;
+        if (epi_member[i]) {
+            // Evaluated with its MatMul; its program node takes its own place here.
+            if ((st = ctx->add_fused_node(graph.elements(i), epi_word[i]))) {
+                pcu_fault ignore;
+                (void)ctx->end_program(&ignore);
+                error = ctx->error;
+                return st;
+            }
+            prog_to_graph.push_back(i);
+            continue;
+        }
         uint64_t n = graph.elements(i);
         int policy = nd.policy < 0 ? 0 : nd.policy;
         if (chain_len[i] > 1) {
@@ -1017,7 +1077,19 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
             if (route[i] == Route::Native)
                 st = ctx->op_native_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
                                            ptr(nd.a), ptr(nd.b), ptr(i));
-            else
+            else if (gemm_epi[i] != UINT32_MAX) {
+                const uint32_t r = gemm_epi[i];
+                const Node &rn = graph.nodes[r];
+                GemmEpilogue epi;
+                epi.op = rn.op == Op::Relu ? kStepRelu : kStepReluBackward;
+                epi.policy = rn.policy < 0 ? 0 : rn.policy;
+                epi.x = rn.op == Op::Relu ? nullptr : ptr(rn.a);
+                epi.out = ptr(r);
+                st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
+                                    ptr(nd.a), ptr(nd.b), ptr(i), policy, false, &epi,
+                                    prog_pos[r] - prog_pos[i] - 1);
+                epi_word[r] = epi.fault;
+            } else
                 st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
                                     ptr(nd.a), ptr(nd.b), ptr(i), policy);
             prog_to_graph.push_back(i);

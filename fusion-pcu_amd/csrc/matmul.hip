@@ -1713,7 +1713,8 @@ template <typename T>
 static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_t N, bool ta,
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault, NodeGate gate,
-                                  hipEvent_t *ev, int engine, ProgramOpen open)
+                                  hipEvent_t *ev, int engine, ProgramOpen open,
+                                  const GemmEpilogue *epi, bool *epi_done)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -1804,7 +1805,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
             tbt = false;
         }
         (void)launch_gemm_mfma_f32(s, m, n, k, ta, tbt, (const float *)A, Bt, (float *)C,
-                                   sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate);
+                                   sc.row_exp, sc.col_exp, thr, risk, sc.suspect, sck, gate, epi, epi_done);
     } else if (!f32 && (uint64_t)grid.x < 256) {
         const double *dA = (const double *)A, *dB = (const double *)B;
         double *dC = (double *)C;
@@ -1903,17 +1904,29 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
-                                hipEvent_t *ev, int engine, ProgramOpen open)
+                                hipEvent_t *ev, int engine, ProgramOpen open,
+                                const GemmEpilogue *epi)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
-    if (dtype == 0)
-        return strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
-                                      (const float *)a, (const float *)b, (float *)c, policy,
-                                      scratch, fault, gate, ev, engine, open);
-    return strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
-                                   (const double *)a, (const double *)b, (double *)c, policy,
-                                   scratch, fault, gate, ev, engine, open);
+    if (epi && epi->op != 0 && epi->op != kStepRelu && epi->op != kStepReluBackward)
+        return hipErrorInvalidValue;
+    bool done = false;
+    const hipError_t e =
+        dtype == 0 ? strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
+                                            (const float *)a, (const float *)b, (float *)c, policy,
+                                            scratch, fault, gate, ev, engine, open, epi, &done)
+                   : strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
+                                             (const double *)a, (const double *)b, (double *)c,
+                                             policy, scratch, fault, gate, ev, engine, open, epi,
+                                             &done);
+    if (e != hipSuccess || !epi || epi->op == 0 || done)
+        return e;
+    // The tile kernel that ran has no such epilogue: the node's own kernel follows.
+    const uint64_t n = rows * cols;
+    if (epi->op == kStepRelu)
+        return launch_relu(s, dtype, n, c, epi->out, epi->policy, epi->fault, epi->gate);
+    return launch_relu_backward(s, dtype, n, epi->x, c, epi->out, epi->policy, epi->fault, epi->gate);
 }
 
 } // namespace pcu

@@ -72,12 +72,16 @@ template <int N> __device__ __forceinline__ void wait_loads_but()
 // loads allowed), so staging runs on advancing pointers with no bound checks.
 // CHECK: the RejectSubnormal form with the partial-sum check (sck), its own instantiation so
 // that the plain form keeps its registers and schedule.
-template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false, bool CHECK = false>
+// EPI: the whole-tile epilogue (three stages, two subtiles a wave) also evaluates `epi`, a
+// ReLU (EPI = kStepRelu) or ReLU backward (kStepReluBackward) of each product cell, with the
+// elementwise kernels' classification, recording into that node's own word.
+template <class Cfg, bool TA, bool TB, bool VA, bool VB, bool WHOLE = false, bool CHECK = false,
+          int EPI = 0>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_gemm_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
     int N, int K, const unsigned long long *__restrict__ row_exp,
     const unsigned long long *__restrict__ col_exp, int thr, int check_risk,
-    unsigned long long *suspect, SumCheck sck, NodeGate gate)
+    unsigned long long *suspect, SumCheck sck, NodeGate gate, GemmEpilogue epi)
 {
     if (block_gate_closed(gate))
         return;
@@ -503,6 +507,18 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         const int cexp1 = check_risk ? exp_of(col_exp[c + 1]) : 0;
         if (sub) // rows m0 + wm .. m0 + wm + 31 of columns c and c + 1 (c even): one block
             flag_sum_block(sck, m0 + wm, c);
+        uint64_t ekey = kNoFault; // the epilogue node's first fault in this lane
+        // The ReLU backward's input at the lane's 32 cells, all loaded before the first
+        // store (a load after each store would wait out its latency 16 times).
+        float2 xin[EPI == kStepReluBackward ? 16 : 1];
+        if constexpr (EPI == kStepReluBackward) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
+                xin[r] = *reinterpret_cast<const float2 *>(
+                    &static_cast<const float *>(epi.x)[(size_t)row * N + c]);
+            }
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -519,7 +535,30 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 key = cell < key ? cell : key;
             else if (bad1)
                 key = cell + 1 < key ? cell + 1 : key;
+            if constexpr (EPI != 0) {
+                float r0, r1;
+                uint32_t k0, k1;
+                if constexpr (EPI == kStepRelu) {
+                    r0 = relu_select(v0);
+                    r1 = relu_select(v1);
+                    k0 = classify_relu(v0, r0, epi.policy);
+                    k1 = classify_relu(v1, r1, epi.policy);
+                } else {
+                    const float2 x = xin[r];
+                    r0 = strictly_positive(x.x) ? v0 : 0.0f;
+                    r1 = strictly_positive(x.y) ? v1 : 0.0f;
+                    k0 = classify_relu_backward(x.x, v0, r0, epi.policy);
+                    k1 = classify_relu_backward(x.y, v1, r1, epi.policy);
+                }
+                *reinterpret_cast<float2 *>(&static_cast<float *>(epi.out)[(size_t)row * N + c]) =
+                    make_float2(r0, r1);
+                const uint64_t e = k0 != kOk ? pack_fault(cell, k0)
+                                 : k1 != kOk ? pack_fault(cell + 1, k1) : kNoFault;
+                ekey = e < ekey ? e : ekey;
+            }
         }
+        if constexpr (EPI != 0)
+            wave_record_fault(ekey, epi.fault, epi.gate);
         block_record_min<Cfg::kThreads / 64>(key, suspect);
         return;
     }
@@ -786,7 +825,7 @@ template <class Cfg, bool TA, bool TB>
 static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *C, int M, int N,
                           int K, const unsigned long long *re, const unsigned long long *ce,
                           int thr, int risk, unsigned long long *suspect, SumCheck sck,
-                          NodeGate gate)
+                          NodeGate gate, const GemmEpilogue *epi, bool *epi_done)
 {
     const dim3 grid((unsigned)(((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN)));
     const dim3 block(Cfg::kThreads);
@@ -799,28 +838,46 @@ static void mfma_dispatch(hipStream_t s, const float *A, const float *B, float *
     const bool offsets32 = 4 * span_a <= UINT32_MAX && (TB || 4 * span_b <= UINT32_MAX);
     const bool whole = va && vb && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
                        ((uintptr_t)C & 7u) == 0 && offsets32;
+    if constexpr (Cfg::SN == 2) {
+        // The whole-tile epilogue evaluates an elementwise node with the product.
+        if (whole && epi && (epi->op == kStepRelu || epi->op == kStepReluBackward)) {
+            if (epi->op == kStepRelu) {
+                hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, false, kStepRelu>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, *epi);
+                if (sck.flag)
+                    hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, true, kStepRelu>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, *epi);
+            } else {
+                hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, false, kStepReluBackward>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, *epi);
+                if (sck.flag)
+                    hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, true, kStepReluBackward>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, *epi);
+            }
+            if (epi_done)
+                *epi_done = true;
+            return;
+        }
+    }
     if (whole)
-        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, true, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); }
     else if (va && vb)
-        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); }
     else if (va)
-        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, true, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); }
     else if (vb)
-        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, true, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); }
     else
-        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate); }
+        { hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); if (sck.flag) hipLaunchKernelGGL((k_strict_gemm_mfma<Cfg, TA, TB, false, false, false, true>), grid, block, 0, s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, GemmEpilogue{}); }
 }
 
 template <class Cfg>
 static void mfma_launch(hipStream_t s, int M, int N, int K, bool ta, bool tb, const float *A,
                         const float *B, float *C, const unsigned long long *re,
                         const unsigned long long *ce, int thr,
-                        int risk, unsigned long long *suspect, SumCheck sck, NodeGate gate)
+                        int risk, unsigned long long *suspect, SumCheck sck, NodeGate gate,
+                        const GemmEpilogue *epi = nullptr, bool *epi_done = nullptr)
 {
-    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
-    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
-    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
-    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate);
+    if (!ta && !tb) mfma_dispatch<Cfg, false, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, epi, epi_done);
+    else if (!ta && tb) mfma_dispatch<Cfg, false, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, epi, epi_done);
+    else if (ta && !tb) mfma_dispatch<Cfg, true, false>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, epi, epi_done);
+    else mfma_dispatch<Cfg, true, true>(s, A, B, C, M, N, K, re, ce, thr, risk, suspect, sck, gate, epi, epi_done);
 }
 
 // 8 waves of 32 x 64 over a 128 x 128 tile, 123-126 VGPRs (4 waves per SIMD). On MI355X at
@@ -837,7 +894,8 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
                                 const float *A, const float *B, float *C,
                                 const unsigned long long *row_exp,
                                 const unsigned long long *col_exp, int thr, int risk,
-                                unsigned long long *suspect, SumCheck sck, NodeGate gate)
+                                unsigned long long *suspect, SumCheck sck, NodeGate gate,
+                                const GemmEpilogue *epi, bool *epi_done)
 {
     const uint64_t big_tiles = (uint64_t)((M + GemmCfg::BM - 1) / GemmCfg::BM) * ((N + GemmCfg::BN - 1) / GemmCfg::BN);
     // 16 x 16 waves: whole 64 x 64 tiles, 16-byte loads, lane offsets within 32 bits, and
@@ -861,7 +919,7 @@ hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, boo
     if (big_tiles < 256)
         mfma_launch<SmallCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, sck, gate);
     else
-        mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, sck, gate);
+        mfma_launch<GemmCfg>(s, M, N, K, ta, tb, A, B, C, row_exp, col_exp, thr, risk, suspect, sck, gate, epi, epi_done);
     return hipGetLastError();
 }
 

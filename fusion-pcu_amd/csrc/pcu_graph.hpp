@@ -28,6 +28,11 @@ enum class Op : uint32_t {
 
 enum class Mode : int32_t { None = -1, Boundary = 0, Strict = 1 };
 
+// How many launches after a strict MatMul the plan looks for the ReLU (backward) that its
+// tile kernel can evaluate (reverse mode places the weight gradient's MatMul between the
+// input gradient's MatMul and its ReLU backward).
+constexpr int kEpiWindow = 4;
+
 // PcuNumericalOptions (core/numerical/numerical.rs:71-78): every node captures the graph's
 // options when it is appended.
 struct NumOptions {
@@ -104,6 +109,14 @@ struct Prepared {
     // first, run as one launch: sgd_partner[first] = second, sgd_second[second] = 1.
     std::vector<uint32_t> sgd_partner;
     std::vector<char> sgd_second;
+    // A strict MatMul followed within a few launches by a ReLU of its product, or by a
+    // ReLU backward taking the product as upstream, evaluates that node with its own launch:
+    // gemm_epi[matmul] = node (UINT32_MAX: none), epi_member[node] = 1. The node keeps its
+    // place in the program (its fault word and gate), so fault order is unchanged.
+    // prog_pos: each launching node's first program node index.
+    std::vector<uint32_t> gemm_epi;
+    std::vector<char> epi_member;
+    std::vector<uint32_t> prog_pos;
     std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
     std::vector<void *> constant_buf; // resident copy of each planned Constant, uploaded at build

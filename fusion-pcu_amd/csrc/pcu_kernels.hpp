@@ -61,6 +61,18 @@ struct ChainStep {
     void *out;           // the step's value is stored here, or nullptr (read by the next step only)
     unsigned long long *fault;
 };
+// An elementwise node that a MatMul evaluates with its product: a ReLU of the product or a
+// ReLU backward taking the product as its upstream (input `x`). It keeps its own value,
+// policy, fault word and gate; the MatMul still stores its own value.
+struct GemmEpilogue {
+    int op = 0; // 0: none; kStepRelu or kStepReluBackward
+    int policy = 0;
+    const void *x = nullptr; // ReLU backward's input, shaped like the product
+    void *out = nullptr;
+    unsigned long long *fault = nullptr;
+    NodeGate gate{nullptr, 0};
+};
+
 struct ChainLaunch {
     int steps = 0;
     const void *head = nullptr;
@@ -142,11 +154,13 @@ MatmulScratch matmul_scratch_carve(void *base, uint64_t rows, uint64_t cols, boo
 // products; the ordered sums stay on the vector unit). F64 always uses the vector unit.
 enum : int { kEngineAuto = 0, kEngineValu = 1, kEngineMfmaProducts = 2 };
 
+// `epi`: evaluated in the epilogue when the chosen tile kernel supports it (*epi_done set).
 hipError_t launch_gemm_mfma_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,
                                 const float *A, const float *B, float *C,
                                 const unsigned long long *row_exp,
                                 const unsigned long long *col_exp, int thr, int risk,
-                                unsigned long long *suspect, SumCheck sck, NodeGate gate);
+                                unsigned long long *suspect, SumCheck sck, NodeGate gate,
+                                const GemmEpilogue *epi = nullptr, bool *epi_done = nullptr);
 
 // C[rows x cols] = op(A) * op(B), k ascending, each multiply and add rounded on its own.
 // Every kernel of the op skips its work once `gate` shows that an earlier program node
@@ -163,12 +177,15 @@ struct ProgramOpen {
     unsigned long long value = 0;
     unsigned int *gate = nullptr;
 };
+// With `epi`, the MatMul also evaluates that elementwise node: in the tile kernel's
+// epilogue where the kernel supports it (whole 128 x 128 matrix-core tiles), else as its own
+// kernel right after the tile kernel.
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto,
-                                ProgramOpen open = {});
+                                ProgramOpen open = {}, const GemmEpilogue *epi = nullptr);
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,

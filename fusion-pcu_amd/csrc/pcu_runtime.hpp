@@ -141,8 +141,16 @@ struct Ctx {
 
     // noalloc: the screen's scratch is the library's fixed per-device array
     // (pcu_strict_matmul_noalloc), so the call allocates nothing.
+    // epi: an elementwise node that takes the product as its operand (a ReLU of it, or a
+    // ReLU backward with it as upstream), evaluated with the MatMul (op, policy, x and out
+    // from `epi`). It is the program node epi_after nodes after the MatMul's: its fault word
+    // and gate are filled in here, and the caller adds it there with add_fused_node.
     pcu_status op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl, int tr,
-                         const void *a, const void *b, void *c, int policy, bool noalloc = false);
+                         const void *a, const void *b, void *c, int policy, bool noalloc = false,
+                         GemmEpilogue *epi = nullptr, uint32_t epi_after = 0);
+    // Adds the program node of an elementwise node already evaluated with its MatMul;
+    // `expect` is the fault word op_matmul gave it.
+    pcu_status add_fused_node(uint64_t n, const unsigned long long *expect);
     pcu_status op_binary(int dtype, int op, uint64_t n, const void *a, const void *b,
                          const void *b_value, void *out, int policy);
     pcu_status op_relu(int dtype, uint64_t n, const void *x, void *out, int policy);

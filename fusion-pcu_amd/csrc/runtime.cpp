@@ -342,6 +342,19 @@ pcu_status Ctx::open_words()
                "open fault words and stage gate");
 }
 
+pcu_status Ctx::add_fused_node(uint64_t n, const unsigned long long *expect)
+{
+    unsigned long long *word;
+    pcu_status st = add_node(NodeInfo{Prim::Elementwise, n, 0}, &word);
+    if (st)
+        return st;
+    if (word != expect) {
+        fail("internal: an elementwise node evaluated with its MatMul lost its program position");
+        return PCU_ERR_STATE;
+    }
+    return PCU_OK;
+}
+
 pcu_status Ctx::add_node(NodeInfo info, unsigned long long **word)
 {
     if (!in_program) {
@@ -693,7 +706,8 @@ static bool matmul_out_overlaps(int dtype, uint64_t rows, uint64_t inner, uint64
 }
 
 pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
-                          int tr, const void *a, const void *b, void *c, int policy, bool noalloc)
+                          int tr, const void *a, const void *b, void *c, int policy, bool noalloc,
+                          GemmEpilogue *epi, uint32_t epi_after)
 {
     if (!valid_dtype(dtype) || !valid_policy(policy) || !c || ((rows * inner) && !a) ||
         ((inner * cols) && !b)) {
@@ -716,11 +730,44 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
             return PCU_ERR_STATE;
         }
     }
+    const uint64_t cells = rows * cols, ds = dsize(dtype);
+    if (epi) {
+        // The tile kernel stores the product and the node's value side by side while other
+        // tiles still read A and B, and the checks after it read the product back: the
+        // value may overlap none of them (x, read cell by cell, only exactly).
+        const bool relu = epi->op == kStepRelu, back = epi->op == kStepReluBackward;
+        if (noalloc || (!relu && !back) || !valid_policy(epi->policy) ||
+            (cells && (!epi->out || (back && !epi->x)))) {
+            fail("strict_matmul: invalid elementwise epilogue");
+            return PCU_ERR_ARGUMENT;
+        }
+        const uint64_t ob = cells * ds;
+        if (cells && (ranges_overlap(epi->out, ob, c, ob) ||
+                      ranges_overlap(epi->out, ob, a, rows * inner * ds) ||
+                      ranges_overlap(epi->out, ob, b, inner * cols * ds) ||
+                      (back && (partial_overlap(epi->out, epi->x, ob) ||
+                                ranges_overlap(epi->x, ob, c, ob))))) {
+            fail("strict_matmul: the epilogue's value overlaps an operand");
+            return PCU_ERR_ARGUMENT;
+        }
+    }
     unsigned long long *word;
-    NodeInfo info{Prim::MatMul, rows * cols, inner};
+    NodeInfo info{Prim::MatMul, cells, inner};
     pcu_status st = add_node(info, &word);
     if (st)
         return st;
+    const bool first_node = nodes.size() == 1;
+    if (epi) {
+        // The elementwise node's word: the program node it will be added as, epi_after
+        // nodes after this one.
+        const size_t at = nodes.size() + (size_t)epi_after;
+        if (at >= kMaxNodes) {
+            fail("program exceeds %u nodes", kMaxNodes);
+            return PCU_ERR_STATE;
+        }
+        epi->fault = fault_words + at;
+        epi->gate = gate_for(epi->fault);
+    }
     if (rows == 0 || cols == 0)
         return PCU_OK;
     // The screen's exponent words carry a generation that only grows, so a later screen
@@ -779,7 +826,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     // As the program's first node, the MatMul's first kernel opens the program (one launch
     // fewer; a first node is never gated, so nothing waits on the gate it opens).
     ProgramOpen open;
-    if (words_pending && nodes.size() == 1) {
+    if (words_pending && first_node) {
         words_pending = false;
         open = {fault_words, kMaxNodes, kNoFaultWord, gate_word()};
     } else if ((st = open_words())) {
@@ -791,7 +838,7 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         return st;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
-                                        timed ? ev : nullptr, matmul_engine, open);
+                                        timed ? ev : nullptr, matmul_engine, open, epi);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
     if (timed) {
@@ -873,6 +920,13 @@ pcu_status Ctx::op_chain(int dtype, uint64_t n, ChainLaunch c)
             fail("elementwise chain: a step's output partly overlaps an operand");
             return PCU_ERR_ARGUMENT;
         }
+        // The kernel loads every operand before any step stores, so no later step may
+        // take an earlier step's stored value as its other operand.
+        for (int j = i + 1; j < c.steps; j++)
+            if (st.out && n && ranges_overlap(st.out, bytes, c.step[j].other, bytes)) {
+                fail("elementwise chain: step %d reads the value step %d stores", j, i);
+                return PCU_ERR_ARGUMENT;
+            }
     }
     unsigned long long *first = nullptr;
     for (int i = 0; i < c.steps; i++) {

@@ -447,3 +447,150 @@ def test_mse_then_chain_fault_order(G, pcu_pkg, dtype):
             finally:
                 for x in dev.values():
                     x.free()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_matmul_relu_epilogue_fault_order(G, pcu_pkg, dtype):
+    """A strict MatMul followed by a ReLU of its product, and one followed by a ReLU
+    backward taking its product as upstream, each a node of its own with its own fault word:
+    F32 at whole 128 x 128 tiles on the large tile kernel evaluates the elementwise node in
+    that kernel's epilogue, other shapes and F64 launch it after the MatMul. With faults
+    planted in a MatMul operand (invalid, overflow), in the ReLU backward's input, in both, a
+    subnormal product under a RejectSubnormal ReLU, or none, the outputs, or the first
+    faulting node and its coordinates, match the oracle's ordered graph."""
+    big = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    tiny = dtype(2.0 ** -70) if dtype == np.float32 else dtype(2.0 ** -530)
+    ctx = G.default_context()
+    rng = np.random.default_rng(37)
+    for m, k, n in ((2048, 64, 2048), (2048, 128, 2176), (2048, 64, 2050), (256, 64, 256)):
+        g = G.Graph()
+        g.set_numerical_mode(True)
+        a, b = g.input((m, k), dtype), g.input((k, n), dtype)
+        b2, x = g.input((k, n), dtype), g.input((m, n), dtype)
+        p = g.matmul(a, b)
+        h = g.relu(p)
+        hb = g.relu_backward(x, g.matmul(a, b2))
+        g.set_underflow_policy(h, 1)
+        outs = [h, hb, p]
+        prep = g.prepare(ctx, outs)
+        ref = og.Graph()
+        ref.mode = "Strict"
+        ra, rb = ref.input((m, k), dtype), ref.input((k, n), dtype)
+        rb2, rx = ref.input((k, n), dtype), ref.input((m, n), dtype)
+        rp = ref.matmul(ra, rb)
+        rh = ref.relu(rp)
+        rhb = ref.relu_backward(rx, ref.matmul(ra, rb2))
+        ref.nodes[rh].policy = 1
+        routs = [rh, rhb, rp]
+        for plant in ("none", "matmul", "overflow", "relu_x", "both", "subnormal"):
+            va = rng.uniform(-1, 1, (m, k)).astype(dtype)
+            vb = rng.uniform(-1, 1, (k, n)).astype(dtype)
+            vb2 = rng.uniform(-1, 1, (k, n)).astype(dtype)
+            vx = rng.uniform(-1, 1, (m, n)).astype(dtype)
+            if plant in ("matmul", "both"):
+                va[m // 3, k // 2] = np.nan  # the first MatMul is invalid from row m / 3 on
+            if plant == "overflow":
+                vb2[k - 1, n - 1] = big
+                va[m - 1, k - 1] = big  # the second MatMul overflows at its last cell
+            if plant in ("relu_x", "both"):
+                vx[m // 2, n - 3] = np.inf  # the ReLU backward is invalid there
+            if plant == "subnormal":
+                va[m // 4, :] = 0
+                va[m // 4, 0] = tiny
+                vb[0, n // 5] = tiny  # an exact subnormal product: a RejectSubnormal ReLU faults
+            vals, rf = ref.evaluate({ra: va, rb: vb, rb2: vb2, rx: vx}, routs)
+            assert (rf is None) == (plant == "none"), (plant, rf)
+            dev = {a: ctx.upload(va), b: ctx.upload(vb), b2: ctx.upload(vb2), x: ctx.upload(vx)}
+            try:
+                if rf is None:
+                    prep.execute([dev[i].ptr for i in prep.input_ids])
+                    for j, want in enumerate(routs):
+                        d = prep.output_desc[j]
+                        have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(j), d["shape"], d["dtype"]).numpy()
+                        np.testing.assert_array_equal(_bits(have), _bits(vals[want]), err_msg=f"{m}x{k}x{n}")
+                else:
+                    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                        prep.execute([dev[i].ptr for i in prep.input_ids])
+                    tf = exc.value.tensor_fault
+                    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                         rf.fault.kind), (m, k, n, plant)
+            finally:
+                for v in dev.values():
+                    v.free()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_relu_backward_epilogue_after_another_matmul(G, pcu_pkg, dtype):
+    """The reverse-mode order: a MatMul, an independent MatMul, then the ReLU backward of the
+    first product. The ReLU backward is evaluated with the first MatMul but keeps its place
+    after the second, so with both later nodes faulting the second MatMul is reported; when
+    the ReLU backward's input is the second MatMul's product it runs on its own. The ReLU
+    backward's fault: an exact subnormal product (no MatMul fault) under its RejectSubnormal
+    policy where its input is positive. Outputs or the first faulting node and its
+    coordinates match the oracle's ordered graph."""
+    big = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    tiny = dtype(2.0 ** -70) if dtype == np.float32 else dtype(2.0 ** -530)
+    ctx = G.default_context()
+    rng = np.random.default_rng(41)
+    m, k, n = 2048, 64, 2048
+    for x_from_second in (False, True):
+        g = G.Graph()
+        g.set_numerical_mode(True)
+        a, b = g.input((m, k), dtype), g.input((k, n), dtype)
+        a2, b2 = g.input((m, k), dtype), g.input((k, n), dtype)
+        x = g.input((m, n), dtype)
+        p = g.matmul(a, b)
+        q = g.matmul(a2, b2)
+        hb = g.relu_backward(q if x_from_second else x, p)
+        g.set_underflow_policy(hb, 1)
+        outs = [hb, q]
+        prep = g.prepare(ctx, outs)
+        ref = og.Graph()
+        ref.mode = "Strict"
+        ra, rb = ref.input((m, k), dtype), ref.input((k, n), dtype)
+        ra2, rb2 = ref.input((m, k), dtype), ref.input((k, n), dtype)
+        rx = ref.input((m, n), dtype)
+        rp = ref.matmul(ra, rb)
+        rq = ref.matmul(ra2, rb2)
+        rhb = ref.relu_backward(rq if x_from_second else rx, rp)
+        ref.nodes[rhb].policy = 1
+        routs = [rhb, rq]
+        for plant in ("none", "first", "second", "relu", "second_and_relu", "all"):
+            va, vb = rng.uniform(-1, 1, (m, k)).astype(dtype), rng.uniform(-1, 1, (k, n)).astype(dtype)
+            va2, vb2 = rng.uniform(-1, 1, (m, k)).astype(dtype), rng.uniform(-1, 1, (k, n)).astype(dtype)
+            vx = rng.uniform(-1, 1, (m, n)).astype(dtype)
+            if plant in ("first", "all"):
+                va[m - 2, 1] = np.nan  # invalid in the first MatMul
+            if plant in ("second", "second_and_relu", "all"):
+                va2[m // 2, k - 1], vb2[k - 1, 7] = big, big  # overflow in the second MatMul
+            if plant in ("relu", "second_and_relu", "all"):
+                i, j = m // 4, n // 5
+                va[i, :] = 0
+                va[i, 0] = tiny
+                vb[0, j] = tiny  # first product: exactly tiny * tiny, subnormal
+                vx[i, j] = 0.5
+                va2[i, :] = 0
+                va2[i, 0] = 1
+                vb2[0, j] = 1  # second product: 1 at (i, j)
+            vals, rf = ref.evaluate({ra: va, rb: vb, ra2: va2, rb2: vb2, rx: vx}, routs)
+            assert (rf is None) == (plant == "none"), (plant, rf)
+            dev = {a: ctx.upload(va), b: ctx.upload(vb), a2: ctx.upload(va2), b2: ctx.upload(vb2),
+                   x: ctx.upload(vx)}
+            try:
+                if rf is None:
+                    prep.execute([dev[i].ptr for i in prep.input_ids if i in dev])
+                    for j, want in enumerate(routs):
+                        d = prep.output_desc[j]
+                        have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(j), d["shape"], d["dtype"]).numpy()
+                        np.testing.assert_array_equal(_bits(have), _bits(vals[want]))
+                else:
+                    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                        prep.execute([dev[i].ptr for i in prep.input_ids if i in dev])
+                    tf = exc.value.tensor_fault
+                    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                         rf.fault.kind), (x_from_second, plant)
+            finally:
+                for v in dev.values():
+                    v.free()
