@@ -644,7 +644,7 @@ void prepared_detach(Prepared *p)
                 (void)ctx->release(q);
                 q = nullptr;
             }
-    for (auto *list : {&p->dense_uniform, &p->constant_buf})
+    for (auto *list : {&p->dense_uniform, &p->constant_buf, &p->pre_rows, &p->pre_cols})
         for (void *&q : *list)
             if (q) {
                 (void)ctx->release(q);
@@ -677,6 +677,8 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
     mse_side.assign(n, 0);
     dense_uniform.assign(n, nullptr);
     constant_buf.assign(n, nullptr);
+    pre_rows.assign(n, nullptr);
+    pre_cols.assign(n, nullptr);
     for (uint32_t o : outputs)
         is_output[o] = 1;
     std::vector<uint32_t> uses(n, 0);
@@ -868,6 +870,23 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
             }
         }
     }
+    // Tables an epilogue writes for the strict F32 MatMuls that read its node's value: op(A)
+    // rows are the value's rows when A is untransposed, its columns when transposed; op(B)
+    // columns are its columns when B is untransposed, its rows when transposed. Only for
+    // values of whole 128 x 128 tiles (where the epilogue can run).
+    std::vector<char> want_rows(n, 0), want_cols(n, 0);
+    for (uint32_t q : order) {
+        const Node &qn = graph.nodes[q];
+        if (qn.op != Op::MatMul || route[q] != Route::Strict || qn.dtype != 0)
+            continue;
+        for (int side = 0; side < 2; side++) {
+            const uint32_t r = side == 0 ? qn.a : qn.b;
+            if (!epi_member[r] || graph.nodes[r].dtype != 0 || graph.nodes[r].shape.size() != 2)
+                continue;
+            const bool transposed = side == 0 ? qn.tl : qn.tr;
+            (side == 0 ? !transposed : transposed) ? (void)(want_rows[r] = 1) : (void)(want_cols[r] = 1);
+        }
+    }
     // The ordered MSE sum runs on the side stream when nothing in the plan consumes its
     // value (the training-loss case): it then overlaps the backward pass. A small one (one
     // kernel of one workgroup) stays on the main stream: the fork and join cost the host
@@ -896,6 +915,18 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
         for (int b = 0; b < (is_output[i] ? 2 : 1); b++)
             if ((st = ctx->alloc(bytes, &buf[b][i])))
                 return st;
+    }
+    for (uint32_t r : order) {
+        if (!want_rows[r] && !want_cols[r])
+            continue;
+        const auto &sh = graph.nodes[r].shape;
+        const uint64_t m = sh[0], w = sh[1];
+        if (m == 0 || w == 0 || m % 128 != 0 || w % 128 != 0)
+            continue; // never whole tiles: its MatMul launches the elementwise kernel
+        if (want_rows[r] && (st = ctx->alloc(m * (w / 64) * sizeof(short), &pre_rows[r])))
+            return st;
+        if (want_cols[r] && (st = ctx->alloc((m / 64) * w * sizeof(short), &pre_cols[r])))
+            return st;
     }
     published_ptr.assign(outputs.size(), nullptr);
     return PCU_OK;
@@ -999,7 +1030,20 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
         return st;
     std::vector<uint32_t> prog_to_graph;
     std::vector<unsigned long long *> epi_word(graph.nodes.size(), nullptr);
+    std::vector<char> tables_written(graph.nodes.size(), 0); // this execution, by an epilogue
     auto ptr = [&](uint32_t id) { return value_ptr(id, in, bank_w); };
+    // The tables this execution's epilogues wrote for a strict F32 MatMul's operands.
+    auto prescreen = [&](uint32_t q) {
+        const Node &qn = graph.nodes[q];
+        Prescreen p;
+        if (qn.dtype != 0)
+            return p;
+        if (tables_written[qn.a])
+            p.a = (const short *)(qn.tl ? pre_cols[qn.a] : pre_rows[qn.a]);
+        if (tables_written[qn.b])
+            p.b = (const short *)(qn.tr ? pre_rows[qn.b] : pre_cols[qn.b]);
+        return p;
+    };
     for (uint32_t i : order) {
         const Node &nd = graph.nodes[i];
         if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform || fused_into[i] >= 0 ||
@@ -1085,13 +1129,18 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
                 epi.policy = rn.policy < 0 ? 0 : rn.policy;
                 epi.x = rn.op == Op::Relu ? nullptr : ptr(rn.a);
                 epi.out = ptr(r);
+                epi.tbl_rows = (short *)pre_rows[r];
+                epi.tbl_cols = (short *)pre_cols[r];
+                bool fused = false;
                 st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
                                     ptr(nd.a), ptr(nd.b), ptr(i), policy, false, &epi,
-                                    prog_pos[r] - prog_pos[i] - 1);
+                                    prog_pos[r] - prog_pos[i] - 1, prescreen(i), &fused);
                 epi_word[r] = epi.fault;
+                tables_written[r] = fused && (epi.tbl_rows || epi.tbl_cols);
             } else
                 st = ctx->op_matmul(nd.dtype, nd.shape[0], inner, nd.shape[1], nd.tl, nd.tr,
-                                    ptr(nd.a), ptr(nd.b), ptr(i), policy);
+                                    ptr(nd.a), ptr(nd.b), ptr(i), policy, false, nullptr, 0,
+                                    prescreen(i));
             prog_to_graph.push_back(i);
             break;
         }

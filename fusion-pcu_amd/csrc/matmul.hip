@@ -36,23 +36,6 @@
 
 namespace pcu {
 
-constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
-
-// Branch-free: the prefilter applies it to every element of both operands.
-__device__ __forceinline__ int ilog2_abs(float v)
-{
-    const uint32_t b = bits_of(v) & 0x7fffffffu, e = b >> 23;
-    const int sub = (31 - __clz(b | 1u)) - 149; // e == 0: b is the fraction
-    const int r = e ? (int)e - 127 : sub;
-    return (e == 0xff || b == 0) ? kExpNone : r;
-}
-__device__ __forceinline__ int ilog2_abs(double v)
-{
-    const uint64_t b = bits_of(v) & 0x7fffffffffffffffull, e = b >> 52;
-    const int sub = (63 - __clzll(b | 1ull)) - 1074;
-    const int r = e ? (int)e - 1023 : sub;
-    return (e == 0x7ff || b == 0) ? kExpNone : r;
-}
 
 __device__ __forceinline__ int wave_min_i32(int v)
 {
@@ -84,6 +67,9 @@ template <typename T> struct ExpJob {
     // entry-major, tbl[row * ceil(C / kSuperSlab) + s]; a columns job (k down its columns)
     // superslab-major, tbl[s * C + column]. Null: no table.
     short *tbl;
+    // A fold job: the entries' minima come from this table (laid out as `tbl` above, written
+    // by the kernel that produced X) instead of from X, which is not read.
+    const short *src = nullptr;
 };
 
 // Superslab of the tables above: 64 k, four slabs of the tiny scan, and the 64-row group of a
@@ -281,8 +267,67 @@ __device__ __forceinline__ void exp_cols_block(const ExpJob<T> &j, uint64_t bid,
     }
 }
 
+// Fold jobs. Rows: one wave per entry folds its row of the table (64 superslabs of a
+// 4096-long k in one load a lane). Columns: 64 entries a block, the four waves taking every
+// fourth superslab and meeting in LDS. Each word is written once, by a plain store.
+template <typename T>
+__device__ __forceinline__ void fold_rows_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen)
+{
+    const uint64_t r = bid * 4 + threadIdx.x / 64;
+    if (r >= j.R)
+        return; // whole wave exits together
+    const int lane = threadIdx.x % 64;
+    const uint64_t nss = (j.C + kSuperSlab - 1) / kSuperSlab;
+    const short *t = j.src + r * nss;
+    int m = kExpNone;
+    for (uint64_t k = lane; k < nss; k += 64) {
+        const int e = unscan_exp(t[k]);
+        m = e < m ? e : m;
+    }
+    m = wave_min_i32(m);
+    if (lane == 0)
+        j.out[r] = exp_word(gen, m);
+}
+
+template <typename T>
+__device__ __forceinline__ void fold_cols_block(const ExpJob<T> &j, uint64_t bid, uint32_t gen,
+                                                int (*part)[64 * 16 / sizeof(T)])
+{
+    const int cx = threadIdx.x % 64, q = threadIdx.x / 64;
+    const uint64_t c = bid * 64 + cx, C = j.C;
+    const uint64_t nss = (j.R + kSuperSlab - 1) / kSuperSlab;
+    int m = kExpNone;
+    if (c < C) {
+        uint64_t k = q;
+        for (; k + 60 < nss; k += 64) {
+            short t[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                t[u] = j.src[(k + 4 * u) * C + c];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int e = unscan_exp(t[u]);
+                m = e < m ? e : m;
+            }
+        }
+        for (; k < nss; k += 4) {
+            const int e = unscan_exp(j.src[k * C + c]);
+            m = e < m ? e : m;
+        }
+    }
+    part[q][cx] = m;
+    __syncthreads();
+    if (q == 0 && c < C) {
+        for (int g = 1; g < 4; g++)
+            m = part[g][cx] < m ? part[g][cx] : m;
+        j.out[c] = exp_word(gen, m);
+    }
+}
+
 template <typename T> __host__ __device__ inline uint64_t exp_blocks(const ExpJob<T> &j)
 {
+    if (j.src)
+        return j.rows ? (j.R + 3) / 4 : (j.C + 63) / 64;
     if (j.rows)
         return (j.R + 3) / 4;
     const uint64_t P = j.vec ? 16 / sizeof(T) : 1;
@@ -321,7 +366,12 @@ __global__ __launch_bounds__(256) void k_exp_screen(ExpJob<T> a, ExpJob<T> b, ui
     const bool first = blockIdx.x < na;
     const ExpJob<T> &j = first ? a : b;
     const uint64_t bid = first ? blockIdx.x : blockIdx.x - na;
-    if (j.rows) {
+    if (j.src) {
+        if (j.rows)
+            fold_rows_block<T>(j, bid, gen);
+        else
+            fold_cols_block<T>(j, bid, gen, part);
+    } else if (j.rows) {
         if (j.tbl) {
             if (j.vec)
                 exp_rows_block_tbl<T, true>(j, bid, gen);
@@ -1714,7 +1764,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault, NodeGate gate,
                                   hipEvent_t *ev, int engine, ProgramOpen open,
-                                  const GemmEpilogue *epi, bool *epi_done)
+                                  const GemmEpilogue *epi, bool *epi_done, Prescreen pre)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -1765,8 +1815,9 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const bool tables = sc.tbl_a != nullptr && (policy == kPolicyIeee || sum_check);
     ScanTables tbls;
     if (tables) {
-        tbls.a = sc.tbl_a;
-        tbls.b = sc.tbl_b;
+        // A prescreened operand's table is the one its producer wrote, in the same layout.
+        tbls.a = pre.a ? pre.a : sc.tbl_a;
+        tbls.b = pre.b ? pre.b : sc.tbl_b;
         tbls.a_xmajor = !ta; // a rows job over A (M x K), else a columns job over A (K x M)
         tbls.b_xmajor = tb;  // a rows job over B (N x K), else a columns job over B (K x N)
     }
@@ -1781,8 +1832,11 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     if (risk && K > 0) {
         // op(A) row r is stored row r (A is M x K) or stored column r (A is K x M); op(B)
         // column c is stored column c (B is K x N) or stored row c (B is N x K).
-        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp, tables ? sc.tbl_a : nullptr};
-        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp, tables ? sc.tbl_b : nullptr};
+        // A prescreened operand is not read: its words are folded from its producer's table.
+        const ExpJob<T> ja{A, ta ? K : M, ta ? M : K, !ta, false, sc.row_exp,
+                           tables && !pre.a ? sc.tbl_a : nullptr, pre.a};
+        const ExpJob<T> jb{B, tb ? N : K, tb ? K : N, tb, false, sc.col_exp,
+                           tables && !pre.b ? sc.tbl_b : nullptr, pre.b};
         prefilter<T>(s, ja, jb, sc.gen, sc.suspect, gate, open);
     } else {
         risk = 0; // AllowGradual, or an empty reduction: no underflow screen
@@ -1905,23 +1959,30 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev, int engine, ProgramOpen open,
-                                const GemmEpilogue *epi)
+                                const GemmEpilogue *epi, Prescreen pre, bool *epi_fused)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (epi && epi->op != 0 && epi->op != kStepRelu && epi->op != kStepReluBackward)
         return hipErrorInvalidValue;
     bool done = false;
+    if (epi_fused)
+        *epi_fused = false;
     const hipError_t e =
         dtype == 0 ? strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                             (const float *)a, (const float *)b, (float *)c, policy,
-                                            scratch, fault, gate, ev, engine, open, epi, &done)
+                                            scratch, fault, gate, ev, engine, open, epi, &done, pre)
                    : strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                              (const double *)a, (const double *)b, (double *)c,
                                              policy, scratch, fault, gate, ev, engine, open, epi,
-                                             &done);
-    if (e != hipSuccess || !epi || epi->op == 0 || done)
+                                             &done, pre);
+    if (e != hipSuccess || !epi || epi->op == 0)
         return e;
+    if (done) {
+        if (epi_fused)
+            *epi_fused = true;
+        return e;
+    }
     // The tile kernel that ran has no such epilogue: the node's own kernel follows.
     const uint64_t n = rows * cols;
     if (epi->op == kStepRelu)

@@ -508,6 +508,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
         if (sub) // rows m0 + wm .. m0 + wm + 31 of columns c and c + 1 (c even): one block
             flag_sum_block(sck, m0 + wm, c);
         uint64_t ekey = kNoFault; // the epilogue node's first fault in this lane
+        // The node's exponents for its superslab tables: per row of the lane (over its two
+        // columns) and per column (over its 16 rows).
+        const bool tbl = EPI != 0 && (epi.tbl_rows != nullptr || epi.tbl_cols != nullptr);
+        int erow[EPI != 0 ? 16 : 1];
+        int ecol0 = kExpNone, ecol1 = kExpNone;
         // The ReLU backward's input at the lane's 32 cells, all loaded before the first
         // store (a load after each store would wait out its latency 16 times).
         float2 xin[EPI == kStepReluBackward ? 16 : 1];
@@ -552,13 +557,68 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 }
                 *reinterpret_cast<float2 *>(&static_cast<float *>(epi.out)[(size_t)row * N + c]) =
                     make_float2(r0, r1);
+                if (tbl) {
+                    const int e0 = ilog2_abs(r0), e1 = ilog2_abs(r1);
+                    erow[r] = e0 < e1 ? e0 : e1;
+                    ecol0 = e0 < ecol0 ? e0 : ecol0;
+                    ecol1 = e1 < ecol1 ? e1 : ecol1;
+                }
                 const uint64_t e = k0 != kOk ? pack_fault(cell, k0)
                                  : k1 != kOk ? pack_fault(cell + 1, k1) : kNoFault;
                 ekey = e < ekey ? e : ekey;
             }
         }
-        if constexpr (EPI != 0)
+        if constexpr (EPI != 0) {
+            if (epi.tbl_rows != nullptr) {
+                // Row minima over the wave's 64 columns (one superslab): each exchange among
+                // the 32 lanes of a half hands over half of the rows still held, so after
+                // five the lane holds row r = col / 2 (16 exchanges rather than 80).
+#pragma unroll
+                for (int w = 8; w >= 1; w >>= 1) {
+                    const int bit = 2 * w; // partner lane: col ^ bit
+                    const bool upper = (col & bit) != 0;
+#pragma unroll
+                    for (int i = 0; i < w; i++) {
+                        const int give = upper ? erow[i] : erow[i + w];
+                        const int keep = upper ? erow[i + w] : erow[i];
+                        const int got = __shfl_xor(give, bit, 64);
+                        erow[i] = got < keep ? got : keep;
+                    }
+                }
+                {
+                    const int got = __shfl_xor(erow[0], 1, 64);
+                    const int e = got < erow[0] ? got : erow[0];
+                    const int r = col >> 1;
+                    if ((col & 1) == 0) {
+                        const int row = m0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
+                        epi.tbl_rows[(size_t)row * (N / 64) + (n0 + wn) / 64] = scan_exp(e);
+                    }
+                }
+            }
+            if (epi.tbl_cols != nullptr) {
+                // Column minima over the wave's 32 rows; the two waves of a 64-row superslab
+                // (wm and wm + 32, the same columns) meet in LDS.
+                __shared__ int csub[2][Cfg::BN];
+                int o = __shfl_xor(ecol0, 32, 64);
+                ecol0 = o < ecol0 ? o : ecol0;
+                o = __shfl_xor(ecol1, 32, 64);
+                ecol1 = o < ecol1 ? o : ecol1;
+                const int ss = wm / 64, lead = (wm / 32) % 2 == 0;
+                if (lead && half == 0) {
+                    csub[ss][wn + 2 * col] = ecol0;
+                    csub[ss][wn + 2 * col + 1] = ecol1;
+                }
+                __syncthreads();
+                if (!lead && half == 0) {
+                    const int p0 = csub[ss][wn + 2 * col], p1 = csub[ss][wn + 2 * col + 1];
+                    const int f0 = p0 < ecol0 ? p0 : ecol0, f1 = p1 < ecol1 ? p1 : ecol1;
+                    short *t = epi.tbl_cols + (size_t)(m0 / 64 + ss) * N + c;
+                    t[0] = scan_exp(f0);
+                    t[1] = scan_exp(f1);
+                }
+            }
             wave_record_fault(ekey, epi.fault, epi.gate);
+        }
         block_record_min<Cfg::kThreads / 64>(key, suspect);
         return;
     }

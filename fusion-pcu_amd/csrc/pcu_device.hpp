@@ -491,6 +491,29 @@ __device__ __forceinline__ bool tile_exp_sum_below(const unsigned long long *row
 // still sum far above any threshold).
 constexpr short kScanExpNone = 16000;
 
+constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
+
+// floor(log2 |v|) of a finite nonzero v (subnormals included), kExpNone for zero and
+// non-finite values. Branch-free: the exponent screen applies it to every element of both
+// operands.
+__device__ __forceinline__ int ilog2_abs(float v)
+{
+    const uint32_t b = bits_of(v) & 0x7fffffffu, e = b >> 23;
+    const int sub = (31 - __clz(b | 1u)) - 149; // e == 0: b is the fraction
+    const int r = e ? (int)e - 127 : sub;
+    return (e == 0xff || b == 0) ? kExpNone : r;
+}
+__device__ __forceinline__ int ilog2_abs(double v)
+{
+    const uint64_t b = bits_of(v) & 0x7fffffffffffffffull, e = b >> 52;
+    const int sub = (63 - __clzll(b | 1ull)) - 1074;
+    const int r = e ? (int)e - 1023 : sub;
+    return (e == 0x7ff || b == 0) ? kExpNone : r;
+}
+// A superslab table entry from a folded exponent, and back.
+__device__ __forceinline__ short scan_exp(int e) { return (short)(e == kExpNone ? kScanExpNone : e); }
+__device__ __forceinline__ int unscan_exp(short t) { return t == kScanExpNone ? kExpNone : (int)t; }
+
 // Gating of the partial-sum check in a checking tile, by superslab (64 k). Products of at
 // least 2^thr (thr = -103, binary64 -970), and zero, are multiples of the smallest normal
 // 2^-126 (2^-1022), and so is every rounded sum of such multiples: a partial sum can only be

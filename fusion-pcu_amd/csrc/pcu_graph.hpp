@@ -117,6 +117,11 @@ struct Prepared {
     std::vector<uint32_t> gemm_epi;
     std::vector<char> epi_member;
     std::vector<uint32_t> prog_pos;
+    // The superslab tables (see Prescreen) that such an epilogue writes for the strict F32
+    // MatMuls reading its node's value, per node: along its rows and down its columns (null:
+    // not wanted). Those MatMuls then fold their screen words from the tables instead of
+    // reading the value again.
+    std::vector<void *> pre_rows, pre_cols;
     std::vector<Route> route;       // per node: scalar IR, strict or native compound
     std::vector<void *> dense_uniform;
     std::vector<void *> constant_buf; // resident copy of each planned Constant, uploaded at build

@@ -71,6 +71,11 @@ struct GemmEpilogue {
     void *out = nullptr;
     unsigned long long *fault = nullptr;
     NodeGate gate{nullptr, 0};
+    // Superslab tables of the node's value for the MatMuls that read it, or null: the
+    // smallest exponent (kScanExpNone for zero and non-finite) of each run of 64 along a
+    // row, tbl_rows[row * (N / 64) + column / 64], and down a column,
+    // tbl_cols[(row / 64) * N + column]. Written only where the epilogue runs (whole tiles).
+    short *tbl_rows = nullptr, *tbl_cols = nullptr;
 };
 
 struct ChainLaunch {
@@ -177,15 +182,24 @@ struct ProgramOpen {
     unsigned long long value = 0;
     unsigned int *gate = nullptr;
 };
+// Operands whose exponent screen its producer already wrote, as superslab tables in the
+// screen's own layouts: op(A)'s rows (a: x-major [M][K/64] when A is untransposed,
+// superslab-major [K/64][M] when transposed) and op(B)'s columns (b: superslab-major
+// [K/64][N] when B is untransposed, x-major [N][K/64] when transposed). The screen then folds
+// their words from these tables instead of reading the operand.
+struct Prescreen {
+    const short *a = nullptr, *b = nullptr;
+};
 // With `epi`, the MatMul also evaluates that elementwise node: in the tile kernel's
-// epilogue where the kernel supports it (whole 128 x 128 matrix-core tiles), else as its own
-// kernel right after the tile kernel.
+// epilogue where the kernel supports it (whole 128 x 128 matrix-core tiles: *epi_fused set,
+// and the epilogue's tables written), else as its own kernel right after the tile kernel.
 hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_t inner,
                                 uint64_t cols, bool transpose_left, bool transpose_right,
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto,
-                                ProgramOpen open = {}, const GemmEpilogue *epi = nullptr);
+                                ProgramOpen open = {}, const GemmEpilogue *epi = nullptr,
+                                Prescreen pre = {}, bool *epi_fused = nullptr);
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,

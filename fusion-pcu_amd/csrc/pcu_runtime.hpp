@@ -145,9 +145,12 @@ struct Ctx {
     // ReLU backward with it as upstream), evaluated with the MatMul (op, policy, x and out
     // from `epi`). It is the program node epi_after nodes after the MatMul's: its fault word
     // and gate are filled in here, and the caller adds it there with add_fused_node.
+    // pre: operands whose screen their producer wrote (see Prescreen); *epi_fused tells
+    // whether the epilogue ran in the tile kernel (and wrote the tables `epi` asked for).
     pcu_status op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl, int tr,
                          const void *a, const void *b, void *c, int policy, bool noalloc = false,
-                         GemmEpilogue *epi = nullptr, uint32_t epi_after = 0);
+                         GemmEpilogue *epi = nullptr, uint32_t epi_after = 0, Prescreen pre = {},
+                         bool *epi_fused = nullptr);
     // Adds the program node of an elementwise node already evaluated with its MatMul;
     // `expect` is the fault word op_matmul gave it.
     pcu_status add_fused_node(uint64_t n, const unsigned long long *expect);

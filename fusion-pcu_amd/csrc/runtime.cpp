@@ -707,8 +707,10 @@ static bool matmul_out_overlaps(int dtype, uint64_t rows, uint64_t inner, uint64
 
 pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t cols, int tl,
                           int tr, const void *a, const void *b, void *c, int policy, bool noalloc,
-                          GemmEpilogue *epi, uint32_t epi_after)
+                          GemmEpilogue *epi, uint32_t epi_after, Prescreen pre, bool *epi_fused)
 {
+    if (epi_fused)
+        *epi_fused = false;
     if (!valid_dtype(dtype) || !valid_policy(policy) || !c || ((rows * inner) && !a) ||
         ((inner * cols) && !b)) {
         fail("strict_matmul: invalid argument");
@@ -838,7 +840,8 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         return st;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
-                                        timed ? ev : nullptr, matmul_engine, open, epi);
+                                        timed ? ev : nullptr, matmul_engine, open, epi,
+                                        noalloc ? Prescreen{} : pre, epi_fused);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
     if (timed) {

@@ -594,3 +594,93 @@ def test_relu_backward_epilogue_after_another_matmul(G, pcu_pkg, dtype):
             finally:
                 for v in dev.values():
                     v.free()
+
+
+@pytest.mark.parametrize("case", ["a_rows", "a_cols", "b_cols", "b_rows", "back_a_rows"])
+def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg, case):
+    """A strict F32 MatMul whose operand is the value of a ReLU (or ReLU backward) that an
+    earlier MatMul evaluated in its epilogue takes that operand's exponent screen from the
+    superslab tables the epilogue wrote: op(A) rows or columns (A untransposed or
+    transposed), op(B) columns or rows. A tiny product planted in the consumer is flagged
+    only by the producer's tables (the consumer no longer reads the operand for its screen),
+    so its underflow fault, with its cell and k, must match the oracle; so must a clean run's
+    bits and an invalid operand elsewhere."""
+    dt = np.float32
+    ctx = G.default_context()
+    rng = np.random.default_rng(43)
+    m, k1, n, w = 2048, 64, 2048, 128
+    back = case.startswith("back")
+    g = G.Graph()
+    g.set_numerical_mode(True)
+    x, w1 = g.input((m, k1), dt), g.input((k1, n), dt)
+    xr = g.input((m, n), dt)
+    prod = g.matmul(x, w1)
+    h = g.relu_backward(xr, prod) if back else g.relu(prod)
+    if case in ("a_rows", "back_a_rows"):
+        wq = g.input((n, w), dt)
+        q = g.matmul(h, wq)
+    elif case == "a_cols":
+        wq = g.input((m, w), dt)
+        q = g.matmul(h, wq, True, False)
+    elif case == "b_cols":
+        wq = g.input((w, m), dt)
+        q = g.matmul(wq, h)
+    else:
+        wq = g.input((w, n), dt)
+        q = g.matmul(wq, h, False, True)
+    prep = g.prepare(ctx, [q, h])
+    ref = og.Graph()
+    ref.mode = "Strict"
+    rx, rw1, rxr = ref.input((m, k1), dt), ref.input((k1, n), dt), ref.input((m, n), dt)
+    rprod = ref.matmul(rx, rw1)
+    rh = ref.relu_backward(rxr, rprod) if back else ref.relu(rprod)
+    wshape = {"a_rows": (n, w), "back_a_rows": (n, w), "a_cols": (m, w), "b_cols": (w, m), "b_rows": (w, n)}[case]
+    rwq = ref.input(wshape, dt)
+    tl, tr = case == "a_cols", case == "b_rows"
+    rq = ref.matmul(rh, rwq, tl, tr) if case.startswith(("a", "back")) else ref.matmul(rwq, rh, tl, tr)
+    tiny = dt(2.0 ** -50)
+    for plant in ("none", "tiny", "invalid"):
+        vx = rng.uniform(-1, 1, (m, k1)).astype(dt)
+        vw1 = rng.uniform(-1, 1, (k1, n)).astype(dt)
+        vxr = rng.uniform(0.25, 1, (m, n)).astype(dt)  # the ReLU backward passes its upstream
+        vw = rng.uniform(-1, 1, wshape).astype(dt)
+        if plant == "tiny":
+            small = dt(1.2345 * 2.0 ** -30)  # a product with a value near 2^-100 is tiny, inexact
+            if case in ("a_rows", "back_a_rows", "b_rows"):
+                i = m // 3  # value row i near 2^-100
+                vx[i, :] = 0
+                vx[i, 0] = tiny
+                vw1[0, :] = (rng.uniform(0.5, 1, n) * tiny).astype(dt)
+            else:
+                j = n // 3  # value column j near 2^-100
+                vw1[:, j] = 0
+                vw1[0, j] = tiny
+                vx[:, 0] = (rng.uniform(0.5, 1, m) * tiny).astype(dt)
+            if case.startswith(("a", "back")):
+                vw[:, w // 2] = small
+            else:
+                vw[w // 2, :] = small
+        if plant == "invalid":
+            vw[wshape[0] - 1, 3] = np.nan
+        vals, rf = ref.evaluate({rx: vx, rw1: vw1, rxr: vxr, rwq: vw}, [rq, rh])
+        assert (rf is None) == (plant == "none"), (plant, rf)
+        if plant == "tiny":
+            assert rf.node == rq and int(rf.fault.kind) == 4, rf  # the consumer's underflow
+        dev = {x: ctx.upload(vx), w1: ctx.upload(vw1), xr: ctx.upload(vxr), wq: ctx.upload(vw)}
+        try:
+            if rf is None:
+                prep.execute([dev[i].ptr for i in prep.input_ids])
+                for j2, want in enumerate((rq, rh)):
+                    d = prep.output_desc[j2]
+                    have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(j2), d["shape"], d["dtype"]).numpy()
+                    np.testing.assert_array_equal(_bits(have), _bits(vals[want]))
+            else:
+                with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                    prep.execute([dev[i].ptr for i in prep.input_ids])
+                tf = exc.value.tensor_fault
+                assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                    (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                     rf.fault.kind), (case, plant)
+        finally:
+            for v in dev.values():
+                v.free()
