@@ -884,7 +884,10 @@ pcu_status Prepared::build(Ctx *c, const Graph &g, const std::vector<uint32_t> &
             if (!epi_member[r] || graph.nodes[r].dtype != 0 || graph.nodes[r].shape.size() != 2)
                 continue;
             const bool transposed = side == 0 ? qn.tl : qn.tr;
-            (side == 0 ? !transposed : transposed) ? (void)(want_rows[r] = 1) : (void)(want_cols[r] = 1);
+            if (side == 0 ? !transposed : transposed)
+                want_rows[r] = 1;
+            else
+                want_cols[r] = 1;
         }
     }
     // The ordered MSE sum runs on the side stream when nothing in the plan consumes its

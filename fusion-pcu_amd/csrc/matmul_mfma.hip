@@ -603,7 +603,8 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::kWavesPerSimd) void k_strict_ge
                 ecol0 = o < ecol0 ? o : ecol0;
                 o = __shfl_xor(ecol1, 32, 64);
                 ecol1 = o < ecol1 ? o : ecol1;
-                const int ss = wm / 64, lead = (wm / 32) % 2 == 0;
+                const int ss = wm / 64;
+                const bool lead = (wm / 32) % 2 == 0;
                 if (lead && half == 0) {
                     csub[ss][wn + 2 * col] = ecol0;
                     csub[ss][wn + 2 * col + 1] = ecol1;
