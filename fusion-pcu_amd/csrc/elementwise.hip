@@ -334,14 +334,28 @@ template <typename T> __device__ __forceinline__ uint32_t chain_classify(int op,
     return classify_div(a, b, r, policy);
 }
 
+// A chain's step operations known when the kernel is compiled: op of step s in bits
+// 4s..4s+3 of SIG, or SIG < 0 (read from the launch). The common chains get kernels of
+// their own, with the other operations' code folded away.
+constexpr int chain_sig_op(int sig, int s) { return sig < 0 ? -1 : (sig >> (4 * s)) & 15; }
+constexpr int chain_sig(int op0, int op1, int op2 = -1, int op3 = -1)
+{
+    return op0 | op1 << 4 | (op2 < 0 ? 0 : op2 << 8) | (op3 < 0 ? 0 : op3 << 12);
+}
+constexpr int kSigSubMul = chain_sig(kOpSub, kOpMul);                          // MSE gradient
+constexpr int kSigAddRelu = chain_sig(kOpAdd, kStepRelu);                       // bias + ReLU
+constexpr int kSigSubMulReluBack = chain_sig(kOpSub, kOpMul, kStepReluBackward); // C1 backward
+
 // The other operand of step S on the lanes [base, base + W) (nothing for a ReLU).
-template <typename T, bool VEC, int S>
+template <typename T, bool VEC, int S, int SIG>
 __device__ __forceinline__ void chain_other(const ChainLaunch &c, uint64_t base, uint64_t n,
                                             T (&o)[Lanes<T, VEC>::W])
 {
     constexpr int W = Lanes<T, VEC>::W;
     const ChainStep &st = c.step[S];
-    if (S >= c.steps || st.op == kStepRelu)
+    constexpr int kop = chain_sig_op(SIG, S);
+    const int op = kop >= 0 ? kop : st.op;
+    if (S >= c.steps || op == kStepRelu)
         return;
     if (st.other) {
         load_lanes<T, VEC>((const T *)st.other, base, n, o);
@@ -353,17 +367,59 @@ __device__ __forceinline__ void chain_other(const ChainLaunch &c, uint64_t base,
     }
 }
 
+// The first fault of a chain step on the lanes [base, base + W) (kNoFault: none), the rare
+// path once a lane is suspect. Out of line, so that the classifiers' code and registers stay
+// out of the streaming loop (inlined into each step they spilled scalar registers into
+// vector lanes).
+template <typename T, int W> struct LaneVals {
+    T x[W];
+};
+template <typename T, int W>
+__device__ __forceinline__ uint64_t chain_first_fault_body(int op, int policy, bool right,
+                                                           const LaneVals<T, W> &v,
+                                                           const LaneVals<T, W> &o,
+                                                           const LaneVals<T, W> &r, uint64_t base,
+                                                           uint64_t n)
+{
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        if (base + j >= n)
+            break;
+        uint32_t kind;
+        if (op == kStepRelu) {
+            kind = classify_relu(v.x[j], r.x[j], policy);
+        } else {
+            const T a = right ? o.x[j] : v.x[j], b = right ? v.x[j] : o.x[j];
+            kind = op == kStepReluBackward ? classify_relu_backward(a, b, r.x[j], policy)
+                                           : chain_classify(op, a, b, r.x[j], policy);
+        }
+        if (kind != kOk)
+            return pack_fault(base + j, kind);
+    }
+    return kNoFault;
+}
+// The call itself makes the kernel keep its scalar arguments in vector lanes across it, so
+// the kernels with their operations fixed at compile time (small once folded) inline it.
+template <typename T, int W>
+__device__ __noinline__ uint64_t chain_first_fault(int op, int policy, bool right, LaneVals<T, W> v,
+                                                   LaneVals<T, W> o, LaneVals<T, W> r,
+                                                   uint64_t base, uint64_t n)
+{
+    return chain_first_fault_body<T, W>(op, policy, right, v, o, r, base, n);
+}
+
 // Step S of a chain on the lanes [base, base + W): v holds the value the step takes and is
 // replaced by the step's result, o the step's other operand (chain_other); key keeps the
 // step's first fault in this thread.
-template <typename T, bool VEC, int S>
+template <typename T, bool VEC, int S, int SIG>
 __device__ __forceinline__ void chain_step(const ChainLaunch &c, uint64_t base, uint64_t n,
                                            T (&v)[Lanes<T, VEC>::W], const T (&o)[Lanes<T, VEC>::W],
                                            uint64_t &key)
 {
     constexpr int W = Lanes<T, VEC>::W;
     const ChainStep &st = c.step[S];
-    const int op = st.op, policy = st.policy;
+    constexpr int kop = chain_sig_op(SIG, S);
+    const int op = kop >= 0 ? kop : st.op, policy = st.policy;
     const bool right = st.chain_right != 0;
     T r[W];
     bool any = false;
@@ -392,31 +448,32 @@ __device__ __forceinline__ void chain_step(const ChainLaunch &c, uint64_t base, 
     if (st.out)
         store_lanes<T, VEC>((T *)st.out, base, n, r);
     if (any && key == kNoFault) {
+        LaneVals<T, W> lv, lo, lr;
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            if (base + j >= n || key != kNoFault)
-                continue;
-            uint32_t kind;
-            if (op == kStepRelu) {
-                kind = classify_relu(v[j], r[j], policy);
-            } else {
-                const T a = right ? o[j] : v[j], b = right ? v[j] : o[j];
-                kind = op == kStepReluBackward ? classify_relu_backward(a, b, r[j], policy)
-                                               : chain_classify(op, a, b, r[j], policy);
-            }
-            if (kind != kOk)
-                key = pack_fault(base + j, kind);
+            lv.x[j] = v[j];
+            lo.x[j] = o[j];
+            lr.x[j] = r[j];
         }
+        if constexpr (kop >= 0)
+            key = chain_first_fault_body<T, W>(op, policy, right, lv, lo, lr, base, n);
+        else
+            key = chain_first_fault<T, W>(op, policy, right, lv, lo, lr, base, n);
     }
 #pragma unroll
     for (int j = 0; j < W; j++)
         v[j] = r[j];
 }
 
-template <typename T, bool VEC>
+// NS = c.steps, a template argument: a kernel for all four steps held every step's
+// parameters and registers at once and spilled scalar registers into vector lanes (about 750
+// lane reads; a two-step chain ran at half the speed of one checked binary op over the
+// same bytes).
+template <typename T, bool VEC, int NS, int SIG = -1>
 __global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n, NodeGate gate)
 {
-    static_assert(kChainMaxSteps == 4, "one chain_step call per step below");
+    static_assert(NS >= 1 && NS <= kChainMaxSteps && kChainMaxSteps == 4,
+                  "one chain_step call per step below");
     if (wave_gate_closed(gate))
         return;
     constexpr int W = Lanes<T, VEC>::W;
@@ -428,24 +485,27 @@ __global__ __launch_bounds__(kEwThreads) void k_chain(ChainLaunch c, uint64_t n,
         // out together, one round trip, instead of one after each step's stores.
         T v[W], o0[W], o1[W], o2[W], o3[W];
         load_lanes<T, VEC>((const T *)c.head, base, n, v);
-        chain_other<T, VEC, 0>(c, base, n, o0);
-        chain_other<T, VEC, 1>(c, base, n, o1);
-        chain_other<T, VEC, 2>(c, base, n, o2);
-        chain_other<T, VEC, 3>(c, base, n, o3);
-        chain_step<T, VEC, 0>(c, base, n, v, o0, k0);
-        if (c.steps > 1)
-            chain_step<T, VEC, 1>(c, base, n, v, o1, k1);
-        if (c.steps > 2)
-            chain_step<T, VEC, 2>(c, base, n, v, o2, k2);
-        if (c.steps > 3)
-            chain_step<T, VEC, 3>(c, base, n, v, o3, k3);
+        chain_other<T, VEC, 0, SIG>(c, base, n, o0);
+        if constexpr (NS > 1)
+            chain_other<T, VEC, 1, SIG>(c, base, n, o1);
+        if constexpr (NS > 2)
+            chain_other<T, VEC, 2, SIG>(c, base, n, o2);
+        if constexpr (NS > 3)
+            chain_other<T, VEC, 3, SIG>(c, base, n, o3);
+        chain_step<T, VEC, 0, SIG>(c, base, n, v, o0, k0);
+        if constexpr (NS > 1)
+            chain_step<T, VEC, 1, SIG>(c, base, n, v, o1, k1);
+        if constexpr (NS > 2)
+            chain_step<T, VEC, 2, SIG>(c, base, n, v, o2, k2);
+        if constexpr (NS > 3)
+            chain_step<T, VEC, 3, SIG>(c, base, n, v, o3, k3);
     }
     wave_record_fault(k0, c.step[0].fault, gate);
-    if (c.steps > 1)
+    if constexpr (NS > 1)
         wave_record_fault(k1, c.step[1].fault, NodeGate{gate.word, gate.node + 1});
-    if (c.steps > 2)
+    if constexpr (NS > 2)
         wave_record_fault(k2, c.step[2].fault, NodeGate{gate.word, gate.node + 2});
-    if (c.steps > 3)
+    if constexpr (NS > 3)
         wave_record_fault(k3, c.step[3].fault, NodeGate{gate.word, gate.node + 3});
 }
 
@@ -1817,10 +1877,36 @@ static hipError_t chain_t(hipStream_t s, uint64_t n, const ChainLaunch &c, NodeG
     for (int i = 0; i < c.steps; i++)
         vec = vec && aligned16(c.step[i].other) && aligned16(c.step[i].out);
     const unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
-    if (vec)
-        hipLaunchKernelGGL((k_chain<T, true>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
-    else
-        hipLaunchKernelGGL((k_chain<T, false>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+    int sig = 0;
+    for (int i = 0; i < c.steps && i < kChainMaxSteps; i++)
+        sig |= c.step[i].op << (4 * i);
+    const int key = c.steps * 2 + (vec ? 1 : 0);
+    if (c.steps == 2 && sig == kSigSubMul) {
+        if (vec) hipLaunchKernelGGL((k_chain<T, true, 2, kSigSubMul>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        else hipLaunchKernelGGL((k_chain<T, false, 2, kSigSubMul>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        return hipGetLastError();
+    }
+    if (c.steps == 2 && sig == kSigAddRelu) {
+        if (vec) hipLaunchKernelGGL((k_chain<T, true, 2, kSigAddRelu>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        else hipLaunchKernelGGL((k_chain<T, false, 2, kSigAddRelu>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        return hipGetLastError();
+    }
+    if (c.steps == 3 && sig == kSigSubMulReluBack) {
+        if (vec) hipLaunchKernelGGL((k_chain<T, true, 3, kSigSubMulReluBack>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        else hipLaunchKernelGGL((k_chain<T, false, 3, kSigSubMulReluBack>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate);
+        return hipGetLastError();
+    }
+    switch (key) {
+    case 3: hipLaunchKernelGGL((k_chain<T, true, 1>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 2: hipLaunchKernelGGL((k_chain<T, false, 1>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 5: hipLaunchKernelGGL((k_chain<T, true, 2>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 4: hipLaunchKernelGGL((k_chain<T, false, 2>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 7: hipLaunchKernelGGL((k_chain<T, true, 3>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 6: hipLaunchKernelGGL((k_chain<T, false, 3>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 9: hipLaunchKernelGGL((k_chain<T, true, 4>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    case 8: hipLaunchKernelGGL((k_chain<T, false, 4>), dim3(grid), dim3(kEwThreads), 0, s, c, n, gate); break;
+    default: return hipErrorInvalidValue; // a chain has 1 to 4 steps
+    }
     return hipGetLastError();
 }
 
