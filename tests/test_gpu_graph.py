@@ -596,15 +596,17 @@ def test_relu_backward_epilogue_after_another_matmul(G, pcu_pkg, dtype):
                     v.free()
 
 
+@pytest.mark.parametrize("policy", [0, 1], ids=["ieee", "reject"])
 @pytest.mark.parametrize("case", ["a_rows", "a_cols", "b_cols", "b_rows", "back_a_rows"])
-def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg, case):
+def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg, case, policy):
     """A strict F32 MatMul whose operand is the value of a ReLU (or ReLU backward) that an
     earlier MatMul evaluated in its epilogue takes that operand's exponent screen from the
     superslab tables the epilogue wrote: op(A) rows or columns (A untransposed or
     transposed), op(B) columns or rows. A tiny product planted in the consumer is flagged
     only by the producer's tables (the consumer no longer reads the operand for its screen),
     so its underflow fault, with its cell and k, must match the oracle; so must a clean run's
-    bits and an invalid operand elsewhere."""
+    bits and an invalid operand elsewhere. Under RejectSubnormal (every node) the tables
+    also gate the consumer's partial-sum check."""
     dt = np.float32
     ctx = G.default_context()
     rng = np.random.default_rng(43)
@@ -628,6 +630,8 @@ def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg,
     else:
         wq = g.input((w, n), dt)
         q = g.matmul(wq, h, False, True)
+    for node in (prod, h, q):
+        g.set_underflow_policy(node, policy)
     prep = g.prepare(ctx, [q, h])
     ref = og.Graph()
     ref.mode = "Strict"
@@ -638,14 +642,24 @@ def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg,
     rwq = ref.input(wshape, dt)
     tl, tr = case == "a_cols", case == "b_rows"
     rq = ref.matmul(rh, rwq, tl, tr) if case.startswith(("a", "back")) else ref.matmul(rwq, rh, tl, tr)
+    for node in (rprod, rh, rq):
+        ref.nodes[node].policy = policy
     tiny = dt(2.0 ** -50)
-    for plant in ("none", "tiny", "invalid"):
+    for plant in ("none", "tiny", "sum", "invalid"):
         vx = rng.uniform(-1, 1, (m, k1)).astype(dt)
         vw1 = rng.uniform(-1, 1, (k1, n)).astype(dt)
         vxr = rng.uniform(0.25, 1, (m, n)).astype(dt)  # the ReLU backward passes its upstream
         vw = rng.uniform(-1, 1, wshape).astype(dt)
-        if plant == "tiny":
-            small = dt(1.2345 * 2.0 ** -30)  # a product with a value near 2^-100 is tiny, inexact
+        if plant in ("tiny", "sum"):
+            # "tiny": a product with a value near 2^-100 is tiny and inexact. "sum": normal
+            # products near 2^-120 of both signs, whose running sums can come out subnormal
+            # (a fault under RejectSubnormal only, found by the partial-sum check the tables
+            # gate; exact under IEEE).
+            small = dt(1.2345 * 2.0 ** -30)
+            if plant == "sum":
+                small = (rng.choice([-1.0, 1.0], size=wshape[0] if case.startswith(("a", "back")) else wshape[1])
+                         * rng.uniform(0.5, 1.0, wshape[0] if case.startswith(("a", "back")) else wshape[1])
+                         * 2.0 ** -20).astype(dt)
             if case in ("a_rows", "back_a_rows", "b_rows"):
                 i = m // 3  # value row i near 2^-100
                 vx[i, :] = 0
@@ -663,8 +677,9 @@ def test_matmul_reads_its_operand_screen_from_the_producing_epilogue(G, pcu_pkg,
         if plant == "invalid":
             vw[wshape[0] - 1, 3] = np.nan
         vals, rf = ref.evaluate({rx: vx, rw1: vw1, rxr: vxr, rwq: vw}, [rq, rh])
-        assert (rf is None) == (plant == "none"), (plant, rf)
-        if plant == "tiny":
+        if plant != "sum":
+            assert (rf is None) == (plant == "none"), (plant, rf)
+        if plant == "tiny" or (plant == "sum" and rf is not None):
             assert rf.node == rq and int(rf.fault.kind) == 4, rf  # the consumer's underflow
         dev = {x: ctx.upload(vx), w1: ctx.upload(vw1), xr: ctx.upload(vxr), wq: ctx.upload(vw)}
         try:
