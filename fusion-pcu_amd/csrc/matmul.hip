@@ -1279,13 +1279,19 @@ __global__ __launch_bounds__(1024) void k_strict_gemm_replay(
     const unsigned long long *__restrict__ col_exp, int thr, int tiny_thr, int serial_screen,
     int tiny, int policy, const unsigned long long *suspect, const unsigned long long *row_flag,
     const unsigned long long *flag_first, const unsigned int *sum_flag, uint32_t flag_cols,
-    uint32_t gen, unsigned long long *fault, NodeGate gate)
+    uint32_t gen, unsigned long long *fault, NodeGate gate, ProgramClose close)
 {
     // No suspect cell: nothing to replay, whatever the gate says. Most launches end here,
-    // before the gate's block-wide read and its barrier.
+    // before the gate's block-wide read and its barrier; no wave writes a fault word then,
+    // so one wave may end the program at once.
     const uint64_t first = *suspect;
-    if (first == kNoFault || K == 0)
+    if (first == kNoFault || K == 0) {
+        if (close.words != nullptr && blockIdx.x == 0 && threadIdx.x < 64)
+            program_close_wave(close);
         return;
+    }
+    // The replay proper; its waves return on their own, then the workgroup takes its ticket.
+    [&]() {
     if (block_gate_closed(gate))
         return; // an earlier node faulted: that fault is the one reported
     const uint64_t cells = M * N;
@@ -1372,6 +1378,8 @@ __global__ __launch_bounds__(1024) void k_strict_gemm_replay(
             }
         }
     }
+    }();
+    program_close_block(close);
 }
 
 // ------------------------------------------------------------ small outputs
@@ -1394,10 +1402,12 @@ template <typename T> constexpr uint64_t fused_cells() { return sizeof(T) == 4 ?
 template <typename T, bool TA, bool TB>
 __global__ __launch_bounds__(256) void k_strict_gemm_fused(
     const T *__restrict__ A, const T *__restrict__ B, T *__restrict__ C, int M, int N, int K,
-    int thr, int risk, int policy, unsigned long long *fault, NodeGate gate)
+    int thr, int risk, int policy, unsigned long long *fault, NodeGate gate, ProgramClose close)
 {
-    if (block_gate_closed(gate))
+    if (block_gate_closed(gate)) {
+        program_close_block(close);
         return;
+    }
     constexpr int P = 16 / (int)sizeof(T), BKP = kFusedBK + P; // row pitch: one 16-byte pad
     __shared__ __align__(16) T As[16][BKP];
     __shared__ __align__(16) T Bs[16][BKP];
@@ -1504,8 +1514,10 @@ __global__ __launch_bounds__(256) void k_strict_gemm_fused(
         n_cand = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
     __syncthreads();
     const int nc = n_cand;
-    if (nc == 0)
+    if (nc == 0) {
+        program_close_block(close);
         return;
+    }
     for (int j = wave; j < nc; j += 4) {
         const int i = cand[j];
         const uint64_t cell = (uint64_t)(m0 + (i >> 4)) * N + n0 + (i & 15);
@@ -1522,6 +1534,7 @@ __global__ __launch_bounds__(256) void k_strict_gemm_fused(
         atomicMin(fault, best);
         gate_record(gate);
     }
+    program_close_block(close);
 }
 
 // ================================================================= launchers
@@ -1764,7 +1777,8 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                                   bool tb, const T *A, const T *B, T *C, int policy,
                                   MatmulScratch sc, unsigned long long *fault, NodeGate gate,
                                   hipEvent_t *ev, int engine, ProgramOpen open,
-                                  const GemmEpilogue *epi, bool *epi_done, Prescreen pre)
+                                  const GemmEpilogue *epi, bool *epi_done, Prescreen pre,
+                                  ProgramClose close)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -1798,10 +1812,10 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         const int m = (int)M, n = (int)N, k = (int)K;
         // The fused kernel walks every cell its exponents mark (no partial-sum check).
         const int fthr = reject ? sub_thr : tiny_thr;
-        if (!ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
-        else if (!ta && tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
-        else if (ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, true, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
-        else hipLaunchKernelGGL((k_strict_gemm_fused<T, true, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate);
+        if (!ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate, close);
+        else if (!ta && tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, false, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate, close);
+        else if (ta && !tb) hipLaunchKernelGGL((k_strict_gemm_fused<T, true, false>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate, close);
+        else hipLaunchKernelGGL((k_strict_gemm_fused<T, true, true>), grid, dim3(256), 0, s, A, B, C, m, n, k, fthr, risk, policy, fault, gate, close);
         if (ev) {
             (void)hipEventRecord(ev[2], s);
             (void)hipEventRecord(ev[3], s);
@@ -1907,7 +1921,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                        (int)ta, (int)tb, sc.row_exp, sc.col_exp, reject ? sub_thr : tiny_thr, tiny_thr,
                        serial_screen, (int)tiny, policy, (const unsigned long long *)sc.suspect,
                        (const unsigned long long *)sc.row_flag, (const unsigned long long *)sc.flag_first,
-                       (const unsigned int *)sck.flag, sc.flag_cols, sc.gen, fault, gate);
+                       (const unsigned int *)sck.flag, sc.flag_cols, sc.gen, fault, gate, close);
     if (ev)
         (void)hipEventRecord(ev[3], s);
     return hipGetLastError();
@@ -1959,11 +1973,15 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 const void *a, const void *b, void *c, int policy,
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev, int engine, ProgramOpen open,
-                                const GemmEpilogue *epi, Prescreen pre, bool *epi_fused)
+                                const GemmEpilogue *epi, Prescreen pre, bool *epi_fused,
+                                ProgramClose close)
 {
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (epi && epi->op != 0 && epi->op != kStepRelu && epi->op != kStepReluBackward)
+        return hipErrorInvalidValue;
+    // The program ends in the MatMul's last kernel only when nothing follows it.
+    if (close.words && ((epi && epi->op != 0) || rows == 0 || cols == 0 || !scratch.suspect))
         return hipErrorInvalidValue;
     bool done = false;
     if (epi_fused)
@@ -1971,11 +1989,12 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
     const hipError_t e =
         dtype == 0 ? strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                             (const float *)a, (const float *)b, (float *)c, policy,
-                                            scratch, fault, gate, ev, engine, open, epi, &done, pre)
+                                            scratch, fault, gate, ev, engine, open, epi, &done, pre,
+                                            close)
                    : strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                              (const double *)a, (const double *)b, (double *)c,
                                              policy, scratch, fault, gate, ev, engine, open, epi,
-                                             &done, pre);
+                                             &done, pre, close);
     if (e != hipSuccess || !epi || epi->op == 0)
         return e;
     if (done) {

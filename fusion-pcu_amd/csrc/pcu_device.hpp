@@ -491,6 +491,49 @@ __device__ __forceinline__ bool tile_exp_sum_below(const unsigned long long *row
 // still sum far above any threshold).
 constexpr short kScanExpNone = 16000;
 
+// A program's end by one wave (see ProgramClose): the words to the pinned mirror, reset,
+// the gate opened, then the sequence number, after a system-scope fence.
+__device__ __forceinline__ void program_close_wave(const ProgramClose &c)
+{
+    const int lane = threadIdx.x & 63;
+    for (uint64_t i = lane; i < c.n; i += 64) {
+        const unsigned long long w =
+            __hip_atomic_load(&c.words[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&c.host_words[i], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        c.words[i] = c.value;
+    }
+    if (lane == 0)
+        *c.gate = 0xffffffffu;
+    __threadfence_system();
+    if (lane == 0)
+        __hip_atomic_store(c.host_seq, (unsigned long long)c.seq, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Every workgroup of the launch calls it once, last thing, with all its threads: the last
+// workgroup to arrive ends the program. The words the end reads are written only by
+// device-scope atomics (fault records, the gate), which are complete once the barrier has
+// waited for the workgroup's memory operations, so no workgroup needs a device-scope
+// release (on this part one writes back and invalidates the XCD's L2: a fence in each of
+// the replay's 4096 waves cost a faulting 1024^3 call about 70 us); only the last one
+// acquires before it reads them.
+__device__ __forceinline__ void program_close_block(const ProgramClose &c)
+{
+    if (c.words == nullptr)
+        return;
+    __shared__ int last;
+    __syncthreads(); // the workgroup's fault records are done
+    if (threadIdx.x == 0)
+        last = atomicAdd(c.ticket, 1u) + 1u == gridDim.x * gridDim.y * gridDim.z;
+    __syncthreads();
+    if (last && threadIdx.x < 64) {
+        __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        if (threadIdx.x == 0)
+            *c.ticket = 0u; // every workgroup has taken its ticket
+        program_close_wave(c);
+    }
+}
+
 constexpr int kExpNone = 1 << 20; // zero or non-finite entry: contributes no tiny product
 
 // floor(log2 |v|) of a finite nonzero v (subnormals included), kExpNone for zero and

@@ -182,6 +182,22 @@ struct ProgramOpen {
     unsigned long long value = 0;
     unsigned int *gate = nullptr;
 };
+// The end of a program whose only node is this MatMul, done by the MatMul's last kernel
+// instead of a publication launch of its own: the n fault words go to the coherent pinned
+// mirror host_words and are reset to `value`, the stage gate is opened, and then the
+// sequence number `seq` is stored to host_seq (the host waits on it). `ticket` (zero between
+// launches) counts the workgroups or waves that have finished when the last of them must do
+// it. words == nullptr: no.
+struct ProgramClose {
+    unsigned long long *words = nullptr;
+    uint64_t n = 0;
+    unsigned long long value = 0;
+    unsigned int *gate = nullptr;
+    unsigned long long *host_words = nullptr;
+    unsigned long long *host_seq = nullptr;
+    uint64_t seq = 0;
+    unsigned int *ticket = nullptr;
+};
 // Operands whose exponent screen its producer already wrote, as superslab tables in the
 // screen's own layouts: op(A)'s rows (a: x-major [M][K/64] when A is untransposed,
 // superslab-major [K/64][M] when transposed) and op(B)'s columns (b: superslab-major
@@ -199,7 +215,8 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto,
                                 ProgramOpen open = {}, const GemmEpilogue *epi = nullptr,
-                                Prescreen pre = {}, bool *epi_fused = nullptr);
+                                Prescreen pre = {}, bool *epi_fused = nullptr,
+                                ProgramClose close = {});
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,

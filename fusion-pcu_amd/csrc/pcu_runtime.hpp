@@ -51,6 +51,9 @@ struct Ctx {
     unsigned long long *host_words = nullptr;
     unsigned long long *host_seq = nullptr;
     uint64_t pub_seq = 0;
+    // The open program's end is done by its only node's last kernel (a MatMul: see
+    // ProgramClose) under this sequence number; 0: read_words launches the publication.
+    uint64_t closed_seq = 0;
     bool in_program = false;
     bool implicit_program = false;
     bool words_pending = false; // the open program's words and gate await their reset

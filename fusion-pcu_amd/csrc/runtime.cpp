@@ -323,6 +323,7 @@ pcu_status Ctx::begin_program(bool implicit)
         return st;
     in_program = true;
     implicit_program = implicit;
+    closed_seq = 0;
     nodes.clear();
     // The previous program's end left the words reset and the gate open, unless it failed.
     words_pending = !words_clean;
@@ -444,18 +445,23 @@ pcu_status Ctx::read_words(size_t *used)
     *used = nodes.size();
     if (!*used)
         return hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
-    // Nodes that launched nothing (empty shapes) still have their words read.
-    if ((st = open_words()))
-        return st;
-    // One kernel copies the words into the coherent mirror, resets them and the gate for the
-    // next program (which then needs no opening launch), and stores this program's sequence
-    // number last; the host spins on that word. Against a D2H copy and a stream
-    // synchronization this saves the copy command and the runtime's wake-up.
-    const uint64_t seq = ++pub_seq;
-    if ((st = hip(launch_program_publish(stream, fault_words, *used, kNoFaultWord, gate_word(),
-                                         host_words, host_seq, seq),
-                  "program publish")))
-        return st;
+    uint64_t seq = closed_seq;
+    closed_seq = 0;
+    if (seq == 0) {
+        // Nodes that launched nothing (empty shapes) still have their words read.
+        if ((st = open_words()))
+            return st;
+        // One kernel copies the words into the coherent mirror, resets them and the gate for
+        // the next program (which then needs no opening launch), and stores this program's
+        // sequence number last; the host spins on that word. Against a D2H copy and a stream
+        // synchronization this saves the copy command and the runtime's wake-up. A program
+        // whose only node is a MatMul had its last kernel do the same (closed_seq).
+        seq = ++pub_seq;
+        if ((st = hip(launch_program_publish(stream, fault_words, *used, kNoFaultWord,
+                                             gate_word(), host_words, host_seq, seq),
+                      "program publish")))
+            return st;
+    }
     for (unsigned spin = 1;; spin++) {
         if (__atomic_load_n(host_seq, __ATOMIC_ACQUIRE) == seq)
             break;
@@ -838,12 +844,28 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
         (st = hip(launch_fill_u64(stream, (unsigned long long *)sc, clear_words, 0),
                   "clear MatMul screen words")))
         return st;
+    // A one-call program (this MatMul its only node) ends in the MatMul's last kernel: one
+    // launch fewer. The no-allocation call keeps the publication launch (its scratch is the
+    // device's shared array).
+    ProgramClose close;
+    if (implicit_program && first_node && !noalloc && !epi && s.suspect) {
+        close.words = fault_words;
+        close.n = nodes.size();
+        close.value = kNoFaultWord;
+        close.gate = gate_word();
+        close.host_words = host_words;
+        close.host_seq = host_seq;
+        close.seq = pub_seq + 1;
+        close.ticket = (unsigned int *)(s.suspect + 2); // the scratch head's third word
+    }
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
                                         timed ? ev : nullptr, matmul_engine, open, epi,
-                                        noalloc ? Prescreen{} : pre, epi_fused);
+                                        noalloc ? Prescreen{} : pre, epi_fused, close);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
+    if (close.words)
+        closed_seq = ++pub_seq;
     if (timed) {
         timings.push_back({PCU_KERNEL_GEMM_PREFILTER, ev[0], ev[1]});
         timings.push_back({PCU_KERNEL_STRICT_GEMM, ev[1], ev[2]});
