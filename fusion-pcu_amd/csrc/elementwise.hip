@@ -560,9 +560,11 @@ template <typename T, bool VEC>
 __global__ __launch_bounds__(kEwThreads) void k_sgd(const T *w,
                                                     const T *g, T rate,
                                                     T *out, uint64_t n, int policy,
-                                                    unsigned long long *fault, NodeGate gate)
+                                                    unsigned long long *fault, NodeGate gate,
+                                                    ProgramClose close)
 {
     sgd_range<T, VEC>(w, g, rate, out, n, policy, fault, gate, blockIdx.x, gridDim.x);
+    program_close_block(close);
 }
 
 // Two updates of one program in one launch: blocks [0, blocks0) take update 0, the rest
@@ -578,7 +580,8 @@ template <typename T> struct SgdPairArgs {
 };
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_sgd_pair(SgdPairArgs<T> a, int policy)
+__global__ __launch_bounds__(kEwThreads) void k_sgd_pair(SgdPairArgs<T> a, int policy,
+                                                         ProgramClose close)
 {
     const bool first = blockIdx.x < a.blocks0;
     const int u = first ? 0 : 1;
@@ -586,6 +589,7 @@ __global__ __launch_bounds__(kEwThreads) void k_sgd_pair(SgdPairArgs<T> a, int p
     const uint64_t nb = first ? a.blocks0 : gridDim.x - a.blocks0;
     sgd_range<T, VEC>(a.w[u], a.g[u], a.rate[u], a.out[u], a.n[u], policy, a.fault[u], a.gate[u],
                       bid, nb);
+    program_close_block(close);
 }
 
 // -------------------------------------------------------------------- MSE
@@ -1981,31 +1985,44 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                       : add_relu_t<double>(s, n, a, b, b_value, out, policy, fault_add, fault_relu, gate);
 }
 
+// An SGD launch ends its program (ProgramClose) only on a grid of at most kCloseMaxBlocks
+// workgroups: every workgroup takes one ticket on a single counter at its end, and the
+// tickets queue behind one another (1024 of them made a 2^20-element update 15 -> 24 us).
+
 template <typename T>
 static hipError_t sgd_t(hipStream_t s, uint64_t n, const void *w, const void *g, T rate,
-                        void *out, int policy, unsigned long long *fault, NodeGate gate)
+                        void *out, int policy, unsigned long long *fault, NodeGate gate,
+                        ProgramClose close, bool *closed)
 {
     constexpr int Wd = Vec<T>::width;
     bool vec = aligned16(w) && aligned16(g) && aligned16(out);
     unsigned grid = grid_for(vec ? (n + Wd - 1) / Wd : n);
+    if (grid > kCloseMaxBlocks)
+        close = ProgramClose{};
+    if (closed)
+        *closed = close.words != nullptr;
     if (vec)
-        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate);
+        hipLaunchKernelGGL((k_sgd<T, true>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate, close);
     else
-        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate);
+        hipLaunchKernelGGL((k_sgd<T, false>), dim3(grid), dim3(kEwThreads), 0, s, (const T *)w, (const T *)g, rate, (T *)out, n, policy, fault, gate, close);
     return hipGetLastError();
 }
 
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate)
+                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate,
+                      ProgramClose close, bool *closed)
 {
+    if (closed)
+        *closed = false;
     if (n == 0)
         return hipSuccess;
-    return dtype == 0 ? sgd_t<float>(s, n, w, g, (float)rate, out, policy, fault, gate)
-                      : sgd_t<double>(s, n, w, g, rate, out, policy, fault, gate);
+    return dtype == 0 ? sgd_t<float>(s, n, w, g, (float)rate, out, policy, fault, gate, close, closed)
+                      : sgd_t<double>(s, n, w, g, rate, out, policy, fault, gate, close, closed);
 }
 
 template <typename T>
-static hipError_t sgd_pair_t(hipStream_t s, const SgdJob &j0, const SgdJob &j1, int policy)
+static hipError_t sgd_pair_t(hipStream_t s, const SgdJob &j0, const SgdJob &j1, int policy,
+                             ProgramClose close, bool *closed)
 {
     constexpr int Wd = Vec<T>::width;
     const SgdJob *j[2] = {&j0, &j1};
@@ -2027,18 +2044,26 @@ static hipError_t sgd_pair_t(hipStream_t s, const SgdJob &j0, const SgdJob &j1, 
     }
     a.blocks0 = blocks[0];
     const dim3 grid(blocks[0] + blocks[1]);
+    if (grid.x > kCloseMaxBlocks)
+        close = ProgramClose{};
+    if (closed)
+        *closed = close.words != nullptr;
     if (vec)
-        hipLaunchKernelGGL((k_sgd_pair<T, true>), grid, dim3(kEwThreads), 0, s, a, policy);
+        hipLaunchKernelGGL((k_sgd_pair<T, true>), grid, dim3(kEwThreads), 0, s, a, policy, close);
     else
-        hipLaunchKernelGGL((k_sgd_pair<T, false>), grid, dim3(kEwThreads), 0, s, a, policy);
+        hipLaunchKernelGGL((k_sgd_pair<T, false>), grid, dim3(kEwThreads), 0, s, a, policy, close);
     return hipGetLastError();
 }
 
-hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy)
+hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy,
+                           ProgramClose close, bool *closed)
 {
+    if (closed)
+        *closed = false;
     if (j0.n == 0 || j1.n == 0)
         return hipErrorInvalidValue;
-    return dtype == 0 ? sgd_pair_t<float>(s, j0, j1, policy) : sgd_pair_t<double>(s, j0, j1, policy);
+    return dtype == 0 ? sgd_pair_t<float>(s, j0, j1, policy, close, closed)
+                      : sgd_pair_t<double>(s, j0, j1, policy, close, closed);
 }
 
 // Scratch of one MSE call: the squares, then the chunk sums and the chunk summaries.

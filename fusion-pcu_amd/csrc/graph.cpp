@@ -1034,6 +1034,16 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
     std::vector<uint32_t> prog_to_graph;
     std::vector<unsigned long long *> epi_word(graph.nodes.size(), nullptr);
     std::vector<char> tables_written(graph.nodes.size(), 0); // this execution, by an epilogue
+    // The program's last launching node: a strict SGD update (or pair) there ends the program
+    // in its own kernel instead of a publication launch.
+    uint32_t last_launch = UINT32_MAX;
+    for (uint32_t i : order) {
+        const Node &nd = graph.nodes[i];
+        if (nd.op == Op::Input || nd.op == Op::Constant || nd.op == Op::Uniform ||
+            fused_into[i] >= 0 || chain_member[i] || sgd_second[i])
+            continue;
+        last_launch = i;
+    }
     auto ptr = [&](uint32_t id) { return value_ptr(id, in, bank_w); };
     // The tables this execution's epilogues wrote for a strict F32 MatMul's operands.
     auto prescreen = [&](uint32_t q) {
@@ -1156,6 +1166,8 @@ pcu_status Prepared::execute(const std::vector<const void *> &in, pcu_fault *fau
             prog_to_graph.push_back(i);
             break;
         case Op::SgdUpdate:
+            if (i == last_launch && route[i] == Route::Strict && !epi_member[i])
+                ctx->close_with_next_op();
             if (route[i] == Route::Native) {
                 st = ctx->op_native_sgd(nd.dtype, n, ptr(nd.a), ptr(nd.b), nd.lr,
                                         nd.options.precision == 1, ptr(i));

@@ -344,8 +344,10 @@ __device__ __forceinline__ void program_open_block(const ProgramOpen &o)
         return;
     for (uint64_t i = threadIdx.x; i < o.n; i += blockDim.x)
         o.words[i] = o.value;
-    if (threadIdx.x == 0)
-        *o.gate = 0xffffffffu;
+    if (threadIdx.x == 0) {
+        o.gate[0] = 0xffffffffu;
+        o.gate[1] = 0u; // the ticket of an in-kernel program end (ProgramClose)
+    }
 }
 
 template <typename T>
@@ -1612,8 +1614,10 @@ __global__ void k_program_open(unsigned long long *words, uint64_t n, unsigned l
     const uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (uint64_t i = i0; i < n; i += (uint64_t)gridDim.x * blockDim.x)
         words[i] = value;
-    if (i0 == 0)
-        *gate = 0xffffffffu;
+    if (i0 == 0) {
+        gate[0] = 0xffffffffu;
+        gate[1] = 0u; // the ticket of an in-kernel program end (ProgramClose)
+    }
 }
 
 hipError_t launch_program_open(hipStream_t s, unsigned long long *words, uint64_t n, uint64_t value,
@@ -1778,7 +1782,7 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
                                   MatmulScratch sc, unsigned long long *fault, NodeGate gate,
                                   hipEvent_t *ev, int engine, ProgramOpen open,
                                   const GemmEpilogue *epi, bool *epi_done, Prescreen pre,
-                                  ProgramClose close)
+                                  ProgramClose close, bool *closed)
 {
     if (M == 0 || N == 0)
         return hipSuccess;
@@ -1809,6 +1813,10 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
         if (ev)
             (void)hipEventRecord(ev[1], s);
         const dim3 grid((unsigned)(((M + 15) / 16) * ((N + 15) / 16)));
+        if (grid.x > kCloseMaxBlocks)
+            close = ProgramClose{}; // the publication launch ends the program
+        if (closed)
+            *closed = close.words != nullptr;
         const int m = (int)M, n = (int)N, k = (int)K;
         // The fused kernel walks every cell its exponents mark (no partial-sum check).
         const int fthr = reject ? sub_thr : tiny_thr;
@@ -1917,6 +1925,8 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const int serial_screen = risk && !tiny;
     // 4096 waves in 256 workgroups: an empty launch (no suspect cell) dispatches a quarter of
     // the workgroups that 256-thread blocks would take.
+    if (closed)
+        *closed = close.words != nullptr;
     hipLaunchKernelGGL(k_strict_gemm_replay<T>, dim3(256), dim3(1024), 0, s, A, B, (const T *)C, M, N, K,
                        (int)ta, (int)tb, sc.row_exp, sc.col_exp, reject ? sub_thr : tiny_thr, tiny_thr,
                        serial_screen, (int)tiny, policy, (const unsigned long long *)sc.suspect,
@@ -1974,8 +1984,10 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 MatmulScratch scratch, unsigned long long *fault, NodeGate gate,
                                 hipEvent_t *ev, int engine, ProgramOpen open,
                                 const GemmEpilogue *epi, Prescreen pre, bool *epi_fused,
-                                ProgramClose close)
+                                ProgramClose close, bool *closed)
 {
+    if (closed)
+        *closed = false;
     if (rows > (uint64_t)INT_MAX || cols > (uint64_t)INT_MAX || inner > (uint64_t)INT_MAX)
         return hipErrorInvalidValue;
     if (epi && epi->op != 0 && epi->op != kStepRelu && epi->op != kStepReluBackward)
@@ -1990,11 +2002,11 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
         dtype == 0 ? strict_matmul_t<float>(s, rows, inner, cols, transpose_left, transpose_right,
                                             (const float *)a, (const float *)b, (float *)c, policy,
                                             scratch, fault, gate, ev, engine, open, epi, &done, pre,
-                                            close)
+                                            close, closed)
                    : strict_matmul_t<double>(s, rows, inner, cols, transpose_left, transpose_right,
                                              (const double *)a, (const double *)b, (double *)c,
                                              policy, scratch, fault, gate, ev, engine, open, epi,
-                                             &done, pre, close);
+                                             &done, pre, close, closed);
     if (e != hipSuccess || !epi || epi->op == 0)
         return e;
     if (done) {

@@ -16,6 +16,27 @@ struct NodeGate {
 
 enum : int { kOpAdd = 0, kOpSub = 1, kOpMul = 2, kOpDiv = 3 };
 
+// The end of a program done by the launch of its last op (a MatMul that is the program's
+// only node, or a final SGD update) instead of a publication launch of its own: the n fault
+// words go to the coherent pinned
+// mirror host_words and are reset to `value`, the stage gate is opened, and then the
+// sequence number `seq` is stored to host_seq (the host waits on it). `ticket` (zero between
+// launches) counts the workgroups or waves that have finished when the last of them must do
+// it. words == nullptr: no.
+// A launch that ends the program takes one ticket per workgroup on a single counter; it
+// does so only with at most this many workgroups (else the tickets queue too long).
+constexpr unsigned kCloseMaxBlocks = 64;
+struct ProgramClose {
+    unsigned long long *words = nullptr;
+    uint64_t n = 0;
+    unsigned long long value = 0;
+    unsigned int *gate = nullptr;
+    unsigned long long *host_words = nullptr;
+    unsigned long long *host_seq = nullptr;
+    uint64_t seq = 0;
+    unsigned int *ticket = nullptr;
+};
+
 // Elementwise family. `b == nullptr` selects the uniform right operand `*b_value`
 // (host memory, dtype-sized). Each launcher enqueues on `s` and never synchronizes.
 hipError_t launch_binary(hipStream_t s, int dtype, int op, uint64_t n, const void *a,
@@ -30,7 +51,8 @@ hipError_t launch_add_relu(hipStream_t s, int dtype, uint64_t n, const void *a, 
                            const void *b_value, void *out, int policy,
                            unsigned long long *fault_add, unsigned long long *fault_relu, NodeGate gate);
 hipError_t launch_sgd(hipStream_t s, int dtype, uint64_t n, const void *w, const void *g,
-                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate);
+                      double rate, void *out, int policy, unsigned long long *fault, NodeGate gate,
+                      ProgramClose close = {}, bool *closed = nullptr);
 // Two strict SGD updates of one dtype and policy in one launch, each with its own fault word
 // and gate (both counts nonzero).
 struct SgdJob {
@@ -44,7 +66,10 @@ struct SgdJob {
 // Measurement aid: copy `bytes` (a multiple of 4 KiB, 16-byte-aligned pointers) reading
 // with global_load_lds_dwordx4 and writing with ordinary stores.
 hipError_t launch_direct_copy(hipStream_t s, const void *src, void *dst, uint64_t bytes);
-hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy);
+// `close` (when set, and the grid is small enough for one ticket per workgroup): the launch
+// also ends the program; *closed tells whether it does.
+hipError_t launch_sgd_pair(hipStream_t s, int dtype, const SgdJob &j0, const SgdJob &j1, int policy,
+                           ProgramClose close = {}, bool *closed = nullptr);
 
 // A chain of elementwise nodes (checked binary, ReLU, ReLU backward) evaluated in one pass:
 // each step takes the value of the step before it (the first takes `head`) and, for a binary
@@ -182,22 +207,6 @@ struct ProgramOpen {
     unsigned long long value = 0;
     unsigned int *gate = nullptr;
 };
-// The end of a program whose only node is this MatMul, done by the MatMul's last kernel
-// instead of a publication launch of its own: the n fault words go to the coherent pinned
-// mirror host_words and are reset to `value`, the stage gate is opened, and then the
-// sequence number `seq` is stored to host_seq (the host waits on it). `ticket` (zero between
-// launches) counts the workgroups or waves that have finished when the last of them must do
-// it. words == nullptr: no.
-struct ProgramClose {
-    unsigned long long *words = nullptr;
-    uint64_t n = 0;
-    unsigned long long value = 0;
-    unsigned int *gate = nullptr;
-    unsigned long long *host_words = nullptr;
-    unsigned long long *host_seq = nullptr;
-    uint64_t seq = 0;
-    unsigned int *ticket = nullptr;
-};
 // Operands whose exponent screen its producer already wrote, as superslab tables in the
 // screen's own layouts: op(A)'s rows (a: x-major [M][K/64] when A is untransposed,
 // superslab-major [K/64][M] when transposed) and op(B)'s columns (b: superslab-major
@@ -216,7 +225,7 @@ hipError_t launch_strict_matmul(hipStream_t s, int dtype, uint64_t rows, uint64_
                                 hipEvent_t *ev = nullptr, int engine = kEngineAuto,
                                 ProgramOpen open = {}, const GemmEpilogue *epi = nullptr,
                                 Prescreen pre = {}, bool *epi_fused = nullptr,
-                                ProgramClose close = {});
+                                ProgramClose close = {}, bool *closed = nullptr);
 
 // Native compound arithmetic (Boundary + BackendDefined): no fault word.
 hipError_t launch_native_gemm_f32(hipStream_t s, int M, int N, int K, bool ta, bool tb,

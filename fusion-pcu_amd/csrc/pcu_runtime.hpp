@@ -135,6 +135,30 @@ struct Ctx {
     pcu_status add_node(NodeInfo info, unsigned long long **word);
     // The program's stage gate sits after the fault words; a node's gate carries its number.
     unsigned int *gate_word() const { return reinterpret_cast<unsigned int *>(fault_words + kMaxNodes); }
+    // Beside the gate: the ticket counter of an in-kernel program end (ProgramClose), zeroed
+    // by every program opening and by the workgroup that ends a program.
+    unsigned int *ticket_word() const { return gate_word() + 1; }
+    // A ProgramClose for the program's end by the launch of its last op (nodes.size() words,
+    // under sequence number pub_seq + 1); the op commits it with closed_seq = ++pub_seq once
+    // launched.
+    ProgramClose program_close() const
+    {
+        ProgramClose c;
+        c.words = fault_words;
+        c.n = nodes.size();
+        c.value = ~0ull; // no fault
+        c.gate = gate_word();
+        c.host_words = host_words;
+        c.host_seq = host_seq;
+        c.seq = pub_seq + 1;
+        c.ticket = ticket_word();
+        return c;
+    }
+    // The program's next op is its last: an SGD update (or pair) then ends the program in
+    // its own kernel when its grid is small (see op_sgd).
+    bool close_next = false;
+    void close_with_next_op() { close_next = in_program; }
+    pcu_status take_close(ProgramClose *c);
     NodeGate gate_for(const unsigned long long *word) const
     {
         return NodeGate{gate_word(), (unsigned int)(word - fault_words)};

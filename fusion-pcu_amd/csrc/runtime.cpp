@@ -324,6 +324,7 @@ pcu_status Ctx::begin_program(bool implicit)
     in_program = true;
     implicit_program = implicit;
     closed_seq = 0;
+    close_next = false;
     nodes.clear();
     // The previous program's end left the words reset and the gate open, unless it failed.
     words_pending = !words_clean;
@@ -848,23 +849,16 @@ pcu_status Ctx::op_matmul(int dtype, uint64_t rows, uint64_t inner, uint64_t col
     // launch fewer. The no-allocation call keeps the publication launch (its scratch is the
     // device's shared array).
     ProgramClose close;
-    if (implicit_program && first_node && !noalloc && !epi && s.suspect) {
-        close.words = fault_words;
-        close.n = nodes.size();
-        close.value = kNoFaultWord;
-        close.gate = gate_word();
-        close.host_words = host_words;
-        close.host_seq = host_seq;
-        close.seq = pub_seq + 1;
-        close.ticket = (unsigned int *)(s.suspect + 2); // the scratch head's third word
-    }
+    if (implicit_program && first_node && !noalloc && !epi)
+        close = program_close();
+    bool closed = false;
     hipError_t e = launch_strict_matmul(stream, dtype, rows, inner, cols, tl != 0, tr != 0, a,
                                         b, c, policy, s, word, gate_for(word),
                                         timed ? ev : nullptr, matmul_engine, open, epi,
-                                        noalloc ? Prescreen{} : pre, epi_fused, close);
+                                        noalloc ? Prescreen{} : pre, epi_fused, close, &closed);
     if ((st = hip(e, "strict_matmul launch")))
         return st;
-    if (close.words)
+    if (closed)
         closed_seq = ++pub_seq;
     if (timed) {
         timings.push_back({PCU_KERNEL_GEMM_PREFILTER, ev[0], ev[1]});
@@ -1049,7 +1043,9 @@ pcu_status Ctx::op_sgd_pair(int dtype, const uint64_t n[2], const void *const w[
                             int policy)
 {
     if (n[0] == 0 || n[1] == 0) {
-        // An empty update launches nothing: the two go alone.
+        // An empty update launches nothing: the two go alone (and the program ends with its
+        // publication launch).
+        close_next = false;
         pcu_status st = op_sgd(dtype, n[0], w[0], g[0], rate[0], out[0], policy);
         return st ? st : op_sgd(dtype, n[1], w[1], g[1], rate[1], out[1], policy);
     }
@@ -1066,10 +1062,31 @@ pcu_status Ctx::op_sgd_pair(int dtype, const uint64_t n[2], const void *const w[
     SgdJob j[2];
     for (int u = 0; u < 2; u++)
         j[u] = SgdJob{w[u], g[u], out[u], n[u], (double)rate[u], word[u], gate_for(word[u])};
+    ProgramClose close;
+    if ((st = take_close(&close)))
+        return st;
+    bool closed = false;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_sgd_pair(stream, dtype, j[0], j[1], policy), "strict_sgd launch");
+    st = hip(launch_sgd_pair(stream, dtype, j[0], j[1], policy, close, &closed), "strict_sgd launch");
     timer_stop(PCU_KERNEL_SGD, t, stream);
+    if (!st && closed)
+        closed_seq = ++pub_seq;
     return st;
+}
+
+// The close for the program's last op (close_with_next_op): every word its end reads must
+// be final when that op's kernel runs, so work still on the side stream is joined first.
+pcu_status Ctx::take_close(ProgramClose *c)
+{
+    *c = ProgramClose{};
+    if (!close_next)
+        return PCU_OK;
+    close_next = false;
+    pcu_status st = join_side();
+    if (st)
+        return st;
+    *c = program_close();
+    return PCU_OK;
 }
 
 pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, float rate,
@@ -1083,9 +1100,19 @@ pcu_status Ctx::op_sgd(int dtype, uint64_t n, const void *w, const void *g, floa
         return st;
     if ((st = open_words()))
         return st;
+    if (implicit_program && nodes.size() == 1)
+        close_next = true; // a single pcu_strict_sgd call: its kernel ends the program
+    ProgramClose close;
+    if ((st = take_close(&close)))
+        return st;
+    bool closed = false;
     hipEvent_t t = timer_start(stream);
-    st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word, gate_for(word)), "strict_sgd launch");
+    st = hip(launch_sgd(stream, dtype, n, w, g, (double)rate, out, policy, word, gate_for(word),
+                        close, &closed),
+             "strict_sgd launch");
     timer_stop(PCU_KERNEL_SGD, t, stream);
+    if (!st && closed)
+        closed_seq = ++pub_seq;
     return st;
 }
 
