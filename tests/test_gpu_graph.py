@@ -450,6 +450,59 @@ def test_mse_then_chain_fault_order(G, pcu_pkg, dtype):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+def test_mse_then_final_sgd_fault_order(G, pcu_pkg, dtype):
+    """An MSE (serial and ordered-walk sizes) followed by a strict SGD update, the last
+    launch of the program: that update publishes the program's fault words when its grid is
+    small and leaves them to the host when it is large. With a fault planted in the MSE's
+    sum, in the update, in both or in neither, the outputs, or the first faulting node and
+    its coordinates, match the oracle's ordered graph, so a fault written by an earlier
+    launch is not lost by the launch that ends the program."""
+    big = dtype(3.0e38) if dtype == np.float32 else dtype(1.7e308)
+    half = dtype(1.5e19) if dtype == np.float32 else dtype(1.0e154)  # squares sum past the top
+    ctx = G.default_context()
+    rng = np.random.default_rng(47)
+    for n, nw in ((1000, 1000), (20000, 1000), (20000, 1 << 20)):
+        g = G.Graph()
+        g.set_numerical_mode(True)
+        p, t = g.input((n,), dtype), g.input((n,), dtype)
+        w, gr = g.input((nw,), dtype), g.input((nw,), dtype)
+        outs = [g.mean_squared_error(p, t), g.sgd_update(w, gr, 0.5)]
+        prep = g.prepare(ctx, outs)
+        ref = og.Graph()
+        ref.mode = "Strict"
+        rp, rt = ref.input((n,), dtype), ref.input((n,), dtype)
+        rw, rg = ref.input((nw,), dtype), ref.input((nw,), dtype)
+        routs = [ref.mean_squared_error(rp, rt), ref.sgd_update(rw, rg, 0.5)]
+        for plant in ("none", "mse", "sgd", "both"):
+            a = [rng.uniform(-1, 1, n).astype(dtype), rng.uniform(-1, 1, n).astype(dtype),
+                 rng.uniform(-1, 1, nw).astype(dtype), rng.uniform(-1, 1, nw).astype(dtype)]
+            if plant in ("mse", "both"):
+                a[0][n // 2:n // 2 + 4] = half  # the ordered sum of squares overflows in an Add
+            if plant in ("sgd", "both"):
+                a[2][nw - 1], a[3][nw - 1] = -big, big  # -big - 0.5 big overflows
+            vals, rf = ref.evaluate({rp: a[0], rt: a[1], rw: a[2], rg: a[3]}, routs)
+            assert (rf is None) == (plant == "none"), (plant, rf)
+            dev = {p: ctx.upload(a[0]), t: ctx.upload(a[1]), w: ctx.upload(a[2]), gr: ctx.upload(a[3])}
+            try:
+                if rf is None:
+                    prep.execute([dev[i].ptr for i in prep.input_ids])
+                    for k, want in enumerate(routs):
+                        d = prep.output_desc[k]
+                        have = pcu_pkg.DeviceArray(ctx, prep.output_ptr(k), d["shape"], d["dtype"]).numpy()
+                        np.testing.assert_array_equal(_bits(have), _bits(vals[want]))
+                else:
+                    with pytest.raises(pcu_pkg.PcuExecutionError) as exc:
+                        prep.execute([dev[i].ptr for i in prep.input_ids])
+                    tf = exc.value.tensor_fault
+                    assert (tf.node, tf.element_index, tf.reduction_index, int(tf.step), int(tf.kind)) == \
+                        (rf.node, rf.fault.element_index, rf.fault.reduction_index, rf.fault.step,
+                         rf.fault.kind), (n, nw, plant)
+            finally:
+                for x in dev.values():
+                    x.free()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
 def test_matmul_relu_epilogue_fault_order(G, pcu_pkg, dtype):
     """A strict MatMul followed by a ReLU of its product, and one followed by a ReLU
     backward taking its product as upstream, each a node of its own with its own fault word:
