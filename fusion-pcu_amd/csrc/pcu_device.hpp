@@ -512,17 +512,20 @@ __device__ __forceinline__ void program_close_wave(const ProgramClose &c)
 
 // Every workgroup of the launch calls it once, last thing, with all its threads: the last
 // workgroup to arrive ends the program. The words the end reads are written only by
-// device-scope atomics (fault records, the gate), which are complete once the barrier has
-// waited for the workgroup's memory operations, so no workgroup needs a device-scope
-// release (on this part one writes back and invalidates the XCD's L2: a fence in each of
-// the replay's 4096 waves cost a faulting 1024^3 call about 70 us); only the last one
-// acquires before it reads them.
+// device-scope atomics (fault records, the gate), performed where every XCD sees them. Each
+// wave waits until its own memory operations have completed (the barrier alone waits only
+// for LDS and scalar operations, so a fault record could still be in flight when the
+// workgroup takes its ticket), and then no workgroup needs a device-scope release (on this
+// part one writes back and invalidates the XCD's L2: a fence in each of the replay's 4096
+// waves cost a faulting 1024^3 call about 70 us); only the last one acquires before it
+// reads them.
 __device__ __forceinline__ void program_close_block(const ProgramClose &c)
 {
     if (c.words == nullptr)
         return;
     __shared__ int last;
-    __syncthreads(); // the workgroup's fault records are done
+    __builtin_amdgcn_s_waitcnt(0); // vmcnt(0) expcnt(0) lgkmcnt(0): the fault records are done
+    __syncthreads();
     if (threadIdx.x == 0)
         last = atomicAdd(c.ticket, 1u) + 1u == gridDim.x * gridDim.y * gridDim.z;
     __syncthreads();
