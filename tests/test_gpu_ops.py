@@ -996,6 +996,63 @@ def test_matmul_replay_paths_for_marked_cells(ctx, pcu_pkg, dtype, engine):
             assert _ofault(rf)[:2] == (17 * n + 33, 9)
 
 
+@pytest.mark.parametrize("tl,tr", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["nn", "tn", "nt", "tt"])
+def test_matmul_full_grid_replay_paths(ctx, pcu_pkg, tl, tr):
+    """The replay's passes under IEEE on F32 full grids of whole 128 x 128 tiles (the
+    large matrix-core tile kernels, with op(B) transposed read from its K x N copy), every
+    layout, two shapes (2048 x 192 x 2048 and 32768 x 192 x 128), each call after a clean
+    call of another shape, against the oracle: (a) every cell marked by the exponent
+    screen, no tiny product, no fault; (b) exact subnormal products in every cell of the
+    first 128 rows before a tiny-inexact product at (17, 33), k 9; (c) a NaN in row 40 and
+    a tiny product in row 50: Invalid; (d) the tiny product in row 10 before that NaN:
+    Underflow; (e) a tiny product at k 1 of the NaN row's first cell, before the NaN at
+    k 3; (f) a tiny product in the last row and the last superslab of k."""
+    rng = np.random.default_rng(77)
+    p2 = lambda e: np.float32(2.0 ** e)
+    other = (ctx.upload(rng.uniform(-1, 1, (2048, 64)).astype(np.float32)),
+             ctx.upload(rng.uniform(-1, 1, (64, 4096)).astype(np.float32)))
+    for m, k, n in ((2048, 192, 2048), (32768, 192, 128)):
+        def base():
+            return (rng.uniform(-1, 1, (m, k)).astype(np.float32),
+                    rng.uniform(-1, 1, (k, n)).astype(np.float32))
+        cases = []
+        a, b = base()
+        a[:, 5] = p2(-120) * np.where(rng.random(m) < 0.5, -1, 1).astype(np.float32)
+        b[5, :] = (rng.uniform(0.5, 1.0, n) * np.where(rng.random(n) < 0.5, -1, 1)).astype(np.float32)
+        cases.append(("clean-marked", a, b))
+        a, b = base()
+        a[:128, 5], b[5, :] = p2(-100), p2(-40)
+        a[17, 9], b[9, 33] = np.float32(1.5) * p2(-100), np.float32(1.3) * p2(-30)
+        cases.append(("exact-then-inexact", a, b))
+        for row, name in ((50, "nan-first"), (10, "tiny-first")):
+            a, b = base()
+            a[40, 3] = np.nan
+            a[row, 9], b[9, 33] = np.float32(1.5) * p2(-100), np.float32(1.3) * p2(-30)
+            cases.append((name, a, b))
+        a, b = base()
+        a[40, 3] = np.nan
+        a[40, 1], b[1, 0] = np.float32(1.5) * p2(-100), np.float32(1.3) * p2(-30)
+        cases.append(("tiny-in-the-nan-cell", a, b))
+        a, b = base()
+        a[m - 1, k - 2], b[k - 2, n - 3] = np.float32(1.5) * p2(-100), np.float32(1.3) * p2(-30)
+        cases.append(("last-superslab", a, b))
+        for name, a, b in cases:
+            aa = np.ascontiguousarray(a.T) if tl else a
+            bb = np.ascontiguousarray(b.T) if tr else b
+            ctx.strict_matmul(other[0], other[1], policy=0).free()
+            got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(aa), ctx.upload(bb), tl, tr, 0).numpy())
+            ref, rf = oracle.matmul(aa, bb, tl, tr, policy=0)
+            assert gf == _ofault(rf), (m, k, n, name, gf, rf)
+            if rf is None:
+                np.testing.assert_array_equal(_bits(got), _bits(ref), err_msg=f"{name} {m}x{k}x{n}")
+            expect = {"clean-marked": None, "exact-then-inexact": (17 * n + 33, 9),
+                      "nan-first": (40 * n, 3), "tiny-first": (10 * n + 33, 9),
+                      "tiny-in-the-nan-cell": (40 * n, 1),
+                      "last-superslab": ((m - 1) * n + n - 3, k - 2)}[name]
+            assert (None if rf is None else _ofault(rf)[:2]) == expect, (name, rf)
+
+
 @pytest.mark.parametrize("policy", [0, 1], ids=["ieee", "reject_subnormal"])
 def test_matmul_screen_after_calls_of_other_shapes(ctx, pcu_pkg, policy, engine):
     """Regression: MatMul calls of different shapes share one scratch buffer. A word that one
