@@ -959,12 +959,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm_tiny_scan(
     const T *__restrict__ A, const T *__restrict__ B, int M, int N, int K,
     const unsigned long long *__restrict__ row_exp, const unsigned long long *__restrict__ col_exp,
     int thr, const unsigned long long *suspect, unsigned long long *row_flag,
-    unsigned long long *flag_first, uint32_t gen, ScanTables tb, NodeGate gate)
+    unsigned long long *flag_first, uint32_t gen, ScanTables tb, NodeGate gate,
+    ProgramClose close)
 {
     // No cell marked: nothing to scan (the same word for every thread). Most launches end
-    // here, before the gate's block-wide read and its barrier.
-    if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault)
+    // here, before the gate's block-wide read and its barrier. Then the replay after this
+    // kernel finds no suspect cell either and writes no fault word, so a MatMul that ends
+    // its program ends it here: one wave publishes at once, and the host need not wait for
+    // the replay launch (which then returns without publishing).
+    if (__atomic_load_n(suspect, __ATOMIC_RELAXED) == kNoFault) {
+        if (close.words != nullptr && blockIdx.x == 0 && threadIdx.x < 64)
+            program_close_wave(close);
         return;
+    }
     if (block_gate_closed(gate))
         return;
     using Cfg = ScanCfg<T>;
@@ -1288,7 +1295,8 @@ __global__ __launch_bounds__(1024) void k_strict_gemm_replay(
     // so one wave may end the program at once.
     const uint64_t first = *suspect;
     if (first == kNoFault || K == 0) {
-        if (close.words != nullptr && blockIdx.x == 0 && threadIdx.x < 64)
+        // After a tiny scan (`tiny`), that scan ended the program on the same condition.
+        if (close.words != nullptr && !tiny && blockIdx.x == 0 && threadIdx.x < 64)
             program_close_wave(close);
         return;
     }
@@ -1740,18 +1748,19 @@ static void gemm_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, T *C
 
 template <typename T, bool TA, bool TB>
 static void tiny_scan_dispatch(hipStream_t s, dim3 grid, const T *A, const T *B, int M, int N,
-                               int K, const MatmulScratch &sc, int thr, ScanTables tb, NodeGate gate)
+                               int K, const MatmulScratch &sc, int thr, ScanTables tb, NodeGate gate,
+                               ProgramClose close)
 {
     const bool va = (TA ? (M % 4 == 0) : (K % 4 == 0)) && aligned16(A);
     const bool vb = (TB ? (K % 4 == 0) : (N % 4 == 0)) && aligned16(B);
     if (va && vb)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate, close);
     else if (va)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, true, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate, close);
     else if (vb)
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, true>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate, close);
     else
-        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate);
+        hipLaunchKernelGGL((k_gemm_tiny_scan<T, TA, TB, false, false>), grid, dim3(256), 0, s, A, B, M, N, K, sc.row_exp, sc.col_exp, thr, sc.suspect, sc.row_flag, sc.flag_first, sc.gen, tb, gate, close);
 }
 
 template <bool TA, bool TB>
@@ -1917,10 +1926,10 @@ static hipError_t strict_matmul_t(hipStream_t s, uint64_t M, uint64_t K, uint64_
     const bool tiny = risk && (policy == kPolicyIeee || sum_check);
     if (tiny) {
         const dim3 sgrid(grid.x < 2u * kGfx950Cus ? grid.x : 2u * kGfx950Cus);
-        if (!ta && !tb) tiny_scan_dispatch<T, false, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
-        else if (!ta && tb) tiny_scan_dispatch<T, false, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
-        else if (ta && !tb) tiny_scan_dispatch<T, true, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
-        else tiny_scan_dispatch<T, true, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate);
+        if (!ta && !tb) tiny_scan_dispatch<T, false, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate, close);
+        else if (!ta && tb) tiny_scan_dispatch<T, false, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate, close);
+        else if (ta && !tb) tiny_scan_dispatch<T, true, false>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate, close);
+        else tiny_scan_dispatch<T, true, true>(s, sgrid, A, B, m, n, k, sc, tiny_thr, tbls, gate, close);
     }
     const int serial_screen = risk && !tiny;
     // 4096 waves in 256 workgroups: an empty launch (no suspect cell) dispatches a quarter of
