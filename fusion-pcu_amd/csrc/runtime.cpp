@@ -456,7 +456,9 @@ pcu_status Ctx::read_words(size_t *used)
         // the next program (which then needs no opening launch), and stores this program's
         // sequence number last; the host spins on that word. Against a D2H copy and a stream
         // synchronization this saves the copy command and the runtime's wake-up. A program
-        // whose only node is a MatMul had its last kernel do the same (closed_seq).
+        // whose only node is a MatMul or a strict SGD update, or whose last launch is a
+        // strict SGD update on a small grid, had one of its own kernels do the same
+        // (closed_seq): a MatMul's tiny scan when no cell is suspect, else its replay.
         seq = ++pub_seq;
         if ((st = hip(launch_program_publish(stream, fault_words, *used, kNoFaultWord,
                                              gate_word(), host_words, host_seq, seq),
