@@ -226,6 +226,37 @@ def test_sgd_faults_parity(ctx, pcu_pkg, dtype):
                 np.testing.assert_array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("n", [1000, 65_536, 65_537, 300_000])
+def test_sgd_call_end_on_small_and_large_grids(ctx, pcu_pkg, dtype, n):
+    """A single strict SGD call ends its one-node program in its own kernel when its grid
+    has at most 64 workgroups (the last workgroup to take a ticket publishes the fault
+    word), and with a publication launch otherwise; the sizes reach both (1000 elements:
+    one workgroup; 65 536: 64 workgroups for binary32, the most that end in-kernel, and 128
+    for binary64; 65 537: 65 and 129; 300 000: several hundred). Clean, one fault in the
+    middle, and faults in the first and the last workgroups, called back to back, each
+    against the oracle."""
+    rng = np.random.default_rng(n + 5)
+    big = np.finfo(dtype).max
+    for plant in ("none", "middle", "ends", "none"):
+        w = rng.normal(0, 1, n).astype(dtype)
+        g = rng.normal(0, 1e-3, n).astype(dtype)
+        if plant == "middle":
+            w[n // 2] = np.nan
+        if plant == "ends":
+            w[n - 1], g[n - 1] = -big, big  # w - g overflows in the last workgroup
+            g[3] = np.inf                    # and an earlier Invalid in the first
+        dw, dg = ctx.upload(w), ctx.upload(g)
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_sgd(dw, dg, 1.0).numpy())
+        ref, rf = oracle.sgd(w, g, 1.0)
+        assert gf == _ofault(rf), (n, plant, gf, rf)
+        assert (rf is None) == (plant == "none"), (n, plant, rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+        dw.free()
+        dg.free()
+
+
 # ---------------------------------------------------------------------- MSE
 
 
