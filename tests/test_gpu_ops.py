@@ -1027,6 +1027,34 @@ def test_matmul_replay_paths_for_marked_cells(ctx, pcu_pkg, dtype, engine):
             assert _ofault(rf)[:2] == (17 * n + 33, 9)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=["f32", "f64"])
+@pytest.mark.parametrize("shape", [(128, 32, 128), (128, 32, 144), (512, 64, 512), (640, 64, 640)],
+                         ids=["fused64", "fused72", "mid", "large"])
+def test_matmul_call_end_paths(ctx, pcu_pkg, dtype, shape):
+    """A single strict MatMul call ends its one-node program in one of its own kernels: the
+    one-launch small-output kernel when its grid has at most 64 workgroups (128 x 128: 64),
+    else a publication launch (128 x 144: 72); on the screened path the tiny scan when no
+    cell is suspect and the replay otherwise (512 x 512 binary32; binary64 takes the
+    one-launch kernel up to 512 x 512, so 640 x 640 reaches its screened path). Clean, a NaN
+    operand, a tiny-inexact product and clean again, back to back, against the oracle."""
+    m, k, n = shape
+    rng = np.random.default_rng(m * 7 + n + k)
+    tiny_a, tiny_b = (-100, -30) if dtype == np.float32 else (-1000, -40)
+    for plant in ("none", "nan", "tiny", "none"):
+        a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+        b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+        if plant == "nan":
+            a[m - 3, 5] = np.nan
+        if plant == "tiny":
+            a[3, 7], b[7, n - 2] = dtype(1.5 * 2.0 ** tiny_a), dtype(1.3 * 2.0 ** tiny_b)
+        got, gf = _gpu_fault(pcu_pkg, lambda: ctx.strict_matmul(ctx.upload(a), ctx.upload(b), False, False, 0).numpy())
+        ref, rf = oracle.matmul(a, b, False, False, policy=0)
+        assert gf == _ofault(rf), (shape, plant, gf, rf)
+        assert (rf is None) == (plant == "none"), (shape, plant, rf)
+        if rf is None:
+            np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
 @pytest.mark.parametrize("tl,tr", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["nn", "tn", "nt", "tt"])
 def test_matmul_full_grid_replay_paths(ctx, pcu_pkg, tl, tr):
